@@ -1,0 +1,227 @@
+"""Benchmark of the SDPA forward on one MI355X (the driver's bench contract).
+
+Headline workload: C3 at S=8192 - B=1, H=8, S=8192, D=128,
+bf16, causal, seed 1234, default knobs.  A "step" is one forward over that batch with the
+inputs already resident in HBM.  Work per step is 4*B*H*S^2*D FLOPs halved for causal
+(137.4 GFLOP), so ``value`` is TFLOP/s.
+
+The JSON line also carries:
+
+* ``roofline``: the attention kernel's achieved TFLOP/s (algorithmic FLOPs per launch /
+  mean launch duration from HIP events recorded around every launch of the timed region on
+  the launch stream) against the dense bf16 MFMA peak, 2516.6 TFLOP/s
+  (256 CU x 4096 FLOP/clk x 2.4 GHz); ``traffic`` is the HBM bytes per launch measured with
+  rocprofv3 counters (profiles/), or null when not measured in this run;
+* ``cpu_baseline``: the reference's eager attention restated on the host CPU
+  (oracle/eager.py, run_study.py:304-335) on a bounded sample of the same workload;
+* ``sweep``: the C3 sequence sweep S in {512..8192}, kernel TFLOP/s and share of peak.
+
+Usage: ``python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]``.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+PEAK_TFLOPS = 2516.6  # dense fp16/bf16 MFMA, MI355X: 256 CU * 4096 FLOP/clk * 2.4 GHz
+REFERENCE_GB10_C3_S8192 = 60.87  # BASELINE.md 1.1 (benchmark_results.csv:548), TFLOP/s
+
+
+def _args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--seq", type=int, default=8192, help="sequence length of the headline workload")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--traffic-json", default=str(ROOT / "profiles" / "traffic.json"),
+                    help="HBM bytes per launch measured by rocprofv3 (optional)")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
+    return ap.parse_args()
+
+
+def _log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def time_kernel(fn, *, steps: int, warmup: int):
+    """Warm up, then time ``steps`` calls: wall clock around the region (synchronized on both
+    sides) and HIP events around every call on the launch stream."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for a, b in ev:
+        a.record(stream)
+        fn()
+        b.record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    per = [a.elapsed_time(b) for a, b in ev]
+    return wall_ms / steps, per
+
+
+def cpu_baseline(shape, dtype: str, seed: int, causal: bool, budget_s: float):
+    """Time the eager restatement on host cores over whole (b, h) slices of the workload."""
+    import torch
+
+    from oracle import eager
+    from oracle import oracle as O
+
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    q, k, v = O.make_inputs(shape, dtype, seed)
+    b_, h_, s, d = shape
+    pairs = [(b, h) for b in range(b_) for h in range(h_)]
+    eager.eager_attention_per_head(q, k, v, causal=causal, heads=pairs[:1])  # warmup
+    times = []
+    start = time.perf_counter()
+    i = 0
+    while True:
+        t0 = time.perf_counter()
+        eager.eager_attention_per_head(q, k, v, causal=causal, heads=[pairs[i % len(pairs)]])
+        times.append(time.perf_counter() - t0)
+        i += 1
+        if i >= 3 and time.perf_counter() - start > budget_s:
+            break
+        if i >= 200:
+            break
+    per_head = statistics.median(times)
+    flops_head = O.attention_forward_flops(b=1, h=1, s=s, d=d, causal=causal)
+    return {
+        "value": flops_head / per_head / 1e12,
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"eager attention (run_study.py:304-335 restated, torch CPU {dtype}) on "
+                   f"{len(times)} single-head slices of the workload, S={s} D={d}, median "
+                   f"{per_head * 1e3:.1f} ms/head; same FLOP count as the GPU line"),
+        "ms_per_head_median": per_head * 1e3,
+        "ms_per_head_p95": O.p95([t * 1e3 for t in times]),
+        "cpu_model": platform.processor() or platform.machine(),
+        "os_cpu_count": os.cpu_count(),
+    }
+
+
+def main() -> int:
+    args = _args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this build "
+              "(every GPU box here has one GPU).", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from oracle import oracle as O
+    from tiledattention_amd import sdpa
+    from tiledattention_amd.kernels import flash_fwd
+
+    dev = torch.device("cuda:0")
+    b, h, s, d = 1, 8, args.seq, 128
+    dtype, causal, seed = "bfloat16", True, 1234
+    _log(f"workload C3 B={b} H={h} S={s} D={d} {dtype} causal seed={seed}")
+    q, k, v = (t.to(dev) for t in O.make_inputs((b, h, s, d), dtype, seed))
+    flops = O.attention_forward_flops(b=b, h=h, s=s, d=d, causal=causal)
+    nbytes = O.approximate_bytes(b=b, h=h, s=s, d=d, bytes_per_elem=2)
+
+    def step():
+        return sdpa(q, k, v, causal=causal)
+
+    ms_step, per = time_kernel(step, steps=args.steps, warmup=args.warmup)
+    kern_ms = statistics.mean(per)
+    value = flops / (ms_step * 1e-3) / 1e12
+    achieved = flops / (kern_ms * 1e-3) / 1e12
+    _log(f"ms/step {ms_step:.4f}  kernel mean {kern_ms:.4f} ms (median {statistics.median(per):.4f})  "
+         f"{value:.1f} TFLOP/s  kernel {achieved:.1f} TFLOP/s ({achieved / PEAK_TFLOPS:.1%} of peak)")
+
+    traffic = None
+    tp = Path(args.traffic_json)
+    if tp.exists():
+        try:
+            rec = json.loads(tp.read_text()).get(f"c3_s{s}")
+            traffic = rec["hbm_bytes_per_launch"] if rec else None
+        except (ValueError, KeyError, TypeError):
+            traffic = None
+
+    sweep = {}
+    if not args.no_sweep:
+        for ss in (512, 1024, 2048, 4096, 8192):
+            qs, ks, vs = (t.to(dev) for t in O.make_inputs((1, 8, ss, 128), dtype, seed))
+            f = O.attention_forward_flops(b=1, h=8, s=ss, d=128, causal=True)
+            _, per_s = time_kernel(lambda: sdpa(qs, ks, vs, causal=True), steps=50, warmup=5)
+            med = statistics.median(per_s)
+            sweep[str(ss)] = {
+                "tflops": round(f / (med * 1e-3) / 1e12, 2),
+                "frac_peak": round(f / (med * 1e-3) / 1e12 / PEAK_TFLOPS, 4),
+                "median_ms": round(med, 5),
+                "p95_ms": round(O.p95(per_s), 5),
+                "hbm_gbps_alg": round(O.approximate_bytes(b=1, h=8, s=ss, d=128, bytes_per_elem=2)
+                                      / (med * 1e-3) / 1e9, 1),
+            }
+            _log(f"sweep S={ss}: {sweep[str(ss)]}")
+            del qs, ks, vs
+
+    tm, tn = flash_fwd._default_tile_config_for_shape_gfx950(seq_len=s, head_dim=d, causal=causal)
+    line = {
+        "metric": "SDPA fwd TFLOP/s vs seq len (fp16/bf16, D=64/128) + % of MI355X MFMA peak",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(value / REFERENCE_GB10_C3_S8192, 3) if s == 8192 else None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v, CPU generator)",
+        "config": {
+            "workload": f"C3: sdpa fwd B={b} H={h} S={s} D={d} bf16 causal, seed {seed}",
+            "B": b, "H": h, "S": s, "D": d, "causal": causal,
+            "tile_m": tm, "tile_n": tn, "accum": "fp32",
+            "flops_per_step": flops,
+            "reference_value_gb10": REFERENCE_GB10_C3_S8192 if s == 8192 else None,
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_TFLOPS, 4),
+            "traffic": traffic,
+            "kernel_mean_ms": round(kern_ms, 5),
+            "alg_bytes": nbytes,
+        },
+        "sweep": sweep,
+    }
+
+    if not args.no_cpu_baseline:
+        _log("cpu baseline (eager restatement on host cores)")
+        line["cpu_baseline"] = cpu_baseline((b, h, s, d), dtype, seed, causal, args.cpu_seconds)
+        _log(f"cpu baseline {line['cpu_baseline']['value']:.4f} TFLOP/s on {line['cpu_baseline']['cores']} threads")
+    else:
+        line["cpu_baseline"] = None
+
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,106 @@
+/*
+ * tiledattn.h — C ABI of the MI355X (gfx950) SDPA forward operator.
+ *
+ * This library is the drop-in boundary for the reference's launch path.  It replaces:
+ *   - the torch op declared in torch-ext/torch_binding.h:5 and registered in
+ *     torch-ext/torch_binding.cpp:6-19 (device guard + current stream + launch,
+ *     tiledattention_cuda/tiledattention.cu:29-32), and
+ *   - the kernel launch ct.launch(stream, grid, kernel, (q_bh, k_t, v_bh, out_bh, scale))
+ *     at src/tiledattention/kernels/flash_fwd.py:809 with its arguments built at :954-969,
+ *   - the in-memory kernel cache src/tiledattention/kernels/compile_cache.py:10-37
+ *     (here: a per-device cache of hipFunction_t loaded from precompiled gfx950 code objects).
+ *
+ * Conventions:
+ *   - Plain C types only; no torch or HIP types cross the boundary.  `stream` is a
+ *     hipStream_t passed as void* (NULL = the device's null stream).
+ *   - The library never allocates or frees device memory; the caller owns q, k, v and o.
+ *   - Calls are asynchronous with respect to the host (work is enqueued on `stream`).
+ *   - Every entry point returns a ta_status; on a non-OK status ta_last_error() returns a
+ *     message for the calling thread.  No C++ exception crosses the boundary.
+ *   - Thread-safe: the kernel cache is guarded by a mutex.
+ */
+#ifndef TILEDATTN_H_
+#define TILEDATTN_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TA_ABI_VERSION 1
+
+typedef enum ta_status {
+  TA_OK = 0,
+  TA_EINVAL = 1,        /* bad argument (null pointer, shape, stride, alignment, tile) */
+  TA_EUNSUPPORTED = 2,  /* valid request this build has no kernel for (head dim, device arch) */
+  TA_ENOKERNEL = 3,     /* code object or kernel symbol could not be loaded */
+  TA_EHIP = 4           /* HIP runtime error (launch failure, bad device or stream) */
+} ta_status;
+
+typedef enum ta_dtype { TA_FP16 = 0, TA_BF16 = 1 } ta_dtype;
+
+/* Accumulation of the P.V product across key tiles: fp32, or the input dtype
+ * (TILEDATTN_ACCUM_MODE=fp16 in the reference, flash_fwd.py:123-146). */
+typedef enum ta_accum { TA_ACC_FP32 = 0, TA_ACC_INPUT = 1 } ta_accum;
+
+/* Arguments of one SDPA forward.  Mirrors what flash_fwd.py:954-956 hands to the kernel:
+ * q, k, v, out as [B,H,S,D] views plus the resolved scale; the reference's [B*H,D,S] K
+ * transpose view is not needed because the kernel reads K row-major. */
+typedef struct ta_fwd_args {
+  const void* q; /* [B,H,S,D] device pointers, dtype elements */
+  const void* k;
+  const void* v;
+  void* o;
+  int64_t B, H, S, D; /* D must be 64 or 128 (callers zero-pad other head dims) */
+  int64_t q_stride[4]; /* element strides for (B,H,S,D); stride[3] must be 1 */
+  int64_t k_stride[4];
+  int64_t v_stride[4];
+  int64_t o_stride[4];
+  float scale;     /* softmax scale, already resolved (sdpa.py:46-47) */
+  int32_t causal;  /* 0/1 */
+  int32_t dtype;   /* ta_dtype */
+  int32_t tile_m;  /* query rows per workgroup: 64 or 128 (TILEDATTN_TILE_M) */
+  int32_t tile_n;  /* keys per tile: 64 or 128 (TILEDATTN_TILE_N) */
+  int32_t accum;   /* ta_accum */
+  int32_t device;  /* HIP device ordinal the pointers and stream belong to */
+  int32_t sched;   /* workgroup -> tile order: 0 plain, 1 XCD-grouped (see ta_sdpa_fwd) */
+  int32_t reserved;
+} ta_fwd_args;
+
+/* Version of this ABI (TA_ABI_VERSION). */
+int ta_abi_version(void);
+
+/* Directory holding the attn_fwd_m<TM>_n<TN>.hsaco code objects.  Must be called before
+ * the first launch; a later call also drops every cached module. */
+ta_status ta_set_code_object_dir(const char* dir);
+
+/* Load (or find in the cache) the kernel for one configuration on `device` without
+ * launching it: the counterpart of compile_cache.get_kernel's miss path
+ * (compile_cache.py:13-29).  `aligned` = 1 selects the variant without tail masking,
+ * valid only when S is a multiple of tile_m and tile_n. */
+ta_status ta_prepare(int32_t device, int32_t dtype, int32_t head_dim, int32_t tile_m,
+                     int32_t tile_n, int32_t causal, int32_t accum, int32_t aligned);
+
+/* Enqueue one SDPA forward on `stream`.  Picks the unmasked-tail kernel when S is a
+ * multiple of both tiles.  Zero-size problems (B*H == 0 or S == 0) return TA_OK with no
+ * launch. */
+ta_status ta_sdpa_fwd(const ta_fwd_args* args, void* stream);
+
+/* Unload every cached module on every device (compile_cache.reset_cache_for_tests). */
+ta_status ta_cache_reset(void);
+
+/* Number of kernels currently cached (all devices). */
+int32_t ta_cache_size(void);
+
+/* Message for the last non-OK status returned on the calling thread ("" if none). */
+const char* ta_last_error(void);
+
+/* Static name of a status code. */
+const char* ta_status_string(int32_t status);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TILEDATTN_H_ */

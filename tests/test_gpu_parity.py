@@ -1,0 +1,310 @@
+"""GPU parity of the gfx950 SDPA forward against the CPU oracle, at every BASELINE config.
+
+Every case names itself on stdout before touching the GPU.  Inputs come from the CPU
+generator (oracle.make_inputs), so they are bit-identical to what the oracle sees.  Sizes
+the oracle finishes in seconds are compared in full; the long sequences (S >= 4096) are
+compared on sampled query rows (first/last 64 rows plus random rows), which the oracle
+computes exactly and independently of the other rows.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from tests.parity_util import (
+    LOWP_TOL,
+    TOL,
+    as_f32,
+    check_close,
+    inputs,
+    oracle_f32,
+    run_gpu,
+    sample_rows,
+    say,
+)
+
+pytestmark = pytest.mark.gpu
+
+TILES = [(64, 64), (64, 128), (128, 64), (128, 128)]
+
+
+# ---------------------------------------------------------------- BASELINE configs
+
+def test_c1_example_workload_all_tiles(gpu):
+    """C1: B1 H2 S64 D64 fp16 causal, seed 0 (the reference's example.py:19-24 workload)."""
+    q, k, v = inputs((1, 2, 64, 64), "float16", 0)
+    ref = oracle_f32(q, k, v, causal=True)
+    for tm, tn in [(None, None)] + TILES:
+        say(f"C1 fp16 causal (1,2,64,64) seed=0 tiles={(tm, tn) if tm else 'default'}")
+        env = {} if tm is None else {"tile_m": tm, "tile_n": tn}
+        out = run_gpu(q, k, v, causal=True, **env)
+        assert out.shape == (1, 2, 64, 64) and out.dtype == q.dtype
+        check_close(as_f32(out), ref, "float16", what=f"C1 tiles={tm},{tn}")
+
+
+def test_reference_small_noncausal_vs_torch(gpu):
+    """Port of the reference's GPU test (tests/test_sdpa_correctness_small.py:20-44):
+    (1,2,64,64) fp16 non-causal, seed 0, against torch's SDPA at atol=rtol=2.5e-2; the
+    torch result is computed in float32 from the same inputs."""
+    import torch
+
+    say("reference small test (1,2,64,64) fp16 non-causal seed=0 vs torch SDPA")
+    q, k, v = inputs((1, 2, 64, 64), "float16", 0)
+    out = run_gpu(q, k, v, causal=False)
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        q.float().cuda(), k.float().cuda(), v.float().cuda(), attn_mask=None, dropout_p=0.0, is_causal=False
+    ).to(torch.float16)
+    torch.cuda.synchronize()
+    assert out.shape == ref.shape
+    assert out.dtype == ref.dtype
+    assert torch.allclose(out, ref, atol=2.5e-2, rtol=2.5e-2)
+    check_close(as_f32(out), oracle_f32(q, k, v, causal=False), "float16", what="reference small")
+
+
+def test_c2_fp16_noncausal_s1024_d64(gpu):
+    """C2: B1 H8 S1024 D64 fp16 non-causal, tile 64x64, fp32 accumulation, seed 2026."""
+    q, k, v = inputs((1, 8, 1024, 64), "float16", 2026)
+    ref = oracle_f32(q, k, v, causal=False)
+    say("C2 fp16 non-causal (1,8,1024,64) seed=2026 tile 64x64 accum fp32")
+    out = run_gpu(q, k, v, causal=False, tile_m=64, tile_n=64, accum_mode="fp32")
+    check_close(as_f32(out), ref, "float16", what="C2")
+    say("C2 with default knobs (auto accumulation picks the input dtype here)")
+    out = run_gpu(q, k, v, causal=False)
+    check_close(as_f32(out), ref, "float16", tol=LOWP_TOL["float16"], what="C2 default")
+
+
+@pytest.mark.parametrize("s", [512, 1024, 2048, 4096, 8192])
+def test_c3_bf16_causal_d128(gpu, s):
+    """C3: B1 H8 D128 bf16 causal, seed 1234, S swept; S >= 4096 on sampled rows."""
+    q, k, v = inputs((1, 8, s, 128), "bfloat16", 1234)
+    rows = None if s <= 2048 else sample_rows(s, 192)
+    ref = oracle_f32(q, k, v, causal=True, rows=rows)
+    say(f"C3 bf16 causal (1,8,{s},128) seed=1234 default tiles rows={'all' if rows is None else len(rows)}")
+    out = run_gpu(q, k, v, causal=True)
+    check_close(as_f32(out, rows), ref, "bfloat16", what=f"C3 S={s}")
+    if s <= 2048:
+        for tm, tn in TILES:
+            say(f"C3 bf16 causal S={s} tiles=({tm},{tn})")
+            out = run_gpu(q, k, v, causal=True, tile_m=tm, tile_n=tn)
+            check_close(as_f32(out), ref, "bfloat16", what=f"C3 S={s} tiles={tm},{tn}")
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("d", [64, 128])
+def test_c4_noncausal_tile_sweep(gpu, dtype, d):
+    """C4: B4 H16 S4096 non-causal, inputs N(0,1)*0.5, seed 2026, TILE_M/TILE_N in {64,128}."""
+    q, k, v = inputs((4, 16, 4096, d), dtype, 2026, scale_inputs=0.5)
+    rows = sample_rows(4096, 64)
+    ref = oracle_f32(q, k, v, causal=False, rows=rows)
+    for tm, tn in TILES:
+        say(f"C4 {dtype} non-causal (4,16,4096,{d}) seed=2026 tiles=({tm},{tn}) accum fp32")
+        out = run_gpu(q, k, v, causal=False, tile_m=tm, tile_n=tn, accum_mode="fp32")
+        check_close(as_f32(out, rows), ref, dtype, what=f"C4 {dtype} D={d} tiles={tm},{tn}")
+
+
+@pytest.mark.parametrize("outliers", [False, True])
+def test_c5_long_sequence_causal(gpu, outliers):
+    """C5: B1 H8 S16384 D128 fp16 causal, seed 1234; C5b: 1% of k entries x20 (seed 1235)."""
+    kw = dict(outlier_frac=0.01, outlier_gain=20.0, outlier_seed=1235) if outliers else {}
+    q, k, v = inputs((1, 8, 16384, 128), "float16", 1234, **kw)
+    rows = sample_rows(16384, 128)
+    ref = oracle_f32(q, k, v, causal=True, rows=rows)
+    say(f"C5{'b' if outliers else ''} fp16 causal (1,8,16384,128) seed=1234 rows={len(rows)}")
+    out = run_gpu(q, k, v, causal=True)
+    check_close(as_f32(out, rows), ref, "float16", what=f"C5{'b' if outliers else ''}")
+
+
+# ---------------------------------------------------------------- ragged / edge shapes
+
+@pytest.mark.parametrize("s", [1, 17, 100, 1000])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype,d", [("float16", 64), ("bfloat16", 128)])
+def test_tails_all_tiles(gpu, s, causal, dtype, d):
+    """S not a multiple of the tile: masked tails (flash_fwd.py:400-403, 415-423)."""
+    q, k, v = inputs((2, 3, s, d), dtype, 100 + s)
+    ref = oracle_f32(q, k, v, causal=causal)
+    for tm, tn in TILES:
+        say(f"tail {dtype} (2,3,{s},{d}) causal={causal} tiles=({tm},{tn})")
+        out = run_gpu(q, k, v, causal=causal, tile_m=tm, tile_n=tn, accum_mode="fp32")
+        check_close(as_f32(out), ref, dtype, what=f"tail S={s} tiles={tm},{tn}")
+
+
+@pytest.mark.parametrize("d", [8, 32, 48, 80, 96, 100])
+def test_head_dim_padding(gpu, d):
+    """D outside {64,128}: zero-padded to the next kernel head dim, output sliced back."""
+    q, k, v = inputs((1, 2, 200, d), "float16", 7 + d)
+    for causal in (False, True):
+        say(f"pad fp16 (1,2,200,{d}) causal={causal}")
+        out = run_gpu(q, k, v, causal=causal)
+        assert out.shape == (1, 2, 200, d)
+        check_close(as_f32(out), oracle_f32(q, k, v, causal=causal), "float16", what=f"pad D={d}")
+
+
+def test_chunked_head_dim_knob_matches_unchunked(gpu):
+    """TILEDATTN_CHUNKED_HEAD_DIMS=96 computes the same attention as the unchunked path."""
+    q, k, v = inputs((1, 2, 256, 96), "bfloat16", 96)
+    say("chunked knob bf16 (1,2,256,96)")
+    a = run_gpu(q, k, v, causal=True, chunked_head_dims="96")
+    b = run_gpu(q, k, v, causal=True)
+    check_close(as_f32(a), oracle_f32(q, k, v, causal=True), "bfloat16", what="chunked 96")
+    assert bool((a == b).all())
+
+
+def test_custom_scale(gpu):
+    q, k, v = inputs((1, 4, 300, 64), "float16", 11)
+    for scale in (0.05, 1.0, 0.3):
+        say(f"scale={scale} fp16 (1,4,300,64)")
+        out = run_gpu(q, k, v, causal=True, scale=scale)
+        check_close(as_f32(out), oracle_f32(q, k, v, causal=True, scale=scale), "float16", what=f"scale {scale}")
+
+
+# ---------------------------------------------------------------- accumulation in the input dtype
+
+@pytest.mark.parametrize("dtype,d,causal", [("float16", 64, False), ("bfloat16", 128, True),
+                                            ("float16", 128, True), ("bfloat16", 64, False)])
+def test_input_dtype_accumulation(gpu, dtype, d, causal):
+    """ACCUM_MODE=fp16: O kept in the input dtype between key tiles (flash_fwd.py:301-372)."""
+    from oracle import oracle as O
+
+    q, k, v = inputs((1, 4, 1000, d), dtype, 31)
+    ref = oracle_f32(q, k, v, causal=causal)
+    dc = O.dtype_code(dtype)
+    for tm, tn in TILES:
+        say(f"accum=input {dtype} (1,4,1000,{d}) causal={causal} tiles=({tm},{tn})")
+        out = run_gpu(q, k, v, causal=causal, tile_m=tm, tile_n=tn, accum_mode="fp16")
+        got = as_f32(out)
+        check_close(got, ref, dtype, tol=LOWP_TOL[dtype], what=f"accum=input vs fp32 oracle tiles={tm},{tn}")
+        emu = O.upcast(O.flash_tiled(O.to_bits(q), O.to_bits(k), O.to_bits(v), dc, causal=causal,
+                                     tile_m=tm, tile_n=tn, accum_lowp=True), dc)
+        check_close(got, emu, dtype, tol=TOL[dtype], what=f"accum=input vs tiled emulation tiles={tm},{tn}")
+
+
+# ---------------------------------------------------------------- layout and launch plumbing
+
+def test_strided_inputs_match_contiguous(gpu):
+    """[B,S,H,D]-stored tensors viewed as [B,H,S,D] run without a copy and match."""
+    import torch
+
+    q, k, v = inputs((2, 4, 333, 128), "float16", 5)
+    say("strided views fp16 (2,4,333,128)")
+    qs, ks, vs = (t.transpose(1, 2).contiguous().transpose(1, 2) for t in (q, k, v))
+    assert not qs.is_contiguous()
+    a = run_gpu(qs, ks, vs, causal=True)
+    b = run_gpu(q, k, v, causal=True)
+    torch.cuda.synchronize()
+    assert bool((a == b).all())
+    check_close(as_f32(a), oracle_f32(q, k, v, causal=True), "float16", what="strided")
+
+
+def test_non_default_stream_and_sync_modes(gpu):
+    import torch
+
+    from tiledattention_amd import sdpa
+    from tests.parity_util import knobs
+
+    q, k, v = (t.cuda() for t in inputs((1, 2, 512, 64), "bfloat16", 9))
+    ref = oracle_f32(q.cpu(), k.cpu(), v.cpu(), causal=False)
+    s = torch.cuda.Stream()
+    for mode in ("async", "post", "strict"):
+        say(f"stream + sync_mode={mode}")
+        with torch.cuda.stream(s), knobs(sync_mode=mode):
+            out = sdpa(q, k, v)
+        s.synchronize()
+        check_close(as_f32(out), ref, "bfloat16", what=f"sync {mode}")
+
+
+def test_zero_size_inputs(gpu):
+    import torch
+
+    from tiledattention_amd import sdpa
+
+    say("zero-size inputs")
+    for shape in [(0, 2, 16, 64), (1, 0, 16, 64), (1, 2, 0, 64)]:
+        q = torch.zeros(shape, dtype=torch.float16, device="cuda")
+        out = sdpa(q, q, q, causal=True)
+        assert out.shape == shape
+
+
+def test_invalid_knobs_raise_before_launch(gpu):
+    import torch
+
+    from tiledattention_amd import sdpa
+    from tests.parity_util import knobs
+
+    q = torch.zeros((1, 1, 64, 64), dtype=torch.float16, device="cuda")
+    say("invalid knobs")
+    for env, msg in [({"tile_m": 32}, "Unsupported tile"), ({"tile_n": "x"}, "must be an integer"),
+                     ({"accum_mode": "fp8"}, "ACCUM_MODE"), ({"sync_mode": "later"}, "SYNC_MODE"),
+                     ({"tile_m": -64}, "must be positive")]:
+        with knobs(**env), pytest.raises(ValueError, match=msg):
+            sdpa(q, q, q)
+    with pytest.raises(Exception, match="head dimension D=160"):
+        sdpa(*(torch.zeros((1, 1, 8, 160), dtype=torch.float16, device="cuda"),) * 3)
+
+
+# ---------------------------------------------------------------- known-answer tests on the GPU
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_kat_causal_row0_is_v0_exactly(gpu, dtype):
+    q, k, v = inputs((2, 4, 700, 128), dtype, 3)
+    say(f"KAT row0 {dtype}")
+    out = run_gpu(q, k, v, causal=True)
+    assert bool((out[:, :, 0, :].cpu() == v[:, :, 0, :]).all())
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_kat_constant_values(gpu, dtype):
+    import torch
+
+    q, k, _ = inputs((1, 3, 257, 64), dtype, 4)
+    v = torch.full(q.shape, 0.75, dtype=q.dtype)
+    for causal in (False, True):
+        say(f"KAT constant v {dtype} causal={causal}")
+        out = run_gpu(q, k, v, causal=causal)
+        # P is rounded to the input dtype before P.V while l sums the unrounded P (as in
+        # the reference), so the result is 0.75 up to that rounding, not bit-exact.
+        check_close(as_f32(out), v.float().numpy(), dtype, what="constant v")
+
+
+def test_kat_zero_keys_give_prefix_mean(gpu):
+    import torch
+
+    q, _, v = inputs((1, 2, 300, 64), "float16", 6)
+    k = torch.zeros_like(q)
+    vf = v.float()
+    say("KAT k=0 prefix mean")
+    out = run_gpu(q, k, v, causal=True)
+    ref = (vf.cumsum(2) / torch.arange(1, 301).view(1, 1, -1, 1)).numpy()
+    check_close(as_f32(out), ref, "float16", what="prefix mean")
+    out = run_gpu(q, k, v, causal=False)
+    check_close(as_f32(out), vf.mean(2, keepdim=True).expand_as(vf).numpy(), "float16", what="mean")
+
+
+def test_kat_noncausal_key_permutation_invariance(gpu):
+    import torch
+
+    q, k, v = inputs((1, 2, 512, 128), "bfloat16", 8)
+    perm = torch.randperm(512, generator=torch.Generator().manual_seed(1))
+    say("KAT key permutation")
+    a = as_f32(run_gpu(q, k, v, causal=False))
+    b = as_f32(run_gpu(q, k[:, :, perm], v[:, :, perm], causal=False))
+    check_close(a, b, "bfloat16", what="permuted keys")
+
+
+def test_kat_heads_are_independent(gpu):
+    q, k, v = inputs((2, 3, 200, 64), "float16", 12)
+    say("KAT head independence")
+    full = as_f32(run_gpu(q, k, v, causal=True))
+    one = as_f32(run_gpu(q[1:2, 2:3], k[1:2, 2:3], v[1:2, 2:3], causal=True))
+    assert np.array_equal(full[1:2, 2:3], one)
+
+
+def test_golden_fixture_c1(gpu):
+    """Committed golden vectors (tests/golden/c1.npz) through the GPU path."""
+    from tests.golden.fixtures import load_fixture
+
+    fx = load_fixture("c1")
+    say("golden c1")
+    out = run_gpu(fx["q"], fx["k"], fx["v"], causal=bool(fx["causal"]))
+    check_close(as_f32(out), fx["out_f32"], str(fx["dtype"]), what="golden c1")

@@ -1,0 +1,165 @@
+"""ctypes binding of the C ABI in ``include/tiledattn.h`` (``lib/libtiledattn.so``).
+
+The library and the gfx950 code objects it loads are built in-tree by
+``tiledattention_amd/csrc/build.py`` into ``tiledattention_amd/lib/``.  ``TILEDATTN_LIB_DIR``
+overrides where both are looked up.  Nothing here falls back to another implementation:
+if the library is missing, ``load()`` raises ``DependencyError``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+from threading import Lock
+
+from ._errors import DependencyError
+
+ABI_VERSION = 1
+
+TA_OK = 0
+TA_EINVAL = 1
+TA_EUNSUPPORTED = 2
+TA_ENOKERNEL = 3
+TA_EHIP = 4
+
+TA_FP16 = 0
+TA_BF16 = 1
+TA_ACC_FP32 = 0
+TA_ACC_INPUT = 1
+
+TILE_SHAPES = ((64, 64), (64, 128), (128, 64), (128, 128))
+
+# Every symbol the header declares; tests check the built library exports all of them.
+EXPORTED_SYMBOLS = (
+    "ta_abi_version",
+    "ta_set_code_object_dir",
+    "ta_prepare",
+    "ta_sdpa_fwd",
+    "ta_cache_reset",
+    "ta_cache_size",
+    "ta_last_error",
+    "ta_status_string",
+)
+
+
+class FwdArgs(ctypes.Structure):
+    """Mirror of ``ta_fwd_args``."""
+
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("o", ctypes.c_void_p),
+        ("B", ctypes.c_int64),
+        ("H", ctypes.c_int64),
+        ("S", ctypes.c_int64),
+        ("D", ctypes.c_int64),
+        ("q_stride", ctypes.c_int64 * 4),
+        ("k_stride", ctypes.c_int64 * 4),
+        ("v_stride", ctypes.c_int64 * 4),
+        ("o_stride", ctypes.c_int64 * 4),
+        ("scale", ctypes.c_float),
+        ("causal", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("tile_m", ctypes.c_int32),
+        ("tile_n", ctypes.c_int32),
+        ("accum", ctypes.c_int32),
+        ("device", ctypes.c_int32),
+        ("sched", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+_lock = Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def lib_dir() -> Path:
+    env = os.getenv("TILEDATTN_LIB_DIR", "").strip()
+    if env:
+        return Path(env)
+    return Path(__file__).resolve().parent / "lib"
+
+
+def library_path() -> Path:
+    return lib_dir() / "libtiledattn.so"
+
+
+def code_object_paths() -> list[Path]:
+    d = lib_dir()
+    return [d / f"attn_fwd_m{tm}_n{tn}.hsaco" for tm, tn in TILE_SHAPES]
+
+
+def _declare(lib: ctypes.CDLL) -> None:
+    i32 = ctypes.c_int32
+    lib.ta_abi_version.argtypes = []
+    lib.ta_abi_version.restype = ctypes.c_int
+    lib.ta_set_code_object_dir.argtypes = [ctypes.c_char_p]
+    lib.ta_set_code_object_dir.restype = i32
+    lib.ta_prepare.argtypes = [i32, i32, i32, i32, i32, i32, i32, i32]
+    lib.ta_prepare.restype = i32
+    lib.ta_sdpa_fwd.argtypes = [ctypes.POINTER(FwdArgs), ctypes.c_void_p]
+    lib.ta_sdpa_fwd.restype = i32
+    lib.ta_cache_reset.argtypes = []
+    lib.ta_cache_reset.restype = i32
+    lib.ta_cache_size.argtypes = []
+    lib.ta_cache_size.restype = i32
+    lib.ta_last_error.argtypes = []
+    lib.ta_last_error.restype = ctypes.c_char_p
+    lib.ta_status_string.argtypes = [i32]
+    lib.ta_status_string.restype = ctypes.c_char_p
+
+
+def load() -> ctypes.CDLL:
+    """Load the C-ABI library once per process; raise ``DependencyError`` if absent."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        path = library_path()
+        if not path.exists():
+            raise DependencyError(
+                f"Native library {path} is missing. Build it with "
+                "`python -m tiledattention_amd.csrc.build` (needs hipcc for gfx950)."
+            )
+        missing = [str(p) for p in code_object_paths() if not p.exists()]
+        if missing:
+            raise DependencyError(
+                "gfx950 code objects are missing: " + ", ".join(missing)
+                + ". Build them with `python -m tiledattention_amd.csrc.build`."
+            )
+        try:
+            lib = ctypes.CDLL(str(path))
+        except OSError as exc:
+            raise DependencyError(f"Native library {path} could not be loaded: {exc}") from exc
+        _declare(lib)
+        ver = int(lib.ta_abi_version())
+        if ver != ABI_VERSION:
+            raise DependencyError(f"libtiledattn ABI {ver} does not match the binding's {ABI_VERSION}.")
+        st = lib.ta_set_code_object_dir(str(lib_dir()).encode())
+        if st != TA_OK:
+            raise DependencyError(f"ta_set_code_object_dir failed: {last_error(lib)}")
+        _lib = lib
+        return lib
+
+
+def loaded() -> ctypes.CDLL | None:
+    """The library if ``load()`` already succeeded in this process, else None."""
+    return _lib
+
+
+def last_error(lib: ctypes.CDLL) -> str:
+    raw = lib.ta_last_error()
+    return raw.decode(errors="replace") if raw else ""
+
+
+def status_name(lib: ctypes.CDLL, status: int) -> str:
+    raw = lib.ta_status_string(int(status))
+    return raw.decode() if raw else str(status)
+
+
+def _reset_for_tests() -> None:
+    global _lib
+    with _lock:
+        _lib = None

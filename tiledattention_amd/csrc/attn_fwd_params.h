@@ -1,0 +1,25 @@
+// Kernel argument block shared by the HIP kernels and the host launcher.
+// Plain C layout: it is passed by value as the kernels' only argument.
+#pragma once
+#include <stdint.h>
+
+namespace ta {
+
+struct FwdParams {
+  const uint16_t* q;  // [B,H,S,D] fp16/bf16 bit patterns, last-dim stride 1
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* o;
+  int64_t q_sb, q_sh, q_ss;  // element strides of batch, head, sequence
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t o_sb, o_sh, o_ss;
+  int32_t H;
+  int32_t S;
+  int32_t n_qblk;      // ceil(S / TILE_M)
+  int32_t n_bh;        // B * H
+  float scale_log2;    // softmax scale * log2(e)
+  int32_t sched;       // block -> tile order: 0 plain, 1 XCD-grouped
+};
+
+}  // namespace ta

@@ -1,0 +1,105 @@
+"""Build recipe for the native parts: gfx950 code objects and the C-ABI library.
+
+Outputs (into ``tiledattention_amd/lib/`` unless told otherwise):
+
+* ``attn_fwd_m<TM>_n<TN>.hsaco`` for TM, TN in {64, 128}: each holds the 32 kernels of
+  one tile shape (dtype x head dim x causal x tail x accumulation), compiled from
+  ``attn_fwd.hip`` with ``hipcc --genco --offload-arch=gfx950``;
+* ``libtiledattn.so``: the host library implementing ``include/tiledattn.h``.
+
+Run as ``python -m tiledattention_amd.csrc.build``.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+PKG = HERE.parent
+REPO = PKG.parent
+LIB_DIR = PKG / "lib"
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+ARCH = "gfx950"
+TILES = ((64, 64), (64, 128), (128, 64), (128, 128))
+
+# Packed-fp32 VALU forms are kept out of every HIP build (see the kernel notes).
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+]
+
+
+def _hipcc() -> str:
+    path = shutil.which("hipcc") or str(ROCM / "bin" / "hipcc")
+    if not Path(path).exists():
+        raise RuntimeError("hipcc not found; a ROCm toolchain is required to build")
+    return path
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd)}\n{proc.stdout}")
+
+
+def code_object_cmd(tm: int, tn: int, out_dir: Path) -> list[str]:
+    out = out_dir / f"attn_fwd_m{tm}_n{tn}.hsaco"
+    return [
+        _hipcc(),
+        *HIP_FLAGS,
+        "--genco",
+        f"-DTA_TILE_M={tm}",
+        f"-DTA_TILE_N={tn}",
+        "-o",
+        str(out),
+        str(HERE / "attn_fwd.hip"),
+    ]
+
+
+def library_cmd(out_dir: Path) -> list[str]:
+    return [
+        os.environ.get("CXX", "g++"),
+        "-O2",
+        "-std=c++17",
+        "-fPIC",
+        "-shared",
+        "-Wall",
+        "-D__HIP_PLATFORM_AMD__",
+        f"-I{ROCM / 'include'}",
+        f"-I{REPO / 'include'}",
+        "-o",
+        str(out_dir / "libtiledattn.so"),
+        str(HERE / "tiledattn.cpp"),
+        f"-L{ROCM / 'lib'}",
+        f"-Wl,-rpath,{ROCM / 'lib'}",
+        "-lamdhip64",
+        "-ldl",
+    ]
+
+
+def build(out_dir: Path | None = None, jobs: int | None = None) -> Path:
+    """Compile every code object and the host library; return the output directory."""
+    out = Path(out_dir) if out_dir is not None else LIB_DIR
+    out.mkdir(parents=True, exist_ok=True)
+    cmds = [code_object_cmd(tm, tn, out) for tm, tn in TILES] + [library_cmd(out)]
+    workers = jobs or min(len(cmds), max(1, (os.cpu_count() or 2)))
+    with cf.ThreadPoolExecutor(max_workers=workers) as pool:
+        for fut in [pool.submit(_run, c) for c in cmds]:
+            fut.result()
+    return out
+
+
+if __name__ == "__main__":
+    d = build()
+    print(f"built into {d}")
+    sys.exit(0)

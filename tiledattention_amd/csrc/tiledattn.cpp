@@ -1,0 +1,274 @@
+// Host side of the C ABI declared in include/tiledattn.h.
+//
+// Replaces the reference's launch boundary (src/tiledattention/kernels/flash_fwd.py:786-818,
+// torch-ext/torch_binding.cpp:6-19, tiledattention_cuda/tiledattention.cu:13-33) and its
+// kernel cache (src/tiledattention/kernels/compile_cache.py:10-37):
+//   * kernels are precompiled per (TILE_M, TILE_N) into gfx950 code objects
+//     attn_fwd_m<TM>_n<TN>.hsaco; one module per (device, TM, TN) is loaded on first use and
+//     kept, and resolved hipFunction_t handles are cached per (device, kernel name);
+//   * the cache is guarded by a mutex (the reference's dict is unguarded);
+//   * launches go to the caller's stream under a device guard, like the reference's torch op
+//     (OptionalCUDAGuard + current stream, tiledattention.cu:29-31).
+#include <dlfcn.h>
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <tuple>
+
+#include "../../include/tiledattn.h"
+#include "attn_fwd_params.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+ta_status fail(ta_status st, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return st;
+}
+
+std::mutex g_mu;
+std::string g_dir;   // code object directory; empty = next to this library
+std::map<std::tuple<int, int, int>, hipModule_t> g_modules;   // (device, tm, tn)
+std::map<std::pair<int, std::string>, hipFunction_t> g_funcs;  // (device, kernel name)
+std::map<int, bool> g_arch_ok;                                 // device -> gfx950?
+
+std::string default_dir() {
+  Dl_info info;
+  if (dladdr(reinterpret_cast<void*>(&default_dir), &info) && info.dli_fname) {
+    std::string p(info.dli_fname);
+    size_t cut = p.find_last_of('/');
+    if (cut != std::string::npos) return p.substr(0, cut);
+  }
+  return ".";
+}
+
+// Restores the caller's current device on scope exit (the reference's torch op does the
+// same with OptionalCUDAGuard, tiledattention.cu:29).
+struct DeviceGuard {
+  int prev = -1;
+  bool changed = false;
+  hipError_t err = hipSuccess;
+  explicit DeviceGuard(int dev) {
+    err = hipGetDevice(&prev);
+    if (err == hipSuccess && prev != dev) {
+      err = hipSetDevice(dev);
+      changed = (err == hipSuccess);
+    }
+  }
+  ~DeviceGuard() {
+    if (changed) (void)hipSetDevice(prev);
+  }
+};
+
+std::string kernel_name(int dtype, int d, int tm, int tn, int causal, int tail, int accum) {
+  char buf[96];
+  snprintf(buf, sizeof(buf), "ta_fwd_%s_d%d_m%d_n%d_c%d_t%d_a%d", dtype == TA_BF16 ? "bf16" : "f16",
+           d, tm, tn, causal ? 1 : 0, tail ? 1 : 0, accum ? 1 : 0);
+  return buf;
+}
+
+bool valid_tile(int t) { return t == 64 || t == 128; }
+
+// Caller holds g_mu and has made `device` current.
+ta_status check_arch_locked(int device) {
+  auto it = g_arch_ok.find(device);
+  if (it != g_arch_ok.end()) {
+    if (!it->second) return fail(TA_EUNSUPPORTED, "device %d is not gfx950", device);
+    return TA_OK;
+  }
+  hipDeviceProp_t prop;
+  hipError_t e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess)
+    return fail(TA_EHIP, "hipGetDeviceProperties(%d): %s", device, hipGetErrorString(e));
+  bool ok = strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+  g_arch_ok[device] = ok;
+  if (!ok)
+    return fail(TA_EUNSUPPORTED, "device %d is %s; kernels are built for gfx950", device,
+                prop.gcnArchName);
+  return TA_OK;
+}
+
+// Caller holds g_mu and has made `device` current.
+ta_status get_function_locked(int device, int dtype, int d, int tm, int tn, int causal, int tail,
+                              int accum, hipFunction_t* out) {
+  std::string name = kernel_name(dtype, d, tm, tn, causal, tail, accum);
+  auto fk = std::make_pair(device, name);
+  auto fit = g_funcs.find(fk);
+  if (fit != g_funcs.end()) {
+    *out = fit->second;
+    return TA_OK;
+  }
+  ta_status st = check_arch_locked(device);
+  if (st != TA_OK) return st;
+  auto mk = std::make_tuple(device, tm, tn);
+  hipModule_t mod = nullptr;
+  auto mit = g_modules.find(mk);
+  if (mit == g_modules.end()) {
+    std::string dir = g_dir.empty() ? default_dir() : g_dir;
+    char path[1024];
+    snprintf(path, sizeof(path), "%s/attn_fwd_m%d_n%d.hsaco", dir.c_str(), tm, tn);
+    hipError_t e = hipModuleLoad(&mod, path);
+    if (e != hipSuccess)
+      return fail(TA_ENOKERNEL, "hipModuleLoad(%s): %s", path, hipGetErrorString(e));
+    g_modules[mk] = mod;
+  } else {
+    mod = mit->second;
+  }
+  hipFunction_t fn = nullptr;
+  hipError_t e = hipModuleGetFunction(&fn, mod, name.c_str());
+  if (e != hipSuccess)
+    return fail(TA_ENOKERNEL, "hipModuleGetFunction(%s): %s", name.c_str(), hipGetErrorString(e));
+  g_funcs[fk] = fn;
+  *out = fn;
+  return TA_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+int ta_abi_version(void) { return TA_ABI_VERSION; }
+
+const char* ta_last_error(void) { return g_last_error.c_str(); }
+
+const char* ta_status_string(int32_t status) {
+  switch (status) {
+    case TA_OK: return "TA_OK";
+    case TA_EINVAL: return "TA_EINVAL";
+    case TA_EUNSUPPORTED: return "TA_EUNSUPPORTED";
+    case TA_ENOKERNEL: return "TA_ENOKERNEL";
+    case TA_EHIP: return "TA_EHIP";
+    default: return "TA_UNKNOWN";
+  }
+}
+
+ta_status ta_cache_reset(void) {
+  std::lock_guard<std::mutex> lock(g_mu);
+  ta_status st = TA_OK;
+  for (auto& kv : g_modules) {
+    DeviceGuard guard(std::get<0>(kv.first));
+    hipError_t e = hipModuleUnload(kv.second);
+    if (e != hipSuccess && st == TA_OK)
+      st = fail(TA_EHIP, "hipModuleUnload: %s", hipGetErrorString(e));
+  }
+  g_modules.clear();
+  g_funcs.clear();
+  return st;
+}
+
+int32_t ta_cache_size(void) {
+  std::lock_guard<std::mutex> lock(g_mu);
+  return static_cast<int32_t>(g_funcs.size());
+}
+
+ta_status ta_set_code_object_dir(const char* dir) {
+  if (dir == nullptr) return fail(TA_EINVAL, "code object dir is NULL");
+  ta_status st = ta_cache_reset();
+  std::lock_guard<std::mutex> lock(g_mu);
+  g_dir = dir;
+  return st;
+}
+
+ta_status ta_prepare(int32_t device, int32_t dtype, int32_t head_dim, int32_t tile_m,
+                     int32_t tile_n, int32_t causal, int32_t accum, int32_t aligned) {
+  if (dtype != TA_FP16 && dtype != TA_BF16) return fail(TA_EINVAL, "dtype %d", dtype);
+  if (head_dim != 64 && head_dim != 128)
+    return fail(TA_EUNSUPPORTED, "head_dim %d (kernels exist for 64 and 128)", head_dim);
+  if (!valid_tile(tile_m) || !valid_tile(tile_n))
+    return fail(TA_EUNSUPPORTED, "tile (%d, %d) (supported: 64 or 128 each)", tile_m, tile_n);
+  if (accum != TA_ACC_FP32 && accum != TA_ACC_INPUT) return fail(TA_EINVAL, "accum %d", accum);
+  std::lock_guard<std::mutex> lock(g_mu);
+  DeviceGuard guard(device);
+  if (guard.err != hipSuccess)
+    return fail(TA_EHIP, "set device %d: %s", device, hipGetErrorString(guard.err));
+  hipFunction_t fn;
+  return get_function_locked(device, dtype, head_dim, tile_m, tile_n, causal != 0, aligned == 0,
+                             accum, &fn);
+}
+
+ta_status ta_sdpa_fwd(const ta_fwd_args* a, void* stream) {
+  if (a == nullptr) return fail(TA_EINVAL, "args is NULL");
+  if (a->dtype != TA_FP16 && a->dtype != TA_BF16) return fail(TA_EINVAL, "dtype %d", a->dtype);
+  if (a->accum != TA_ACC_FP32 && a->accum != TA_ACC_INPUT)
+    return fail(TA_EINVAL, "accum %d", a->accum);
+  if (a->causal != 0 && a->causal != 1) return fail(TA_EINVAL, "causal %d", a->causal);
+  if (a->sched != 0 && a->sched != 1) return fail(TA_EINVAL, "sched %d", a->sched);
+  if (a->B < 0 || a->H < 0 || a->S < 0) return fail(TA_EINVAL, "negative shape");
+  if (a->D != 64 && a->D != 128)
+    return fail(TA_EUNSUPPORTED, "head_dim %lld (kernels exist for 64 and 128)", (long long)a->D);
+  if (!valid_tile(a->tile_m) || !valid_tile(a->tile_n))
+    return fail(TA_EUNSUPPORTED, "tile (%d, %d) (supported: 64 or 128 each)", a->tile_m,
+                a->tile_n);
+  if (a->B == 0 || a->H == 0 || a->S == 0) return TA_OK;
+  if (!a->q || !a->k || !a->v || !a->o) return fail(TA_EINVAL, "null tensor pointer");
+  if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->o))
+    return fail(TA_EINVAL, "q/k/v/o must be 16-byte aligned");
+  const int64_t* st[4] = {a->q_stride, a->k_stride, a->v_stride, a->o_stride};
+  const char* nm[4] = {"q", "k", "v", "o"};
+  for (int i = 0; i < 4; ++i) {
+    if (st[i][3] != 1) return fail(TA_EINVAL, "%s: last-dim stride must be 1", nm[i]);
+    for (int j = 0; j < 3; ++j)
+      if (st[i][j] < 0 || (st[i][j] & 7) != 0)
+        return fail(TA_EINVAL, "%s: stride[%d]=%lld must be a non-negative multiple of 8", nm[i], j,
+                    (long long)st[i][j]);
+  }
+  if (a->S > 0x7fffffffLL || a->H > 0x7fffffffLL) return fail(TA_EINVAL, "S or H too large");
+  const int64_t n_bh = a->B * a->H;
+  const int64_t n_qblk = (a->S + a->tile_m - 1) / a->tile_m;
+  if (n_bh > 0x7fffffffLL || n_bh * n_qblk > 0x7fffffffLL)
+    return fail(TA_EINVAL, "grid too large (B*H*ceil(S/TM) must fit in int32)");
+
+  const bool aligned = (a->S % a->tile_m == 0) && (a->S % a->tile_n == 0);
+  hipFunction_t fn = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_mu);
+    DeviceGuard guard(a->device);
+    if (guard.err != hipSuccess)
+      return fail(TA_EHIP, "set device %d: %s", a->device, hipGetErrorString(guard.err));
+    ta_status s = get_function_locked(a->device, a->dtype, (int)a->D, a->tile_m, a->tile_n,
+                                      a->causal, !aligned, a->accum, &fn);
+    if (s != TA_OK) return s;
+  }
+
+  ta::FwdParams p;
+  p.q = static_cast<const uint16_t*>(a->q);
+  p.k = static_cast<const uint16_t*>(a->k);
+  p.v = static_cast<const uint16_t*>(a->v);
+  p.o = static_cast<uint16_t*>(a->o);
+  p.q_sb = a->q_stride[0]; p.q_sh = a->q_stride[1]; p.q_ss = a->q_stride[2];
+  p.k_sb = a->k_stride[0]; p.k_sh = a->k_stride[1]; p.k_ss = a->k_stride[2];
+  p.v_sb = a->v_stride[0]; p.v_sh = a->v_stride[1]; p.v_ss = a->v_stride[2];
+  p.o_sb = a->o_stride[0]; p.o_sh = a->o_stride[1]; p.o_ss = a->o_stride[2];
+  p.H = static_cast<int32_t>(a->H);
+  p.S = static_cast<int32_t>(a->S);
+  p.n_qblk = static_cast<int32_t>(n_qblk);
+  p.n_bh = static_cast<int32_t>(n_bh);
+  p.scale_log2 = static_cast<float>(static_cast<double>(a->scale) * 1.4426950408889634);
+  p.sched = a->sched;
+
+  DeviceGuard guard(a->device);
+  if (guard.err != hipSuccess)
+    return fail(TA_EHIP, "set device %d: %s", a->device, hipGetErrorString(guard.err));
+  void* params[] = {&p};
+  const unsigned grid = static_cast<unsigned>(n_bh * n_qblk);
+  const unsigned block = static_cast<unsigned>(a->tile_m * 2);  // tile_m / 32 waves of 64
+  hipError_t e = hipModuleLaunchKernel(fn, grid, 1, 1, block, 1, 1, 0,
+                                       static_cast<hipStream_t>(stream), params, nullptr);
+  if (e != hipSuccess) return fail(TA_EHIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
+  return TA_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,400 @@
+"""Host side of the SDPA forward: knob policy, argument preparation, launch.
+
+Keeps the reference's function names and policies (src/tiledattention/kernels/
+flash_fwd.py:12-259, 786-973) so that callers and tests written against it read the same,
+and replaces its cuTile launch with one call into the C ABI (``ta_sdpa_fwd``) on torch's
+current HIP stream of the inputs' device.
+
+Environment knobs are re-read on every call, as in the reference:
+
+``TILEDATTN_TILE_M`` / ``TILEDATTN_TILE_N``
+    Query rows per workgroup / keys per tile.  If either is set, the other defaults to 64
+    (flash_fwd.py:68-84, 851-856); non-integers and non-positive values raise
+    ``ValueError`` as there.  The gfx950 kernels exist for 64 and 128 only; any other
+    positive value raises ``ValueError`` naming the supported set.  When neither is set
+    the tile is chosen by ``_default_tile_config_for_shape_gfx950``.
+``TILEDATTN_ACCUM_MODE``
+    ``auto`` | ``fp32`` | ``fp16``; "fp16" accumulates in the input dtype (bf16 for bf16
+    inputs).  Policy restated from flash_fwd.py:102-146.
+``TILEDATTN_SYNC_MODE``
+    ``async`` (default) | ``post`` | ``strict`` (flash_fwd.py:805-818).  Validated before
+    the launch here (the reference validates after launching).
+``TILEDATTN_DISABLE_ALIGNED_FASTPATH``
+    As flash_fwd.py:225-226.
+``TILEDATTN_KERNEL_OPT_LEVEL`` / ``_OCCUPANCY`` / ``_NUM_CTAS``
+    Parsed as in flash_fwd.py:87-99 (``ValueError`` on non-integers) and kept in the cache
+    key; the code objects are precompiled at -O3, so they do not change the kernel.
+``TILEDATTN_CHUNKED_HEAD_DIMS``
+    Parsed as in flash_fwd.py:166-196.  A chunked plan computes the same attention as the
+    unchunked one, so here it runs the zero-padded kernel (96 -> 128); 160 is rejected.
+``TILEDATTN_SCHED`` (this build only)
+    Workgroup-to-tile order: ``0`` plain, ``1`` XCD-grouped; default picks 1 when the grid
+    splits evenly over the 8 XCDs.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Any
+
+from .. import _lib, _runtime
+from .._errors import DTypeNotSupportedError, InvalidShapeError, TiledAttentionError
+from .compile_cache import get_kernel
+
+_DEFAULT_TM = 64
+_DEFAULT_TN = 64
+_NEG_LARGE = -1.0e30
+_DIRECT_HEAD_DIMS = frozenset({64, 128})
+_ALIGNED_FASTPATH_HEAD_DIMS = frozenset({64, 128})
+_ALIGNED_FASTPATH_MIN_SEQ_BY_HEAD_DIM = {
+    64: 1024,
+    128: 2048,
+}
+_CHUNKED_HEAD_DIM_PARTS = {
+    96: (64, 32),
+    160: (128, 32),
+}
+_SUPPORTED_TILES = frozenset({64, 128})
+_KERNEL_HEAD_DIMS = (64, 128)
+_SYNC_MODES = ("strict", "post", "async")
+
+
+def _dtype_code_for_torch_dtype(torch_dtype: Any) -> int:
+    """fp16 -> TA_FP16, bf16 -> TA_BF16, else ``DTypeNotSupportedError`` (cf. flash_fwd.py:27-44)."""
+    torch_mod = _runtime.get_torch_module()
+    if torch_dtype == torch_mod.float16:
+        return _lib.TA_FP16
+    if torch_dtype == torch_mod.bfloat16:
+        return _lib.TA_BF16
+    raise DTypeNotSupportedError("q dtype must be torch.float16 or torch.bfloat16.")
+
+
+def _get_env_int(name: str, default: int | None) -> int | None:
+    """Integer env knob; unset or blank -> ``default`` (flash_fwd.py:47-65)."""
+    raw = os.getenv(name)
+    if raw is None or raw.strip() == "":
+        return default
+    try:
+        return int(raw)
+    except ValueError as exc:
+        raise ValueError(f"Environment variable {name} must be an integer.") from exc
+
+
+def _resolve_tile_config() -> tuple[int, int]:
+    """(TILE_M, TILE_N) from the environment; unset one defaults to 64 (flash_fwd.py:68-84)."""
+    tile_m = _get_env_int("TILEDATTN_TILE_M", None)
+    tile_n = _get_env_int("TILEDATTN_TILE_N", None)
+    if tile_m is None:
+        tile_m = _DEFAULT_TM
+    if tile_n is None:
+        tile_n = _DEFAULT_TN
+    if tile_m <= 0 or tile_n <= 0:
+        raise ValueError("TILEDATTN_TILE_M and TILEDATTN_TILE_N must be positive.")
+    return tile_m, tile_n
+
+
+def _check_tile_supported(tile_m: int, tile_n: int) -> None:
+    if tile_m not in _SUPPORTED_TILES or tile_n not in _SUPPORTED_TILES:
+        raise ValueError(
+            f"Unsupported tile ({tile_m}, {tile_n}): the gfx950 kernels are built for "
+            "TILEDATTN_TILE_M and TILEDATTN_TILE_N in {64, 128}."
+        )
+
+
+def _resolve_kernel_options() -> tuple[int, int | None, int | None]:
+    """(opt_level, occupancy, num_ctas) as flash_fwd.py:87-99 parses them."""
+    opt_level = _get_env_int("TILEDATTN_KERNEL_OPT_LEVEL", 3)
+    occupancy = _get_env_int("TILEDATTN_KERNEL_OCCUPANCY", None)
+    num_ctas = _get_env_int("TILEDATTN_KERNEL_NUM_CTAS", None)
+    assert opt_level is not None
+    return opt_level, occupancy, num_ctas
+
+
+def _default_accum_mode_for_shape(*, seq_len: int, head_dim: int, causal: bool) -> str:
+    """Auto accumulation policy of flash_fwd.py:102-120: input dtype iff non-causal, D == 64, S >= 1024."""
+    if (not causal) and head_dim == 64 and seq_len >= 1024:
+        return "fp16"
+    return "fp32"
+
+
+def _resolve_accum_mode(*, seq_len: int, head_dim: int, causal: bool) -> str:
+    """``TILEDATTN_ACCUM_MODE`` (auto|fp32|fp16, case-insensitive) -> 'fp32' | 'fp16' (flash_fwd.py:123-146)."""
+    raw_mode = os.getenv("TILEDATTN_ACCUM_MODE")
+    if raw_mode is None or raw_mode.strip() == "":
+        return _default_accum_mode_for_shape(seq_len=seq_len, head_dim=head_dim, causal=causal)
+    mode = raw_mode.strip().lower()
+    if mode == "auto":
+        return _default_accum_mode_for_shape(seq_len=seq_len, head_dim=head_dim, causal=causal)
+    if mode not in {"fp32", "fp16"}:
+        raise ValueError(
+            f"Unsupported TILEDATTN_ACCUM_MODE={mode!r}. Use one of: auto, fp32, fp16."
+        )
+    return mode
+
+
+def _resolve_kernel_head_dim(head_dim: int) -> tuple[int, int]:
+    """The reference's padding rule (flash_fwd.py:149-163): D in {64,128} as is, else next power of two."""
+    if head_dim in _DIRECT_HEAD_DIMS:
+        return head_dim, 0
+    kernel_head_dim = 1 << (head_dim - 1).bit_length()
+    return kernel_head_dim, kernel_head_dim - head_dim
+
+
+def _resolve_kernel_head_dim_gfx950(head_dim: int) -> tuple[int, int]:
+    """Head dim of the gfx950 kernel that runs ``head_dim``, and the zero padding to add.
+
+    Kernels exist for D = 64 and 128.  Smaller head dims are zero-padded to the next of
+    them, which leaves Q K^T unchanged and only adds zero output columns that are sliced
+    off (the reference pads the same way, to a power of two, flash_fwd.py:149-163).
+    """
+    if head_dim <= 0:
+        raise InvalidShapeError("head dimension D must be positive.")
+    for kd in _KERNEL_HEAD_DIMS:
+        if head_dim <= kd:
+            return kd, kd - head_dim
+    raise InvalidShapeError(
+        f"head dimension D={head_dim} is not supported: the gfx950 kernels cover D <= 128."
+    )
+
+
+def _resolve_chunk_plan(head_dim: int) -> tuple[tuple[int, int], ...] | None:
+    """``TILEDATTN_CHUNKED_HEAD_DIMS`` plan for ``head_dim`` (flash_fwd.py:166-196)."""
+    enabled = os.getenv("TILEDATTN_CHUNKED_HEAD_DIMS", "").strip()
+    if enabled == "":
+        return None
+    try:
+        enabled_dims = {int(x.strip()) for x in enabled.split(",") if x.strip() != ""}
+    except ValueError as exc:
+        raise ValueError(
+            "Environment variable TILEDATTN_CHUNKED_HEAD_DIMS must be a comma-separated list of integers."
+        ) from exc
+    if head_dim not in enabled_dims:
+        return None
+    parts = _CHUNKED_HEAD_DIM_PARTS.get(head_dim)
+    if parts is None:
+        return None
+    offset = 0
+    plan: list[tuple[int, int]] = []
+    for width in parts:
+        plan.append((offset, width))
+        offset += width
+    return tuple(plan)
+
+
+def _should_use_aligned_noncausal_fastpath(
+    *,
+    seq_len: int,
+    head_dim: int,
+    causal: bool,
+    pad_dim: int,
+    chunk_plan: tuple[tuple[int, int], ...] | None,
+    tile_m: int,
+    tile_n: int,
+) -> bool:
+    """The reference's unmasked-variant predicate (flash_fwd.py:199-238)."""
+    if os.getenv("TILEDATTN_DISABLE_ALIGNED_FASTPATH", "").strip() not in {"", "0", "false", "False"}:
+        return False
+    if causal:
+        return False
+    if chunk_plan is not None:
+        return False
+    if pad_dim != 0:
+        return False
+    if head_dim not in _ALIGNED_FASTPATH_HEAD_DIMS:
+        return False
+    min_seq = _ALIGNED_FASTPATH_MIN_SEQ_BY_HEAD_DIM.get(head_dim, 2048)
+    if seq_len < min_seq:
+        return False
+    return (seq_len % tile_m == 0) and (seq_len % tile_n == 0)
+
+
+def _default_tile_config_for_shape(*, seq_len: int, head_dim: int, causal: bool) -> tuple[int, int]:
+    """The reference's GB10-tuned default (flash_fwd.py:241-259), kept for API compatibility."""
+    tile_m = _DEFAULT_TM
+    tile_n = _DEFAULT_TN
+    if (not causal) and head_dim == 128 and seq_len >= 2048:
+        tile_n = 128
+    return tile_m, tile_n
+
+
+def _default_tile_config_for_shape_gfx950(*, seq_len: int, head_dim: int, causal: bool) -> tuple[int, int]:
+    """Default (TILE_M, TILE_N) on gfx950 when neither env knob is set.
+
+    128 query rows (4 waves) per workgroup and 64-key tiles: two workgroups fit on a CU
+    (64 KiB of LDS each at D = 128) and the K/V staging fits in registers.
+    """
+    del seq_len, head_dim, causal
+    return 128, 64
+
+
+def _resolve_sync_mode() -> str:
+    """``TILEDATTN_SYNC_MODE`` -> 'async' | 'post' | 'strict' (flash_fwd.py:805-818), checked up front."""
+    sync_mode = os.getenv("TILEDATTN_SYNC_MODE", "async").strip().lower()
+    if sync_mode not in _SYNC_MODES:
+        raise ValueError(
+            f"Unsupported TILEDATTN_SYNC_MODE={sync_mode!r}. Use one of: strict, post, async."
+        )
+    return sync_mode
+
+
+def _resolve_sched(*, n_blocks: int) -> int:
+    raw = os.getenv("TILEDATTN_SCHED", "").strip()
+    if raw == "":
+        return 1 if n_blocks % 8 == 0 else 0
+    if raw not in {"0", "1"}:
+        raise ValueError(f"Unsupported TILEDATTN_SCHED={raw!r}. Use 0 or 1.")
+    return int(raw)
+
+
+class _Launcher:
+    """A kernel resolved in the native cache for one device; calling it enqueues a launch."""
+
+    __slots__ = ("lib", "device", "config")
+
+    def __init__(self, lib, device: int, config: tuple[int, ...]):
+        self.lib = lib
+        self.device = device
+        self.config = config
+        dtype, head_dim, tile_m, tile_n, causal, accum, aligned = config
+        st = lib.ta_prepare(device, dtype, head_dim, tile_m, tile_n, causal, accum, aligned)
+        _raise_for_status(lib, st)
+
+    def __call__(self, args: _lib.FwdArgs, stream: int) -> None:
+        st = self.lib.ta_sdpa_fwd(ctypes.byref(args), ctypes.c_void_p(stream))
+        _raise_for_status(self.lib, st)
+
+
+def _raise_for_status(lib, status: int) -> None:
+    if status == _lib.TA_OK:
+        return
+    msg = f"{_lib.status_name(lib, status)}: {_lib.last_error(lib)}"
+    if status == _lib.TA_EINVAL:
+        raise InvalidShapeError(msg)
+    if status == _lib.TA_EUNSUPPORTED:
+        raise InvalidShapeError(msg)
+    if status == _lib.TA_ENOKERNEL:
+        from .._errors import DependencyError
+
+        raise DependencyError(msg)
+    raise TiledAttentionError(msg)
+
+
+def _kernel_ready(torch_mod, t, kernel_head_dim: int, pad_dim: int):
+    """Tensor in a layout the kernel reads directly: [B,H,S,kernel_D], unit last stride, 16-byte rows."""
+    if pad_dim > 0:
+        return torch_mod.nn.functional.pad(t, (0, pad_dim)).contiguous()
+    st = t.stride()
+    ok = (
+        st[3] == 1
+        and all(s % 8 == 0 for s in st[:3])
+        and t.data_ptr() % 16 == 0
+        and t.shape[3] == kernel_head_dim
+    )
+    return t if ok else t.contiguous()
+
+
+def run_flash_fwd(
+    q,
+    k,
+    v,
+    *,
+    causal: bool,
+    scale: float,
+):
+    """Run the gfx950 SDPA forward on validated [B,H,S,D] fp16/bf16 tensors; returns o.
+
+    Follows flash_fwd.py:821-973: resolve knobs, pad the head dim if needed, allocate the
+    output, pick the kernel through the cache, launch, apply the sync mode, and return
+    ``[B,H,S,D]`` (a view sliced back to D when padded).  K is read row-major in place; no
+    transposed view or per-call copy is made unless the inputs' strides require one.
+    """
+    torch_mod = _runtime.get_torch_module()
+    lib = _runtime.get_native_library()
+    opt_level, occupancy, num_ctas = _resolve_kernel_options()
+    sync_mode = _resolve_sync_mode()
+
+    batch, heads, seq_len, head_dim = map(int, q.shape)
+    accum_mode = _resolve_accum_mode(seq_len=seq_len, head_dim=head_dim, causal=causal)
+    bh = batch * heads
+    if os.getenv("TILEDATTN_TILE_M") or os.getenv("TILEDATTN_TILE_N"):
+        tile_m, tile_n = _resolve_tile_config()
+        _check_tile_supported(tile_m, tile_n)
+    else:
+        tile_m, tile_n = _default_tile_config_for_shape_gfx950(
+            seq_len=seq_len, head_dim=head_dim, causal=causal
+        )
+
+    chunk_plan = _resolve_chunk_plan(head_dim)
+    kernel_head_dim, pad_dim = _resolve_kernel_head_dim_gfx950(head_dim)
+    dtype_code = _dtype_code_for_torch_dtype(q.dtype)
+
+    device = q.device
+    out_shape = (batch, heads, seq_len, kernel_head_dim)
+    if bh == 0 or seq_len == 0:
+        out = torch_mod.empty(out_shape, dtype=q.dtype, device=device)
+        return out[..., :head_dim] if pad_dim > 0 else out
+
+    qk = _kernel_ready(torch_mod, q, kernel_head_dim, pad_dim)
+    kk = _kernel_ready(torch_mod, k, kernel_head_dim, pad_dim)
+    vk = _kernel_ready(torch_mod, v, kernel_head_dim, pad_dim)
+    out = torch_mod.empty(out_shape, dtype=q.dtype, device=device)
+
+    use_aligned_fastpath = _should_use_aligned_noncausal_fastpath(
+        seq_len=seq_len,
+        head_dim=head_dim,
+        causal=causal,
+        pad_dim=pad_dim,
+        chunk_plan=chunk_plan,
+        tile_m=tile_m,
+        tile_n=tile_n,
+    )
+    if chunk_plan is not None:
+        kernel_variant = "chunked"
+    elif use_aligned_fastpath:
+        kernel_variant = "direct_aligned_noncausal"
+    else:
+        kernel_variant = "direct"
+    aligned = int(seq_len % tile_m == 0 and seq_len % tile_n == 0)
+    accum_code = _lib.TA_ACC_INPUT if accum_mode == "fp16" else _lib.TA_ACC_FP32
+    device_index = device.index if device.index is not None else torch_mod.cuda.current_device()
+
+    kernel_key = (
+        tile_m,
+        tile_n,
+        kernel_head_dim,
+        kernel_variant,
+        str(q.dtype),
+        causal,
+        accum_mode,
+        opt_level,
+        occupancy if occupancy is not None else -1,
+        num_ctas if num_ctas is not None else -1,
+        aligned,
+        device_index,
+    )
+    config = (dtype_code, kernel_head_dim, tile_m, tile_n, int(causal), accum_code, aligned)
+    kernel = get_kernel(kernel_key, lambda: _Launcher(lib, device_index, config))
+
+    n_qblk = (seq_len + tile_m - 1) // tile_m
+    args = _lib.FwdArgs()
+    args.q, args.k, args.v, args.o = qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), out.data_ptr()
+    args.B, args.H, args.S, args.D = batch, heads, seq_len, kernel_head_dim
+    for name, t in (("q_stride", qk), ("k_stride", kk), ("v_stride", vk), ("o_stride", out)):
+        getattr(args, name)[:] = tuple(t.stride())
+    args.scale = float(scale)
+    args.causal = int(causal)
+    args.dtype = dtype_code
+    args.tile_m, args.tile_n = tile_m, tile_n
+    args.accum = accum_code
+    args.device = device_index
+    args.sched = _resolve_sched(n_blocks=bh * n_qblk)
+
+    stream = torch_mod.cuda.current_stream(device)
+    if sync_mode == "strict":
+        torch_mod.cuda.synchronize(device)
+    kernel(args, stream.cuda_stream)
+    if sync_mode in {"strict", "post"}:
+        stream.synchronize()
+
+    return out[..., :head_dim] if pad_dim > 0 else out
