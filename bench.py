@@ -49,6 +49,9 @@ def _args():
     ap.add_argument("--traffic-json", default=str(ROOT / "profiles" / "traffic.json"),
                     help="HBM bytes per launch measured by rocprofv3 (optional)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="also run a plain device copy of this many MiB (calibrates rocprofv3 "
+                         "FETCH_SIZE / WRITE_SIZE against a known byte count)")
     return ap.parse_args()
 
 
@@ -144,6 +147,12 @@ def main() -> int:
     def step():
         return sdpa(q, k, v, causal=causal)
 
+    # Bring clocks up before any timing: ~0.5 s of the workload itself.
+    t_end = time.perf_counter() + 0.5
+    while time.perf_counter() < t_end:
+        step()
+        torch.cuda.synchronize()
+
     ms_step, per = time_kernel(step, steps=args.steps, warmup=args.warmup)
     kern_ms = statistics.mean(per)
     value = flops / (ms_step * 1e-3) / 1e12
@@ -211,6 +220,16 @@ def main() -> int:
         },
         "sweep": sweep,
     }
+
+    if args.copy_probe_mib > 0:
+        n = args.copy_probe_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        line["copy_probe_bytes"] = n * 4
+        del src, dst
 
     if not args.no_cpu_baseline:
         _log("cpu baseline (eager restatement on host cores)")

@@ -64,7 +64,8 @@ typedef struct ta_fwd_args {
   int32_t tile_n;  /* keys per tile: 64 or 128 (TILEDATTN_TILE_N) */
   int32_t accum;   /* ta_accum */
   int32_t device;  /* HIP device ordinal the pointers and stream belong to */
-  int32_t sched;   /* workgroup -> tile order: 0 plain, 1 XCD-grouped (see ta_sdpa_fwd) */
+  int32_t sched;   /* workgroup -> tile order: 0 plain, 1 XCD-grouped, 2 XCD-grouped with
+                      causal heavy/light complementary order */
   int32_t reserved;
 } ta_fwd_args;
 

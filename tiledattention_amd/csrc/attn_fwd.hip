@@ -17,10 +17,10 @@
 //   the transposed V reads use the same permutation, so no lane shuffle is needed.  Each
 //   lane again holds one query, so the per-query rescale by alpha and the final 1/l are
 //   lane-local.
-// * K/V tiles go HBM -> VGPR -> LDS through two LDS stages: tile t+1 is fetched while
-//   tile t is consumed; one barrier per tile.  Rows are unpadded and 16-byte chunks are
-//   XOR-swizzled per row (different swizzles for K and V) so the b128 K reads and the b64
-//   transposed V reads are free of bank conflicts on the 64-bank LDS.
+// * K/V tiles go HBM -> VGPR -> LDS through two LDS stages: tile t+1 is fetched (buffer
+//   loads, range-checked so rows past S read as zero) while tile t is consumed; one
+//   barrier per tile.  LDS rows are padded (K: 2D+16 bytes, V: 2D+64 bytes) so the b128 K
+//   reads and the b64 transposed V reads are free of bank conflicts on the 64-bank LDS.
 // * exp is v_exp_f32 (2^x) with scale*log2(e) folded into one FMA per score.
 // * Causal: tiles above the diagonal are never loaded by a wave that does not need them,
 //   32-key blocks above a wave's rows are skipped, and only the diagonal block is masked.
@@ -32,6 +32,8 @@
 //   sequence (acc = rnd(rnd(acc*rnd(alpha)) + rnd(P.V)), l from the unrounded P).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 #include "attn_fwd_params.h"
 
@@ -53,7 +55,6 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef short s16x4 __attribute__((__vector_size__(4 * sizeof(short))));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 
 // Initial running max, raw score units (the reference starts from -1e30, flash_fwd.py:14).
 // Finite, so the first rescale factor 2^((m0 - m)*c) is exactly 0 rather than NaN.
@@ -123,16 +124,29 @@ __device__ static inline void swap32(float x, float& a, float& b) {
 
 __device__ static inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// 16-byte chunk swizzles (chunk index within a row, row index within the tile).
-// K: the 16 lanes of one b128 read pass hit 16 consecutive rows at one logical chunk.
-// V: one b64 transposed read pass covers 4 rows x 4 consecutive logical chunks.
+// IEEE 754-2019 maximum (NaN-propagating): lowers to v_maximum3_f32 on gfx950 without the
+// operand canonicalisation fmaxf needs in IEEE mode.
+__device__ static inline float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ static inline float vmax3(float a, float b, float c) { return vmax(a, vmax(b, c)); }
+
+// LDS rows are padded so that every LDS address is a per-lane base plus an immediate
+// offset and both read patterns are free of bank conflicts on the 64-bank LDS:
+// * K (stride 2D + 16 bytes = 4 banks mod 64): one b128 read pass covers 16 consecutive
+//   rows at one 16-byte column -> 16 disjoint 4-bank groups;
+// * V (stride 2D + 64 bytes = 16 banks mod 64): one b64 transposed read pass covers 4
+//   consecutive rows x 64 bytes -> 4 disjoint 16-bank groups.
 template <int D>
-__device__ static inline int swz_k(int row) {
-  return D == 128 ? (row & 15) : ((row >> 1) & 7);
-}
-template <int D>
-__device__ static inline int swz_v(int row) {
-  return D == 128 ? ((row & 3) << 2) : (((row >> 1) & 1) << 2);
+struct LdsLayout {
+  static constexpr int KS = 2 * D + 16;  // K row stride, bytes
+  static constexpr int VS = 2 * D + 64;  // V row stride, bytes
+};
+
+// Buffer resource for rows [0, rows) of a row-major tensor with `row_bytes` between rows:
+// loads past the last row return zeros (the hardware range check), which zero-fills the
+// ragged last key tile without any per-lane select.
+__device__ static inline __amdgpu_buffer_rsrc_t row_rsrc(const void* base, int rows, int row_bytes) {
+  const int bytes = rows > 0 ? rows * row_bytes : 0;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
 }
 
 template <int DT, int D, int TM, int TN, bool CAUSAL, bool TAIL, bool LOWP>
@@ -143,13 +157,15 @@ __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
   constexpr int DK = D / 16;         // k-steps of the QK^T product
   constexpr int DB = D / 32;         // 32-wide d blocks of O
   constexpr int CPR = D / 8;         // 16-byte chunks per row
-  constexpr int TILE_CHUNKS = TN * CPR;
-  constexpr int LD_PER_THREAD = TILE_CHUNKS / NT;  // chunks per thread per tensor per tile
-  static_assert(TILE_CHUNKS % NT == 0, "tile must split evenly over threads");
-  constexpr int TILE_ELEMS = TN * D;  // halves per K (or V) tile
+  constexpr int LD = TN * CPR / NT;  // 16-byte chunks per thread per tensor per tile
+  constexpr int RPP = NT / CPR;      // rows covered by one staging pass
+  static_assert((TN * CPR) % NT == 0 && NT % CPR == 0, "tile must split evenly over threads");
+  using L = LdsLayout<D>;
+  constexpr int K_BYTES = TN * L::KS;
+  constexpr int STAGE = K_BYTES + TN * L::VS;
   using DTy = DType<DT>;
 
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * 2 * TILE_ELEMS];
+  __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -158,18 +174,24 @@ __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
   const int hl = lane >> 5;  // which half of the wave
 
   // ---- block -> (bh, q tile) ------------------------------------------------------
+  // sched 0: block ids in (bh, q tile) order.  sched >= 1: hardware hands block ids to
+  // the 8 XCDs round-robin (block b runs on XCD b % 8), so consecutive logical tiles are
+  // regrouped onto one XCD, keeping a head's K/V in one L2.  Causal tiles get heavier
+  // with the tile index; sched <= 1 issues them heaviest first, sched 2 issues the
+  // heavier half first and then the lighter half from the top, so the j-th and
+  // (j + nq/2)-th tiles of a head - which land on the same CU when each XCD fills one
+  // workgroup slot per CU before the next - add up to the same amount of work.
   const int nq = p.n_qblk;
   const int total = nq * p.n_bh;
   int lin = blockIdx.x;
-  if (p.sched == 1) {
-    // Group consecutive logical tiles onto one XCD: hardware hands block ids to the 8
-    // XCDs round-robin, so block id b runs on XCD b % 8.
-    const int per = total >> 3;
-    if ((total & 7) == 0) lin = (lin & 7) * per + (lin >> 3);
-  }
+  if (p.sched >= 1 && (total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
   const int bh = lin / nq;
-  int qt = lin - bh * nq;
-  if (CAUSAL) qt = nq - 1 - qt;  // heaviest query tiles first
+  const int j = lin - bh * nq;
+  int qt = j;
+  if (CAUSAL) {
+    const int half = (nq + 1) >> 1;
+    qt = (p.sched == 2) ? (j < half ? nq - 1 - j : j - half) : nq - 1 - j;
+  }
   const int b = bh / p.H;
   const int h = bh - b * p.H;
   const int S = p.S;
@@ -178,6 +200,8 @@ __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
   const uint16_t* __restrict__ kp = p.k + b * p.k_sb + h * p.k_sh;
   const uint16_t* __restrict__ vp = p.v + b * p.v_sb + h * p.v_sh;
   uint16_t* __restrict__ op = p.o + b * p.o_sb + h * p.o_sh;
+  const int k_rb = (int)p.k_ss * 2;  // row bytes
+  const int v_rb = (int)p.v_ss * 2;
 
   const int q0 = qt * TM;
   const int wq0 = q0 + wave * 32;  // first query row of this wave
@@ -200,33 +224,45 @@ __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
   const int n_tiles = (kv_end + TN - 1) / TN;
   const int wave_kv_end = CAUSAL ? min(S, wq0 + 32) : S;
 
-  // ---- staging: HBM -> VGPR -> LDS ----------------------------------------------------
-  u32x4 stk[LD_PER_THREAD], stv[LD_PER_THREAD];
+  // ---- staging: HBM -> VGPR -> LDS --------------------------------------------------
+  // Thread t moves 16-byte chunks t, t + NT, ... of each tile: row (t / CPR) + i * RPP,
+  // column chunk t % CPR.  Global side: buffer loads at a fixed per-thread byte offset
+  // from a per-tile resource; LDS side: a fixed per-thread base plus immediates.
+  const int st_row = tid / CPR;
+  const int st_ch = tid % CPR;
+  const int st_koff = st_row * k_rb + st_ch * 16;
+  const int st_voff = st_row * v_rb + st_ch * 16;
+  const int st_klds = st_row * L::KS + st_ch * 16;
+  const int st_vlds = K_BYTES + st_row * L::VS + st_ch * 16;
+  u32x4 stk[LD], stv[LD];
   auto load_tile = [&](int kt) {
+    const int rows = S - kt * TN;
+    const __amdgpu_buffer_rsrc_t kr = row_rsrc(kp + (int64_t)kt * TN * p.k_ss, rows, k_rb);
+    const __amdgpu_buffer_rsrc_t vr = row_rsrc(vp + (int64_t)kt * TN * p.v_ss, rows, v_rb);
 #pragma unroll
-    for (int i = 0; i < LD_PER_THREAD; ++i) {
-      const int idx = tid + i * NT;
-      const int row = idx / CPR;
-      const int pc = idx % CPR;
-      const int key = kt * TN + row;
-      const bool ok = !TAIL || key < S;
-      const int kr = ok ? key : 0;
-      u32x4 kv = *(const u32x4*)(kp + (int64_t)kr * p.k_ss + ((pc ^ swz_k<D>(row)) << 3));
-      u32x4 vv = *(const u32x4*)(vp + (int64_t)kr * p.v_ss + ((pc ^ swz_v<D>(row)) << 3));
-      stk[i] = ok ? kv : u32x4{0, 0, 0, 0};
-      stv[i] = ok ? vv : u32x4{0, 0, 0, 0};
+    for (int i = 0; i < LD; ++i) {
+      stk[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, st_koff + i * RPP * k_rb, 0, 0));
+      stv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, st_voff + i * RPP * v_rb, 0, 0));
     }
   };
   auto store_tile = [&](int stage) {
-    uint16_t* kd = smem + stage * 2 * TILE_ELEMS;
-    uint16_t* vd = kd + TILE_ELEMS;
+    char* base = smem + stage * STAGE;
 #pragma unroll
-    for (int i = 0; i < LD_PER_THREAD; ++i) {
-      const int idx = tid + i * NT;
-      *(u32x4*)(kd + idx * 8) = stk[i];
-      *(u32x4*)(vd + idx * 8) = stv[i];
+    for (int i = 0; i < LD; ++i) {
+      *(u32x4*)(base + st_klds + i * RPP * L::KS) = stk[i];
+      *(u32x4*)(base + st_vlds + i * RPP * L::VS) = stv[i];
     }
   };
+
+  // ---- per-lane LDS read offsets --------------------------------------------------------
+  // K (A operand of S^T = K Q^T): lane reads row l32 of a 32-key block, 16 bytes at
+  // column 16 * (2 kk + hl).
+  const int k_rd = l32 * L::KS + hl * 16;
+  // V^T (A operand of O^T = V^T P^T) via the transposed read: lane l of 16-lane group G
+  // addresses row (key) 4 * hl + (l % 16) / 4 of a 16-key chunk and d = 16 * (G % 2) +
+  // 4 * (l % 4); the hardware hands lane l column d = 16 * (G % 2) + l % 16 of those 4 rows.
+  const int v_rd = K_BYTES + (4 * hl + ((lane & 15) >> 2)) * L::VS +
+                   (16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2;
 
   // ---- running state (lane = query l32 of this wave) ----------------------------------
   float m_run = kNegLarge;   // reference point of the exponent, raw score units
@@ -238,45 +274,35 @@ __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
     o_acc[db] = f32x16{};
     if (LOWP) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) o_lp[db][j] = 0u;
+      for (int jj = 0; jj < 8; ++jj) o_lp[db][jj] = 0u;
     }
   }
   const float c = p.scale_log2;
 
-  if (n_tiles > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  __syncthreads();
-
-  for (int kt = 0; kt < n_tiles; ++kt) {
-    const bool has_next = kt + 1 < n_tiles;
-    if (has_next) load_tile(kt + 1);
-
-    const int k0 = kt * TN;
-    if (k0 < wave_kv_end) {
-      const uint16_t* ks = smem + (kt & 1) * 2 * TILE_ELEMS;
-      const uint16_t* vs = ks + TILE_ELEMS;
-
-      // -- S^T blocks ------------------------------------------------------------------
-      f32x16 s[KB];
-      bool active[KB];
+  // One key tile.  FULL: every 32-key block of the tile is visible to every row of the
+  // wave (no mask, no skipped block) - the common case, compiled without any per-block
+  // condition.
+  auto tile = [&](const char* st, int k0, auto full_tag) {
+    constexpr bool FULL = decltype(full_tag)::value;
+    bool active[KB];
 #pragma unroll
-      for (int bk = 0; bk < KB; ++bk) {
-        active[bk] = (k0 + 32 * bk) < wave_kv_end;
-        s[bk] = f32x16{};
-        if (active[bk]) {
-          const int row = 32 * bk + l32;
+    for (int bk = 0; bk < KB; ++bk) active[bk] = FULL || (k0 + 32 * bk) < wave_kv_end;
+
+    // -- S^T blocks ------------------------------------------------------------------
+    f32x16 s[KB];
 #pragma unroll
-          for (int kk = 0; kk < DK; ++kk) {
-            const int ch = (2 * kk + hl) ^ swz_k<D>(row);
-            u32x4 a = *(const u32x4*)(ks + row * D + ch * 8);
-            s[bk] = DTy::mfma(a, qf[kk], s[bk]);
-          }
-        }
+    for (int bk = 0; bk < KB; ++bk) {
+      if (active[bk]) {
+        const char* kb = st + k_rd + bk * 32 * L::KS;
+        f32x16 acc = DTy::mfma(*(const u32x4*)kb, qf[0], f32x16{});
+#pragma unroll
+        for (int kk = 1; kk < DK; ++kk) acc = DTy::mfma(*(const u32x4*)(kb + 32 * kk), qf[kk], acc);
+        s[bk] = acc;
       }
+    }
 
-      // -- mask (diagonal block for causal, keys past S for ragged tails) ---------------
+    // -- mask (diagonal block for causal, keys past S for ragged tails) ---------------
+    if (!FULL) {
       const bool need_tail = TAIL && (k0 + TN > S);
 #pragma unroll
       for (int bk = 0; bk < KB; ++bk) {
@@ -293,113 +319,133 @@ __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
           }
         }
       }
+    }
 
-      // -- row max -----------------------------------------------------------------------
-      float mx = kMasked;
+    // -- row max -----------------------------------------------------------------------
+    float mxa = kMasked, mxb = kMasked;  // two independent 3-input chains
 #pragma unroll
-      for (int bk = 0; bk < KB; ++bk) {
-        if (active[bk]) {
+    for (int bk = 0; bk < KB; ++bk) {
+      if (active[bk]) {
 #pragma unroll
-          for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[bk][r], s[bk][r + 1]));
+        for (int r = 0; r < 16; r += 4) {
+          mxa = vmax3(mxa, s[bk][r], s[bk][r + 1]);
+          mxb = vmax3(mxb, s[bk][r + 2], s[bk][r + 3]);
         }
       }
-      {
-        float a0, a1;
-        swap32(mx, a0, a1);
-        mx = fmaxf(a0, a1);
-      }
+    }
+    float mx;
+    {
+      float a0, a1;
+      swap32(vmax(mxa, mxb), a0, a1);
+      mx = vmax(a0, a1);
+    }
 
-      // -- new reference point, rescale of running state ---------------------------------
-      float alpha = 1.0f;
-      if (LOWP) {
-        const float m_new = fmaxf(m_run, mx);
+    // -- new reference point, rescale of running state ---------------------------------
+    float alpha = 1.0f;
+    if (LOWP) {
+      const float m_new = vmax(m_run, mx);
+      alpha = fast_exp2((m_run - m_new) * c);
+      m_run = m_new;
+    } else {
+      const bool need = (mx - m_run) * c > kRescaleLog2;
+      if (__ballot(need)) {
+        const float m_new = need ? mx : m_run;
         alpha = fast_exp2((m_run - m_new) * c);
         m_run = m_new;
-      } else {
-        const bool need = (mx - m_run) * c > kRescaleLog2;
-        if (__builtin_amdgcn_read_exec() & __ballot(need)) {
-          const float m_new = need ? mx : m_run;
-          alpha = fast_exp2((m_run - m_new) * c);
-          m_run = m_new;
 #pragma unroll
-          for (int db = 0; db < DB; ++db) o_acc[db] *= alpha;
-        }
+        for (int db = 0; db < DB; ++db) o_acc[db] *= alpha;
       }
-      l_part *= alpha;
+    }
+    l_part *= alpha;
 
-      // -- P = 2^(s*c - m*c), packed to the input dtype -------------------------------------
-      // fp32 accumulation sums l from the same rounded P that feeds P.V, so the weights
-      // are normalised consistently (with the lazy reference point the dominant key's P
-      // is not exactly 1 and its rounding would otherwise not cancel).  Input-dtype
-      // accumulation keeps the reference's fp32 sum of the unrounded P (flash_fwd.py:429).
-      const float mc = m_run * c;
-      uint32_t pk[KB][8];
+    // -- P = 2^(s*c - m*c), packed to the input dtype -------------------------------------
+    // fp32 accumulation sums l from the same rounded P that feeds P.V, so the weights
+    // are normalised consistently (with the lazy reference point the dominant key's P
+    // is not exactly 1 and its rounding would otherwise not cancel).  Input-dtype
+    // accumulation keeps the reference's fp32 sum of the unrounded P (flash_fwd.py:429).
+    const float mc = m_run * c;
+    uint32_t pk[KB][8];
+#pragma unroll
+    for (int bk = 0; bk < KB; ++bk) {
+      if (active[bk]) {
+        float la = 0.0f, lb = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+          const float p0 = fast_exp2(__builtin_fmaf(s[bk][r], c, -mc));
+          const float p1 = fast_exp2(__builtin_fmaf(s[bk][r + 1], c, -mc));
+          const uint32_t w = DTy::pack(p0, p1);
+          pk[bk][r >> 1] = w;
+          if (LOWP) {
+            l_part += p0 + p1;
+          } else if (r & 2) {
+            lb = DTy::sum2(w, lb);
+          } else {
+            la = DTy::sum2(w, la);
+          }
+        }
+        if (!LOWP) l_part += la + lb;
+      }
+    }
+
+    // -- O^T += V^T P^T ------------------------------------------------------------------
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      f32x16 acc = LOWP ? f32x16{} : o_acc[db];
 #pragma unroll
       for (int bk = 0; bk < KB; ++bk) {
         if (active[bk]) {
-          float la = 0.0f, lb = 0.0f;
 #pragma unroll
-          for (int r = 0; r < 16; r += 2) {
-            const float p0 = fast_exp2(__builtin_fmaf(s[bk][r], c, -mc));
-            const float p1 = fast_exp2(__builtin_fmaf(s[bk][r + 1], c, -mc));
-            const uint32_t w = DTy::pack(p0, p1);
-            pk[bk][r >> 1] = w;
-            if (LOWP) {
-              l_part += p0 + p1;
-            } else if (r & 2) {
-              lb = DTy::sum2(w, lb);
-            } else {
-              la = DTy::sum2(w, la);
-            }
+          for (int kc = 0; kc < 2; ++kc) {
+            const char* a0p = st + v_rd + (32 * bk + 16 * kc) * L::VS + 64 * db;
+            s16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)a0p);
+            s16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a0p + 8 * L::VS));
+            u32x2 w0 = __builtin_bit_cast(u32x2, r0);
+            u32x2 w1 = __builtin_bit_cast(u32x2, r1);
+            u32x4 a = {w0[0], w0[1], w1[0], w1[1]};
+            u32x4 bfrag = {pk[bk][4 * kc + 0], pk[bk][4 * kc + 1], pk[bk][4 * kc + 2],
+                           pk[bk][4 * kc + 3]};
+            acc = DTy::mfma(a, bfrag, acc);
           }
-          if (!LOWP) l_part += la + lb;
         }
       }
+      if (LOWP) {
+        const float al = DTy::round(alpha);
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          const float t0 = DTy::round(DTy::lo(o_lp[db][jj]) * al);
+          const float t1 = DTy::round(DTy::hi(o_lp[db][jj]) * al);
+          const float u0 = DTy::round(acc[2 * jj]);
+          const float u1 = DTy::round(acc[2 * jj + 1]);
+          o_lp[db][jj] = DTy::pack(t0 + u0, t1 + u1);
+        }
+      } else {
+        o_acc[db] = acc;
+      }
+    }
+  };
 
-      // -- O^T += V^T P^T ------------------------------------------------------------------
-      // Transposed V read: lane l of 16-lane group G reads row (key) r = (l%16)/4 of the
-      // 4-key group and 4 consecutive d at 4*(l%4); the hardware hands lane l column
-      // d = 16*(G%2) + l%16 of those 4 rows.
-      const int tr_r = (lane & 15) >> 2;
-      const int tr_d = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        f32x16 acc = LOWP ? f32x16{} : o_acc[db];
-#pragma unroll
-        for (int bk = 0; bk < KB; ++bk) {
-          if (active[bk]) {
-#pragma unroll
-            for (int kc = 0; kc < 2; ++kc) {
-              const int kbase = 32 * bk + 16 * kc + 4 * hl + tr_r;
-              const int d = 32 * db + tr_d;
-              const int row0 = kbase, row1 = kbase + 8;
-              const uint16_t* a0p = vs + row0 * D + (((d >> 3) ^ swz_v<D>(row0)) << 3) + (d & 7);
-              const uint16_t* a1p = vs + row1 * D + (((d >> 3) ^ swz_v<D>(row1)) << 3) + (d & 7);
-              s16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)a0p);
-              s16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)a1p);
-              u32x2 w0 = __builtin_bit_cast(u32x2, r0);
-              u32x2 w1 = __builtin_bit_cast(u32x2, r1);
-              u32x4 a = {w0[0], w0[1], w1[0], w1[1]};
-              u32x4 bfrag = {pk[bk][4 * kc + 0], pk[bk][4 * kc + 1], pk[bk][4 * kc + 2],
-                             pk[bk][4 * kc + 3]};
-              acc = DTy::mfma(a, bfrag, acc);
-            }
-          }
-        }
-        if (LOWP) {
-          const float al = DTy::round(alpha);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float t0 = DTy::round(DTy::lo(o_lp[db][j]) * al);
-            const float t1 = DTy::round(DTy::hi(o_lp[db][j]) * al);
-            const float u0 = DTy::round(acc[2 * j]);
-            const float u1 = DTy::round(acc[2 * j + 1]);
-            o_lp[db][j] = DTy::pack(t0 + u0, t1 + u1);
-          }
-        } else {
-          o_acc[db] = acc;
-        }
-      }
+  if (n_tiles > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  // Drain the Q-fragment loads here, on every path into the loop: otherwise the
+  // waitcnt insertion merges a "Q still in flight" state into the loop header and puts a
+  // vmcnt wait on the next tile's prefetch in front of every QK^T MFMA.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  for (int kt = 0; kt < n_tiles; ++kt) {
+    const bool has_next = kt + 1 < n_tiles;
+    if (has_next) load_tile(kt + 1);
+
+    const int k0 = kt * TN;
+    const char* st = smem + (kt & 1) * STAGE;
+    // Fully visible: every key of the tile is <= the wave's first query (causal) and < S.
+    const bool full = (!CAUSAL || k0 + TN - 1 <= wq0) && (!TAIL || k0 + TN <= S);
+    if (full) {
+      tile(st, k0, std::true_type{});
+    } else if (k0 < wave_kv_end) {
+      tile(st, k0, std::false_type{});
     }
 
     if (has_next) store_tile((kt + 1) & 1);
@@ -434,6 +480,15 @@ __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
 
 }  // namespace ta
 
+// Waves per SIMD the register allocation is sized for: two when two workgroups fit a CU
+// by LDS (TM = 128, TN = 64: 8 waves per CU), so one wave's MFMAs overlap the other's
+// softmax; one otherwise.
+#if TA_TILE_M == 128 && TA_TILE_N == 64
+#define TA_WAVES_PER_SIMD 2
+#else
+#define TA_WAVES_PER_SIMD 1
+#endif
+
 // One extern "C" entry per (dtype, D, causal, tail, accumulation) at this file's (TM, TN).
 // Name: ta_fwd_<f16|bf16>_d<D>_m<TM>_n<TN>_c<0|1>_t<0|1>_a<0|1>.
 #define TA_NAME2(DTN, D, M, N, C, T, A) ta_fwd_##DTN##_d##D##_m##M##_n##N##_c##C##_t##T##_a##A
@@ -441,6 +496,7 @@ __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
 
 #define TA_DEFINE(DTN, DT, D, C, T, A)                                                      \
   extern "C" __global__ void __launch_bounds__(TA_TILE_M * 2)                               \
+      __attribute__((amdgpu_waves_per_eu(TA_WAVES_PER_SIMD, TA_WAVES_PER_SIMD)))            \
       TA_NAME(DTN, D, TA_TILE_M, TA_TILE_N, C, T, A)(ta::FwdParams p) {                     \
     ta::attn_fwd_body<DT, D, TA_TILE_M, TA_TILE_N, (C != 0), (T != 0), (A != 0)>(p);         \
   }

@@ -205,7 +205,7 @@ ta_status ta_sdpa_fwd(const ta_fwd_args* a, void* stream) {
   if (a->accum != TA_ACC_FP32 && a->accum != TA_ACC_INPUT)
     return fail(TA_EINVAL, "accum %d", a->accum);
   if (a->causal != 0 && a->causal != 1) return fail(TA_EINVAL, "causal %d", a->causal);
-  if (a->sched != 0 && a->sched != 1) return fail(TA_EINVAL, "sched %d", a->sched);
+  if (a->sched < 0 || a->sched > 2) return fail(TA_EINVAL, "sched %d", a->sched);
   if (a->B < 0 || a->H < 0 || a->S < 0) return fail(TA_EINVAL, "negative shape");
   if (a->D != 64 && a->D != 128)
     return fail(TA_EUNSUPPORTED, "head_dim %lld (kernels exist for 64 and 128)", (long long)a->D);
@@ -226,6 +226,9 @@ ta_status ta_sdpa_fwd(const ta_fwd_args* a, void* stream) {
                     (long long)st[i][j]);
   }
   if (a->S > 0x7fffffffLL || a->H > 0x7fffffffLL) return fail(TA_EINVAL, "S or H too large");
+  // K and V are read with buffer instructions whose byte range is 32-bit.
+  if (a->S * a->k_stride[2] * 2 > 0x7fffffffLL || a->S * a->v_stride[2] * 2 > 0x7fffffffLL)
+    return fail(TA_EINVAL, "k/v: S * row stride must stay below 2^31 bytes per (b, h) slice");
   const int64_t n_bh = a->B * a->H;
   const int64_t n_qblk = (a->S + a->tile_m - 1) / a->tile_m;
   if (n_bh > 0x7fffffffLL || n_bh * n_qblk > 0x7fffffffLL)

@@ -28,8 +28,8 @@ Environment knobs are re-read on every call, as in the reference:
     Parsed as in flash_fwd.py:166-196.  A chunked plan computes the same attention as the
     unchunked one, so here it runs the zero-padded kernel (96 -> 128); 160 is rejected.
 ``TILEDATTN_SCHED`` (this build only)
-    Workgroup-to-tile order: ``0`` plain, ``1`` XCD-grouped; default picks 1 when the grid
-    splits evenly over the 8 XCDs.
+    Workgroup-to-tile order: ``0`` plain, ``1`` XCD-grouped, ``2`` XCD-grouped with causal
+    heavy/light complementary order; default: see ``_resolve_sched``.
 """
 
 from __future__ import annotations
@@ -238,12 +238,22 @@ def _resolve_sync_mode() -> str:
     return sync_mode
 
 
-def _resolve_sched(*, n_blocks: int) -> int:
+_CU_COUNT = 256  # MI355X
+
+
+def _resolve_sched(*, n_blocks: int, causal: bool, tile_m: int, tile_n: int) -> int:
+    """Workgroup order.  XCD grouping needs the grid to split evenly over the 8 XCDs; the
+    complementary causal order pays off only when every workgroup is resident at once
+    (two per CU for the 128x64 tile, one otherwise), because it relies on which
+    workgroups share a CU."""
     raw = os.getenv("TILEDATTN_SCHED", "").strip()
     if raw == "":
-        return 1 if n_blocks % 8 == 0 else 0
-    if raw not in {"0", "1"}:
-        raise ValueError(f"Unsupported TILEDATTN_SCHED={raw!r}. Use 0 or 1.")
+        if n_blocks % 8 != 0:
+            return 0
+        resident = _CU_COUNT * (2 if (tile_m, tile_n) == (128, 64) else 1)
+        return 2 if causal and n_blocks <= resident else 1
+    if raw not in {"0", "1", "2"}:
+        raise ValueError(f"Unsupported TILEDATTN_SCHED={raw!r}. Use 0, 1 or 2.")
     return int(raw)
 
 
@@ -388,7 +398,7 @@ def run_flash_fwd(
     args.tile_m, args.tile_n = tile_m, tile_n
     args.accum = accum_code
     args.device = device_index
-    args.sched = _resolve_sched(n_blocks=bh * n_qblk)
+    args.sched = _resolve_sched(n_blocks=bh * n_qblk, causal=causal, tile_m=tile_m, tile_n=tile_n)
 
     stream = torch_mod.cuda.current_stream(device)
     if sync_mode == "strict":
