@@ -1,0 +1,138 @@
+"""The C-ABI library on the CPU: it loads, exports every function include/tiledattn.h
+declares, and rejects bad arguments with the documented status before any HIP call.
+No kernel is launched here (there is no GPU in the CPU suite)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from tiledattention_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "tiledattn.h"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.library_path().exists():
+        pytest.fail("libtiledattn.so is not built: run __graft_entry__.build() first")
+    return _lib.load()
+
+
+def _declared_functions() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"^\s*(?:[A-Za-z_][\w\s\*]*?)\b(ta_\w+)\s*\(", text, flags=re.M))
+
+
+def test_header_and_binding_agree():
+    assert _declared_functions() == set(_lib.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    raw = ctypes.CDLL(str(_lib.library_path()))
+    for name in _declared_functions():
+        assert hasattr(raw, name), name
+
+
+def test_abi_version_and_status_names(lib):
+    assert lib.ta_abi_version() == _lib.ABI_VERSION == 1
+    names = [lib.ta_status_string(i).decode() for i in range(5)]
+    assert names == ["TA_OK", "TA_EINVAL", "TA_EUNSUPPORTED", "TA_ENOKERNEL", "TA_EHIP"]
+    assert lib.ta_status_string(99).decode() == "TA_UNKNOWN"
+
+
+def _args(**kw) -> _lib.FwdArgs:
+    a = _lib.FwdArgs()
+    a.q = a.k = a.v = a.o = 0x10000  # never dereferenced: validation fails or no launch
+    a.B, a.H, a.S, a.D = 1, 2, 64, 64
+    for name in ("q_stride", "k_stride", "v_stride", "o_stride"):
+        getattr(a, name)[:] = (2 * 64 * 64, 64 * 64, 64, 1)
+    a.scale, a.causal, a.dtype, a.tile_m, a.tile_n, a.accum, a.device, a.sched = 0.125, 0, 0, 64, 64, 0, 0, 0
+    for key, val in kw.items():
+        if key.endswith("_stride"):
+            getattr(a, key)[:] = val
+        else:
+            setattr(a, key, val)
+    return a
+
+
+def _call(lib, a):
+    return lib.ta_sdpa_fwd(ctypes.byref(a), None)
+
+
+@pytest.mark.parametrize("kw,status,msg", [
+    (dict(dtype=2), _lib.TA_EINVAL, "dtype"),
+    (dict(accum=5), _lib.TA_EINVAL, "accum"),
+    (dict(causal=2), _lib.TA_EINVAL, "causal"),
+    (dict(sched=3), _lib.TA_EINVAL, "sched"),
+    (dict(S=-1), _lib.TA_EINVAL, "negative"),
+    (dict(D=96), _lib.TA_EUNSUPPORTED, "head_dim"),
+    (dict(tile_m=32), _lib.TA_EUNSUPPORTED, "tile"),
+    (dict(tile_n=256), _lib.TA_EUNSUPPORTED, "tile"),
+    (dict(q=0), _lib.TA_EINVAL, "null"),
+    (dict(v=0x10008), _lib.TA_EINVAL, "16-byte aligned"),
+    (dict(k_stride=(2 * 64 * 64, 64 * 64, 64, 2)), _lib.TA_EINVAL, "last-dim stride"),
+    (dict(o_stride=(2 * 64 * 64, 64 * 64, 68, 1)), _lib.TA_EINVAL, "multiple of 8"),
+    (dict(S=1 << 24, k_stride=(0, 0, 128, 1), D=128), _lib.TA_EINVAL, "2^31"),
+])
+def test_argument_validation(lib, kw, status, msg):
+    st = _call(lib, _args(**kw))
+    assert st == status
+    assert msg in _lib.last_error(lib)
+
+
+def test_null_args_pointer(lib):
+    assert lib.ta_sdpa_fwd(None, None) == _lib.TA_EINVAL
+    assert "NULL" in _lib.last_error(lib)
+
+
+@pytest.mark.parametrize("kw", [dict(B=0), dict(H=0), dict(S=0)])
+def test_zero_size_is_ok_without_launch(lib, kw):
+    assert _call(lib, _args(q=0, k=0, v=0, o=0, **kw)) == _lib.TA_OK
+
+
+@pytest.mark.parametrize("args,status", [
+    ((0, 3, 64, 64, 64, 0, 0, 1), _lib.TA_EINVAL),        # dtype
+    ((0, 0, 96, 64, 64, 0, 0, 1), _lib.TA_EUNSUPPORTED),  # head dim
+    ((0, 0, 64, 48, 64, 0, 0, 1), _lib.TA_EUNSUPPORTED),  # tile
+    ((0, 0, 64, 64, 64, 0, 9, 1), _lib.TA_EINVAL),        # accum
+])
+def test_prepare_validation(lib, args, status):
+    assert lib.ta_prepare(*args) == status
+
+
+def test_cache_calls_and_code_object_dir(lib):
+    assert lib.ta_cache_reset() == _lib.TA_OK
+    assert lib.ta_cache_size() == 0
+    assert lib.ta_set_code_object_dir(None) == _lib.TA_EINVAL
+    assert lib.ta_set_code_object_dir(str(_lib.lib_dir()).encode()) == _lib.TA_OK
+
+
+def test_error_text_is_thread_local(lib):
+    import threading
+
+    _call(lib, _args(D=96))
+    seen = {}
+
+    def other():
+        seen["msg"] = _lib.last_error(lib)
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["msg"] == ""
+    assert "head_dim" in _lib.last_error(lib)
+
+
+def test_code_objects_built_for_gfx950():
+    for path in _lib.code_object_paths():
+        data = path.read_bytes()
+        # hipcc --genco writes a clang offload bundle holding the gfx950 ELF
+        assert data.startswith(b"__CLANG_OFFLOAD_BUNDLE__") or data[:4] == b"\x7fELF"
+        assert b"amdgcn-amd-amdhsa--gfx950" in data and b"\x7fELF" in data
+        for name in ("ta_fwd_bf16_d128", "ta_fwd_f16_d64"):
+            assert name.encode() in data

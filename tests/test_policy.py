@@ -1,0 +1,237 @@
+"""Knob and dispatch policy, pinned by closed-form case tables.
+
+Every table below is written from the reference source it restates (cited per test), not
+from this package's code, so a wrong threshold, a swapped default or a missing strip()
+fails here.  These run on the CPU.
+"""
+
+from __future__ import annotations
+
+import pytest
+
+from tiledattention_amd._errors import DTypeNotSupportedError, InvalidShapeError
+from tiledattention_amd.kernels import flash_fwd as ff
+
+
+# ---------------------------------------------------------------- flash_fwd.py:47-65
+@pytest.mark.parametrize("raw,default,expected", [
+    (None, 7, 7), ("", 7, 7), ("   ", 7, 7), ("64", None, 64), (" 128 ", None, 128), ("-3", 1, -3),
+])
+def test_get_env_int(monkeypatch, raw, default, expected):
+    if raw is None:
+        monkeypatch.delenv("TILEDATTN_X", raising=False)
+    else:
+        monkeypatch.setenv("TILEDATTN_X", raw)
+    assert ff._get_env_int("TILEDATTN_X", default) == expected
+
+
+def test_get_env_int_rejects_non_integer(monkeypatch):
+    monkeypatch.setenv("TILEDATTN_X", "64.0")
+    with pytest.raises(ValueError, match="Environment variable TILEDATTN_X must be an integer."):
+        ff._get_env_int("TILEDATTN_X", None)
+
+
+# ---------------------------------------------------------------- flash_fwd.py:68-84
+@pytest.mark.parametrize("m,n,expected", [
+    ("128", None, (128, 64)),   # unset partner defaults to 64
+    (None, "128", (64, 128)),
+    ("64", "64", (64, 64)),
+    ("128", "128", (128, 128)),
+    ("32", None, (32, 64)),     # parsed fine; the gfx950 dispatcher rejects it later
+])
+def test_resolve_tile_config(monkeypatch, m, n, expected):
+    for name, val in (("TILEDATTN_TILE_M", m), ("TILEDATTN_TILE_N", n)):
+        if val is None:
+            monkeypatch.delenv(name, raising=False)
+        else:
+            monkeypatch.setenv(name, val)
+    assert ff._resolve_tile_config() == expected
+
+
+@pytest.mark.parametrize("m,n", [("0", "64"), ("64", "-64")])
+def test_resolve_tile_config_rejects_non_positive(monkeypatch, m, n):
+    monkeypatch.setenv("TILEDATTN_TILE_M", m)
+    monkeypatch.setenv("TILEDATTN_TILE_N", n)
+    with pytest.raises(ValueError, match="must be positive"):
+        ff._resolve_tile_config()
+
+
+@pytest.mark.parametrize("tm,tn,ok", [(64, 64, True), (64, 128, True), (128, 64, True), (128, 128, True),
+                                      (32, 64, False), (64, 256, False), (96, 64, False)])
+def test_gfx950_tile_set(tm, tn, ok):
+    if ok:
+        ff._check_tile_supported(tm, tn)
+    else:
+        with pytest.raises(ValueError, match="Unsupported tile"):
+            ff._check_tile_supported(tm, tn)
+
+
+# ---------------------------------------------------------------- flash_fwd.py:241-259
+@pytest.mark.parametrize("s,d,causal,expected", [
+    (2048, 128, False, (64, 128)), (8192, 128, False, (64, 128)),
+    (2047, 128, False, (64, 64)), (2048, 128, True, (64, 64)),
+    (4096, 64, False, (64, 64)), (4096, 96, False, (64, 64)), (64, 64, True, (64, 64)),
+])
+def test_reference_default_tile_table(s, d, causal, expected):
+    assert ff._default_tile_config_for_shape(seq_len=s, head_dim=d, causal=causal) == expected
+
+
+# ---------------------------------------------------------------- flash_fwd.py:87-99
+def test_kernel_options_defaults_and_parse(monkeypatch):
+    assert ff._resolve_kernel_options() == (3, None, None)
+    monkeypatch.setenv("TILEDATTN_KERNEL_OPT_LEVEL", "2")
+    monkeypatch.setenv("TILEDATTN_KERNEL_OCCUPANCY", "4")
+    monkeypatch.setenv("TILEDATTN_KERNEL_NUM_CTAS", "2")
+    assert ff._resolve_kernel_options() == (2, 4, 2)
+    monkeypatch.setenv("TILEDATTN_KERNEL_OCCUPANCY", "many")
+    with pytest.raises(ValueError, match="TILEDATTN_KERNEL_OCCUPANCY must be an integer"):
+        ff._resolve_kernel_options()
+
+
+# ---------------------------------------------------------------- flash_fwd.py:102-146
+@pytest.mark.parametrize("s,d,causal,expected", [
+    (1024, 64, False, "fp16"), (4096, 64, False, "fp16"), (1023, 64, False, "fp32"),
+    (1024, 64, True, "fp32"), (1024, 128, False, "fp32"), (8192, 128, False, "fp32"),
+    (1024, 32, False, "fp32"),
+])
+def test_default_accum_mode_table(s, d, causal, expected):
+    assert ff._default_accum_mode_for_shape(seq_len=s, head_dim=d, causal=causal) == expected
+
+
+@pytest.mark.parametrize("raw,expected", [
+    (None, "fp16"), ("", "fp16"), ("auto", "fp16"), (" AUTO ", "fp16"),
+    ("fp32", "fp32"), (" FP32", "fp32"), ("fp16", "fp16"), ("Fp16 ", "fp16"),
+])
+def test_resolve_accum_mode(monkeypatch, raw, expected):
+    if raw is None:
+        monkeypatch.delenv("TILEDATTN_ACCUM_MODE", raising=False)
+    else:
+        monkeypatch.setenv("TILEDATTN_ACCUM_MODE", raw)
+    # shape where auto picks the input dtype: non-causal, D=64, S>=1024
+    assert ff._resolve_accum_mode(seq_len=2048, head_dim=64, causal=False) == expected
+
+
+@pytest.mark.parametrize("raw", ["bf16", "fp8", "32"])
+def test_resolve_accum_mode_rejects(monkeypatch, raw):
+    monkeypatch.setenv("TILEDATTN_ACCUM_MODE", raw)
+    with pytest.raises(ValueError, match="Unsupported TILEDATTN_ACCUM_MODE"):
+        ff._resolve_accum_mode(seq_len=64, head_dim=64, causal=False)
+
+
+# ---------------------------------------------------------------- flash_fwd.py:149-163
+@pytest.mark.parametrize("d,expected", [
+    (64, (64, 0)), (128, (128, 0)), (32, (32, 0)), (96, (128, 32)), (160, (256, 96)),
+    (48, (64, 16)), (100, (128, 28)), (1, (1, 0)), (65, (128, 63)),
+])
+def test_reference_head_dim_padding_rule(d, expected):
+    assert ff._resolve_kernel_head_dim(d) == expected
+
+
+@pytest.mark.parametrize("d,expected", [
+    (1, (64, 63)), (32, (64, 32)), (64, (64, 0)), (65, (128, 63)), (96, (128, 32)), (128, (128, 0)),
+])
+def test_gfx950_head_dim_padding(d, expected):
+    assert ff._resolve_kernel_head_dim_gfx950(d) == expected
+
+
+@pytest.mark.parametrize("d", [0, 129, 160, 256])
+def test_gfx950_head_dim_rejects(d):
+    with pytest.raises(InvalidShapeError):
+        ff._resolve_kernel_head_dim_gfx950(d)
+
+
+# ---------------------------------------------------------------- flash_fwd.py:166-196
+@pytest.mark.parametrize("raw,d,expected", [
+    (None, 96, None), ("", 96, None), ("96", 96, ((0, 64), (64, 32))),
+    ("160", 160, ((0, 128), (128, 32))), ("96,160", 160, ((0, 128), (128, 32))),
+    (" 96 , 160 ", 96, ((0, 64), (64, 32))), ("96", 128, None), ("64", 64, None), ("96,", 96, ((0, 64), (64, 32))),
+])
+def test_resolve_chunk_plan(monkeypatch, raw, d, expected):
+    if raw is None:
+        monkeypatch.delenv("TILEDATTN_CHUNKED_HEAD_DIMS", raising=False)
+    else:
+        monkeypatch.setenv("TILEDATTN_CHUNKED_HEAD_DIMS", raw)
+    assert ff._resolve_chunk_plan(d) == expected
+
+
+def test_resolve_chunk_plan_rejects(monkeypatch):
+    monkeypatch.setenv("TILEDATTN_CHUNKED_HEAD_DIMS", "96,x")
+    with pytest.raises(ValueError, match="comma-separated list of integers"):
+        ff._resolve_chunk_plan(96)
+
+
+# ---------------------------------------------------------------- flash_fwd.py:199-238
+_FP = dict(pad_dim=0, chunk_plan=None, tile_m=64, tile_n=64)
+
+
+@pytest.mark.parametrize("kw,expected", [
+    (dict(seq_len=1024, head_dim=64, causal=False), True),
+    (dict(seq_len=1023, head_dim=64, causal=False), False),      # below the D=64 threshold
+    (dict(seq_len=1024, head_dim=128, causal=False), False),     # D=128 needs S >= 2048
+    (dict(seq_len=2048, head_dim=128, causal=False), True),
+    (dict(seq_len=2048, head_dim=128, causal=True), False),      # never for causal
+    (dict(seq_len=1088, head_dim=64, causal=False, tile_n=128), False),  # 1088 % 128 != 0
+    (dict(seq_len=1152, head_dim=64, causal=False, tile_m=128), True),   # 1152 = 9*128
+    (dict(seq_len=4096, head_dim=96, causal=False), False),      # D not in {64, 128}
+    (dict(seq_len=4096, head_dim=64, causal=False, pad_dim=8), False),
+    (dict(seq_len=4096, head_dim=64, causal=False, chunk_plan=((0, 64),)), False),
+])
+def test_aligned_fastpath_predicate(kw, expected):
+    args = {**_FP, **kw}
+    assert ff._should_use_aligned_noncausal_fastpath(**args) is expected
+
+
+@pytest.mark.parametrize("raw,expected", [("", True), ("0", True), ("false", True), ("False", True),
+                                          ("1", False), ("true", False), ("FALSE", False), ("yes", False)])
+def test_aligned_fastpath_disable_env(monkeypatch, raw, expected):
+    monkeypatch.setenv("TILEDATTN_DISABLE_ALIGNED_FASTPATH", raw)
+    args = {**_FP, **dict(seq_len=1024, head_dim=64, causal=False)}
+    assert ff._should_use_aligned_noncausal_fastpath(**args) is expected
+
+
+# ---------------------------------------------------------------- flash_fwd.py:805-818
+@pytest.mark.parametrize("raw,expected", [(None, "async"), ("post", "post"), (" STRICT ", "strict"),
+                                          ("Async", "async")])
+def test_sync_mode(monkeypatch, raw, expected):
+    if raw is None:
+        monkeypatch.delenv("TILEDATTN_SYNC_MODE", raising=False)
+    else:
+        monkeypatch.setenv("TILEDATTN_SYNC_MODE", raw)
+    assert ff._resolve_sync_mode() == expected
+
+
+def test_sync_mode_rejected_before_launch(monkeypatch):
+    monkeypatch.setenv("TILEDATTN_SYNC_MODE", "eventually")
+    with pytest.raises(ValueError, match="Unsupported TILEDATTN_SYNC_MODE='eventually'"):
+        ff._resolve_sync_mode()
+
+
+# ---------------------------------------------------------------- flash_fwd.py:27-44
+def test_dtype_codes():
+    import torch
+
+    assert ff._dtype_code_for_torch_dtype(torch.float16) == 0
+    assert ff._dtype_code_for_torch_dtype(torch.bfloat16) == 1
+    with pytest.raises(DTypeNotSupportedError, match="float16 or torch.bfloat16"):
+        ff._dtype_code_for_torch_dtype(torch.float32)
+
+
+# ---------------------------------------------------------------- workgroup order (this build)
+@pytest.mark.parametrize("n,causal,tiles,expected", [
+    (512, True, (128, 64), 2),    # C3 S=8192: all 512 workgroups resident (2 per CU)
+    (1024, True, (128, 64), 1),   # C5: two rounds -> heavy first
+    (256, True, (128, 128), 2),
+    (512, True, (128, 128), 1),
+    (512, False, (128, 64), 1),
+    (12, True, (128, 64), 0),     # does not split over the 8 XCDs
+])
+def test_sched_default(n, causal, tiles, expected):
+    assert ff._resolve_sched(n_blocks=n, causal=causal, tile_m=tiles[0], tile_n=tiles[1]) == expected
+
+
+def test_sched_env(monkeypatch):
+    monkeypatch.setenv("TILEDATTN_SCHED", "0")
+    assert ff._resolve_sched(n_blocks=512, causal=True, tile_m=128, tile_n=64) == 0
+    monkeypatch.setenv("TILEDATTN_SCHED", "3")
+    with pytest.raises(ValueError, match="TILEDATTN_SCHED"):
+        ff._resolve_sched(n_blocks=512, causal=True, tile_m=128, tile_n=64)
