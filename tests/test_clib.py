@@ -134,5 +134,7 @@ def test_code_objects_built_for_gfx950():
         # hipcc --genco writes a clang offload bundle holding the gfx950 ELF
         assert data.startswith(b"__CLANG_OFFLOAD_BUNDLE__") or data[:4] == b"\x7fELF"
         assert b"amdgcn-amd-amdhsa--gfx950" in data and b"\x7fELF" in data
-        for name in ("ta_fwd_bf16_d128", "ta_fwd_f16_d64"):
+        names = ("ta_fwd_pp_bf16_d128", "ta_fwd_pp_f16_d64") if path.name == "attn_fwd_pp.hsaco" \
+            else ("ta_fwd_bf16_d128", "ta_fwd_f16_d64")
+        for name in names:
             assert name.encode() in data

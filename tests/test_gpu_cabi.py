@@ -69,3 +69,8 @@ def test_cabi_bad_device_is_a_hip_error(gpu):
     say("C-ABI invalid device ordinal")
     assert lib.ta_sdpa_fwd(ctypes.byref(a), None) == _lib.TA_EHIP
     assert "device" in _lib.last_error(lib)
+    # The failure is reported through the status only: the next torch launch must not
+    # find it in the runtime's last-error slot.
+    x = torch.ones(4, device="cuda") * 2
+    torch.cuda.synchronize()
+    assert float(x.sum()) == 8.0

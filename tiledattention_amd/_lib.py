@@ -88,7 +88,7 @@ def library_path() -> Path:
 
 def code_object_paths() -> list[Path]:
     d = lib_dir()
-    return [d / f"attn_fwd_m{tm}_n{tn}.hsaco" for tm, tn in TILE_SHAPES]
+    return [d / f"attn_fwd_m{tm}_n{tn}.hsaco" for tm, tn in TILE_SHAPES] + [d / "attn_fwd_pp.hsaco"]
 
 
 def _declare(lib: ctypes.CDLL) -> None:

@@ -35,6 +35,7 @@
 
 #include <type_traits>
 
+#include "attn_fwd_common.h"
 #include "attn_fwd_params.h"
 
 #ifndef TA_TILE_M
@@ -45,89 +46,6 @@
 #endif
 
 namespace ta {
-
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef short s16x4 __attribute__((__vector_size__(4 * sizeof(short))));
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-
-// Initial running max, raw score units (the reference starts from -1e30, flash_fwd.py:14).
-// Finite, so the first rescale factor 2^((m0 - m)*c) is exactly 0 rather than NaN.
-constexpr float kNegLarge = -1.0e30f;
-// Masked scores are -inf: 2^(-inf) = 0 whatever the running max is, and a lane whose keys
-// are all masked keeps max = -inf without ever forming inf - inf against kNegLarge.
-constexpr float kMasked = -__builtin_huge_valf();
-// Lazy-rescale threshold in log2 units: P = 2^(s*c - m*c) stays <= 2^8.
-constexpr float kRescaleLog2 = 8.0f;
-
-template <int DT>
-struct DType;
-
-template <>
-struct DType<0> {  // float16
-  __device__ static inline f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
-                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-  }
-  // Round-to-nearest-even pack of two floats (v_cvt_pk_f16_f32).
-  __device__ static inline uint32_t pack(float a, float b) {
-    f16x2 h = {(_Float16)a, (_Float16)b};
-    return __builtin_bit_cast(uint32_t, h);
-  }
-  __device__ static inline float lo(uint32_t u) {
-    return (float)__builtin_bit_cast(f16x2, u)[0];
-  }
-  __device__ static inline float hi(uint32_t u) {
-    return (float)__builtin_bit_cast(f16x2, u)[1];
-  }
-  __device__ static inline float round(float x) { return (float)(_Float16)x; }
-  // acc + lo(u) + hi(u) in fp32 (v_dot2c_f32_f16 against (1, 1); keeps fp16 subnormals).
-  __device__ static inline float sum2(uint32_t u, float acc) {
-    const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, u), one, acc, false);
-  }
-};
-
-template <>
-struct DType<1> {  // bfloat16
-  __device__ static inline f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
-                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  }
-  // Round-to-nearest-even pack of two floats (v_cvt_pk_bf16_f32).
-  __device__ static inline uint32_t pack(float a, float b) {
-    bf16x2 h = {(__bf16)a, (__bf16)b};
-    return __builtin_bit_cast(uint32_t, h);
-  }
-  __device__ static inline float lo(uint32_t u) { return __uint_as_float(u << 16); }
-  __device__ static inline float hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
-  __device__ static inline float round(float x) { return (float)(__bf16)x; }
-  // acc + lo(u) + hi(u) in fp32 (v_dot2c_f32_bf16 against (1, 1)).
-  __device__ static inline float sum2(uint32_t u, float acc) {
-    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, u), one, acc, false);
-  }
-};
-
-// Symmetric exchange with lane ^ 32: returns (own, partner) in some order; callers only
-// combine the pair with a commutative op.
-__device__ static inline void swap32(float x, float& a, float& b) {
-  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  a = __uint_as_float(r[0]);
-  b = __uint_as_float(r[1]);
-}
-
-__device__ static inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// IEEE 754-2019 maximum (NaN-propagating): lowers to v_maximum3_f32 on gfx950 without the
-// operand canonicalisation fmaxf needs in IEEE mode.
-__device__ static inline float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
-__device__ static inline float vmax3(float a, float b, float c) { return vmax(a, vmax(b, c)); }
 
 // LDS rows are padded so that every LDS address is a per-lane base plus an immediate
 // offset and both read patterns are free of bank conflicts on the 64-bank LDS:
@@ -140,14 +58,6 @@ struct LdsLayout {
   static constexpr int KS = 2 * D + 16;  // K row stride, bytes
   static constexpr int VS = 2 * D + 64;  // V row stride, bytes
 };
-
-// Buffer resource for rows [0, rows) of a row-major tensor with `row_bytes` between rows:
-// loads past the last row return zeros (the hardware range check), which zero-fills the
-// ragged last key tile without any per-lane select.
-__device__ static inline __amdgpu_buffer_rsrc_t row_rsrc(const void* base, int rows, int row_bytes) {
-  const int bytes = rows > 0 ? rows * row_bytes : 0;
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
-}
 
 template <int DT, int D, int TM, int TN, bool CAUSAL, bool TAIL, bool LOWP>
 __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {

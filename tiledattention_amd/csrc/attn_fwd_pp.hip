@@ -1,0 +1,475 @@
+// SDPA forward for CDNA4 (gfx950), fp32 accumulation, 128 query rows per workgroup:
+// eight waves in a barrier-locked ping-pong.
+//
+// Math: the reference's tiled forward with fp32 accumulation
+// (src/tiledattention/kernels/flash_fwd.py:374-446, unmasked form :533-574): per query row
+// keep (m, l, acc), stream key tiles, finish with acc / l.  Schedule and layout are this
+// file's own:
+//
+// * Waves w and w + 4 of the workgroup share a SIMD and the same 32 query rows
+//   (row block w % 4).  The workgroup walks the keys in steps of 128; in each step wave
+//   group 0 (waves 0-3) takes the first 64 keys and group 1 (waves 4-7) the last 64.  Each
+//   wave keeps its own online-softmax state over its keys; the two states of a row block
+//   are merged through LDS at the end (m = max, weights 2^((m_g - m) * c)).
+// * Each wave alternates two clusters: the MFMA cluster (S of the next step,
+//   S^T = K Q^T, and O^T += V^T P^T of the current one) and the VALU cluster (mask, row
+//   max, rescale, exp, pack of P).  Group 1 runs one cluster behind group 0 and every
+//   cluster ends at a workgroup barrier, so on every SIMD one wave issues MFMAs while the
+//   other does the softmax arithmetic of its own step.
+// * K/V go HBM -> LDS directly (buffer loads with the LDS-write form, 16 bytes a lane,
+//   1 KiB a wave instruction), two stages each, with 16-byte chunks XOR-swizzled per row so
+//   the K reads (b128) and the transposed V reads (ds_read_b64_tr_b16) are free of bank
+//   conflicts.  The loads of step u + 1's K and step u's V are issued at the start of
+//   global phase 2u and waited for by the issuing wave before the barrier that ends phase
+//   2u + 1; both land in stages last read in phase 2u - 1.
+// * Operand layouts are those of the 128 x 64 kernel (attn_fwd.hip): scores transposed so
+//   a lane owns one query, row reductions in-lane plus v_permlane32_swap, P packed from the
+//   score registers straight into the B operand of the P.V MFMA, exp2 with scale*log2(e)
+//   folded into one FMA, lazy rescale of O with a 2^8 threshold, l summed from the rounded
+//   P.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "attn_fwd_common.h"
+#include "attn_fwd_params.h"
+
+namespace ta {
+
+// 16-byte chunk swizzle of the unpadded LDS tiles (row = 2D bytes, 64 banks x 4 bytes):
+// * K: a b128 read pass covers 16 consecutive rows at one logical chunk;
+//   physical chunk = logical ^ (row & 15) for D = 128, ^ ((row >> 1) & 7) for D = 64.
+// * V: a b64 transposed read pass covers 4 consecutive rows x 4 logical chunks;
+//   physical chunk = logical ^ 4 * (row & 3) for D = 128, ^ 4 * ((row >> 1) & 1) for D = 64.
+template <int D>
+__device__ static inline int pp_swz_k(int row) {
+  return D == 128 ? (row & 15) : ((row >> 1) & 7);
+}
+template <int D>
+__device__ static inline int pp_swz_v(int row) {
+  return D == 128 ? ((row & 3) << 2) : (((row >> 1) & 1) << 2);
+}
+
+template <int DT, int D, bool CAUSAL, bool TAIL>
+__device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
+  constexpr int TM = 128;            // query rows per workgroup
+  constexpr int TK = 128;            // keys per workgroup step (64 per wave group)
+  constexpr int KB = 2;              // 32-key blocks per wave per step
+  constexpr int DK = D / 16;         // k-steps of the QK^T product
+  constexpr int DB = D / 32;         // 32-wide d blocks of O
+  constexpr int CPR = D / 8;         // 16-byte chunks per row
+  constexpr int RB = 2 * D;          // bytes per LDS row
+  constexpr int STAGE = TK * RB;     // bytes of one K or V stage
+  constexpr int RPL = 1024 / RB;     // rows one wave instruction fills
+  constexpr int NLD = STAGE / 1024 / 8;  // load instructions per wave per tensor per step
+  static_assert(STAGE % (8 * 1024) == 0, "stage must split over the eight waves");
+  using DTy = DType<DT>;
+
+  // One array per (tensor, stage): the stage of every access is a compile-time constant
+  // (the key loop is unrolled by two), so the compiler can tell the loads in flight into
+  // one stage from the reads of the other and does not wait on the former for the latter.
+  __shared__ __attribute__((aligned(1024))) char lds_k0[STAGE];
+  __shared__ __attribute__((aligned(1024))) char lds_k1[STAGE];
+  __shared__ __attribute__((aligned(1024))) char lds_v0[STAGE];
+  __shared__ __attribute__((aligned(1024))) char lds_v1[STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps it in SGPRs
+  const int grp = wave >> 2;  // key half of every step
+  const int wr = wave & 3;    // row block
+  const int l32 = lane & 31;
+  const int hl = lane >> 5;
+
+  // ---- block -> (bh, q tile) ------------------------------------------------------
+  // One workgroup per CU (LDS and registers); the hardware hands block ids to the 8 XCDs
+  // round-robin, so with sched >= 1 consecutive logical tiles are regrouped onto one XCD
+  // (one head's K/V in one L2).  Causal tiles are issued heaviest first: each CU takes the
+  // next tile when its current one ends, which pairs heavy with light tiles.
+  const int nq = p.n_qblk;
+  const int total = nq * p.n_bh;
+  int lin = blockIdx.x;
+  if (p.sched >= 1 && (total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
+  const int bh = lin / nq;
+  const int j = lin - bh * nq;
+  const int qt = CAUSAL ? nq - 1 - j : j;
+  const int b = bh / p.H;
+  const int h = bh - b * p.H;
+  const int S = p.S;
+
+  const uint16_t* __restrict__ qp = p.q + b * p.q_sb + h * p.q_sh;
+  const uint16_t* __restrict__ kp = p.k + b * p.k_sb + h * p.k_sh;
+  const uint16_t* __restrict__ vp = p.v + b * p.v_sb + h * p.v_sh;
+  uint16_t* __restrict__ op = p.o + b * p.o_sb + h * p.o_sh;
+  const int k_rb = (int)p.k_ss * 2;  // global row bytes
+  const int v_rb = (int)p.v_ss * 2;
+
+  const int q0 = qt * TM;
+  const int wq0 = q0 + wr * 32;  // first query row of this wave
+  const int my_q = wq0 + l32;    // this lane's query row
+
+  // ---- Q fragment: B operand of S^T = K Q^T, kept for the whole key loop ------------
+  u32x4 qf[DK];
+  {
+    const bool ok = !TAIL || my_q < S;
+    const uint16_t* row = qp + (int64_t)(ok ? my_q : 0) * p.q_ss;
+#pragma unroll
+    for (int kk = 0; kk < DK; ++kk) {
+      u32x4 v = *(const u32x4*)(row + 16 * kk + 8 * hl);
+      qf[kk] = ok ? v : u32x4{0, 0, 0, 0};
+    }
+  }
+
+  // ---- key range --------------------------------------------------------------------
+  const int kv_end = CAUSAL ? min(S, q0 + TM) : S;
+  const int n_steps = (kv_end + TK - 1) / TK;
+  const int wave_kv_end = CAUSAL ? min(S, wq0 + 32) : S;
+  const int koff = 64 * grp;  // this wave's keys in a step: [TK * t + koff, + 64)
+
+  // ---- staging: HBM -> LDS directly -------------------------------------------------
+  // Wave w fills the 1 KiB chunks g = w + 8 i of a stage: lane l writes physical chunk
+  // l % CPR of row g * RPL + l / CPR, so it loads logical chunk (l % CPR) ^ swz(row) of that
+  // row.  swz depends on g only through g & 3 (K, D = 128) or g & 1 (K, D = 64), both fixed
+  // by w, so one per-lane byte offset (plus i * 8 * RPL rows) serves every load of a tensor.
+  // One buffer resource per step starts at the step's first key; rows past S are outside
+  // it and read as zero.
+  const int ld_row = wave * RPL + lane / CPR;
+  const int ld_pc = lane % CPR;
+  const int kvo = ld_row * k_rb + ((ld_pc ^ pp_swz_k<D>(ld_row)) << 4);
+  const int vvo = ld_row * v_rb + ((ld_pc ^ pp_swz_v<D>(ld_row)) << 4);
+  auto dma = [&](const uint16_t* gbase, int64_t row_stride, int rb, int vo, int t, char* stage) {
+    const int row0 = t * TK;
+    const __amdgpu_buffer_rsrc_t r = row_rsrc(gbase + (int64_t)row0 * row_stride, S - row0, rb);
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          r, (__attribute__((address_space(3))) void*)(stage + (wave + 8 * i) * 1024), 16,
+          vo + i * 8 * RPL * rb, 0, 0, 0);
+    }
+  };
+  // Wait for this wave's direct-to-LDS loads (vmcnt = 0), before the barrier that
+  // publishes them.
+  auto wait_dma = [&]() { __builtin_amdgcn_s_waitcnt(0x0F70); };
+
+  // ---- per-lane LDS read offsets --------------------------------------------------------
+  // K: lane reads row koff + 32 bk + l32 at logical chunk 2 kk + hl; with m = swz_k(l32)
+  // that is byte (koff + l32) * RB + (32 * (m >> 1) + 16 * (hl ^ (m & 1))) ^ (32 kk), plus
+  // 32 * bk * RB.
+  const int mk = pp_swz_k<D>(l32);
+  const int k_rd = (koff + l32) * RB + 32 * (mk >> 1) + 16 * (hl ^ (mk & 1));
+  // V^T via the transposed read: lane l of 16-lane group G addresses row 4 hl + r,
+  // r = (l % 16) / 4, of a 16-key chunk and d = 32 db + 16 (G % 2) + 4 (l % 4); the hardware
+  // hands lane l column 32 db + 16 (G % 2) + l % 16 of those 4 rows.  swz_v depends only on
+  // r, so the byte address is v_rd ^ (64 db), plus (koff + 32 bk + 16 kc) * RB.
+  const int tr_r = (lane & 15) >> 2;
+  const int tr_d = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const int v_rd = (koff + 4 * hl + tr_r) * RB +
+                   16 * ((tr_d >> 3) ^ pp_swz_v<D>(4 * hl + tr_r)) + 2 * (tr_d & 7);
+
+  // ---- running state (lane = query l32 of this wave) ----------------------------------
+  float m_run = kNegLarge;
+  float l_part = 0.0f;
+  f32x16 o_acc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) o_acc[db] = f32x16{};
+  const float c = p.scale_log2;
+
+  // Step t, from this wave's point of view: first key, whether all 32-key blocks hold keys
+  // it needs, and whether no score needs a mask.
+  auto key0 = [&](int t) { return t * TK + koff; };
+  auto all_active = [&](int t) { return key0(t) + 32 * (KB - 1) < wave_kv_end; };
+  auto no_mask = [&](int t) {
+    return (!CAUSAL || key0(t) + 63 <= wq0) && (!TAIL || key0(t) + 64 <= S);
+  };
+
+  f32x16 s[KB];        // S^T blocks of the step whose softmax comes next
+  uint32_t pk[KB][8];  // packed P of the step whose P.V comes next
+
+  // S^T = K Q^T of a step from stage `kst`, every block (blocks holding no key the wave
+  // needs are masked whole by the softmax).
+  auto qk = [&](const char* kst) {
+#pragma unroll
+    for (int kk = 0; kk < DK; ++kk) {
+#pragma unroll
+      for (int bk = 0; bk < KB; ++bk) {
+        const u32x4 a = *(const u32x4*)(kst + bk * 32 * RB + (k_rd ^ (32 * kk)));
+        s[bk] = DTy::mfma(a, qf[kk], kk == 0 ? f32x16{} : s[bk]);
+      }
+    }
+  };
+
+  // O^T += V^T P^T of the step held in pk, from stage `vst`.  Every block: P is exactly 0
+  // for masked keys.
+  auto pv = [&](const char* vst) {
+#pragma unroll
+    for (int bk = 0; bk < KB; ++bk) {
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        const u32x4 bfrag = {pk[bk][4 * kc + 0], pk[bk][4 * kc + 1], pk[bk][4 * kc + 2],
+                             pk[bk][4 * kc + 3]};
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const char* a0p = vst + (v_rd ^ (64 * db)) + (32 * bk + 16 * kc) * RB;
+          s16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)a0p);
+          s16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a0p + 8 * RB));
+          u32x2 w0 = __builtin_bit_cast(u32x2, r0);
+          u32x2 w1 = __builtin_bit_cast(u32x2, r1);
+          const u32x4 a = {w0[0], w0[1], w1[0], w1[1]};
+          o_acc[db] = DTy::mfma(a, bfrag, o_acc[db]);
+        }
+      }
+    }
+  };
+
+  // VALU cluster of step t: mask, row max, rescale, P = 2^(s*c - m*c) packed, l.  One
+  // code path for every step (blocks without a needed key are masked whole), so the
+  // rescale of O exists once and O keeps one register assignment through the loop.
+  auto softmax = [&](int t) {
+    // Blocks past the wave's last key are masked whole by the same test: all their keys
+    // are past the wave's last query (causal) or past S.
+    if (!(no_mask(t) && all_active(t))) {
+#pragma unroll
+      for (int bk = 0; bk < KB; ++bk) {
+        const int kb0 = key0(t) + 32 * bk;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kb0 + (r >> 2) * 8 + hl * 4 + (r & 3);
+          bool bad = false;
+          if (CAUSAL) bad = key > my_q;
+          if (TAIL) bad = bad || key >= S;
+          s[bk][r] = bad ? kMasked : s[bk][r];
+        }
+      }
+    }
+    float mxa = kMasked, mxb = kMasked;
+#pragma unroll
+    for (int bk = 0; bk < KB; ++bk) {
+#pragma unroll
+      for (int r = 0; r < 16; r += 4) {
+        mxa = vmax3(mxa, s[bk][r], s[bk][r + 1]);
+        mxb = vmax3(mxb, s[bk][r + 2], s[bk][r + 3]);
+      }
+    }
+    float mx;
+    {
+      float a0, a1;
+      swap32(vmax(mxa, mxb), a0, a1);
+      mx = vmax(a0, a1);
+    }
+    const bool need = (mx - m_run) * c > kRescaleLog2;
+    if (__ballot(need)) {
+      const float m_new = need ? mx : m_run;
+      const float alpha = fast_exp2((m_run - m_new) * c);
+      m_run = m_new;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) o_acc[db] *= alpha;
+      l_part *= alpha;
+    }
+    const float mc = m_run * c;
+    float la = 0.0f, lb = 0.0f;
+#pragma unroll
+    for (int bk = 0; bk < KB; ++bk) {
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const float p0 = fast_exp2(__builtin_fmaf(s[bk][r], c, -mc));
+        const float p1 = fast_exp2(__builtin_fmaf(s[bk][r + 1], c, -mc));
+        const uint32_t w = DTy::pack(p0, p1);
+        pk[bk][r >> 1] = w;
+        if (r & 2) {
+          lb = DTy::sum2(w, lb);
+        } else {
+          la = DTy::sum2(w, la);
+        }
+      }
+    }
+    l_part += la + lb;
+    // Keep the P computation in this cluster: without a use here the compiler sinks it
+    // past the barrier to its consumers, the P.V MFMAs of the other cluster.
+#pragma unroll
+    for (int bk = 0; bk < KB; ++bk) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(pk[bk][i]));
+    }
+  };
+
+  // Issue order of the MFMA cluster: AHEAD LDS reads first, then each MFMA followed by the
+  // reads of the MFMA AHEAD places later (1 for a K operand, 2 for a transposed V operand).
+  auto mfma_cluster_order = [&]() {
+    constexpr int NQ = KB * DK;      // QK^T MFMAs
+    constexpr int NP = KB * 2 * DB;  // P.V MFMAs
+    constexpr int AHEAD = 4;
+    __builtin_amdgcn_sched_group_barrier(0x100, AHEAD, 0);
+#pragma unroll
+    for (int i = 0; i < NQ - AHEAD; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, AHEAD, 0);
+  };
+
+  // Workgroup barrier without a memory fence: a fence would also wait for this wave's
+  // direct-to-LDS loads, which are meant to stay in flight across the next barrier.  The
+  // wave's LDS accesses are complete first (lgkmcnt = 0); the empty asm statements keep
+  // the compiler from moving memory accesses across the barrier.  Loads into LDS are
+  // waited for explicitly (wait_dma) by the wave that issued them before the barrier that
+  // publishes them.
+  auto barrier = [&]() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  // ---- prologue and key loop ---------------------------------------------------------
+  // Global phases: phase 0 = group 0 computes S_0 (group 1 idles); phase 2t + 1 = group 0's
+  // softmax of step t with group 1's MFMA cluster of step t - 1 (S_0 for t = 0); phase
+  // 2t + 2 = group 0's MFMA cluster of step t (S_{t+1}, P_t.V_t) with group 1's softmax of
+  // step t.  Every phase ends at a workgroup barrier.  The loads of K_{u+1} and V_u start
+  // in phase 2u (group 0 at the start of its MFMA cluster, group 1 at the start of its
+  // softmax) and are waited for by the issuing wave before the barrier that ends phase
+  // 2u + 1; they go to stages last read in phase 2u - 1.  The two groups run separate
+  // copies of the loop so that every wait sits at a fixed place in each copy (the
+  // compiler then sees that no load is in flight into a stage a cluster reads).
+  //
+  // Drain the Q-fragment loads first, on every path into the loop, so the waitcnt
+  // insertion does not carry a pending-load state into the loop.
+  __builtin_amdgcn_s_waitcnt(0);
+  dma(kp, p.k_ss, k_rb, kvo, 0, lds_k0);
+  wait_dma();
+  barrier();
+  if (n_steps > 1) dma(kp, p.k_ss, k_rb, kvo, 1, lds_k1);
+  dma(vp, p.v_ss, v_rb, vvo, 0, lds_v0);
+
+  // Stages of step t with parity PAR: K_t (consumed, receives K_{t+2}), K_{t+1}, V_t, and
+  // the stage receiving V_{t+1}.
+  auto issue = [&](int t, char* k_cur, char* v_nxt) {
+    if (t + 2 < n_steps) dma(kp, p.k_ss, k_rb, kvo, t + 2, k_cur);
+    if (t + 1 < n_steps) dma(vp, p.v_ss, v_rb, vvo, t + 1, v_nxt);
+  };
+  // MFMA cluster of step t: S of step t + 1 (past the last step it reads a stale stage
+  // and is never used) and P.V of step t, one straight-line block whose LDS reads run
+  // AHEAD MFMAs in front of their consumers.
+  auto mfma_cluster = [&](const char* k_nxt, const char* v_cur) {
+    qk(k_nxt);
+    pv(v_cur);
+    mfma_cluster_order();
+  };
+  if (grp == 0) {
+    qk(lds_k0);
+    barrier();
+    auto iter0 = [&](int t, auto par_tag) {
+      constexpr int PAR = decltype(par_tag)::value;
+      char* k_cur = PAR ? lds_k1 : lds_k0;
+      char* k_nxt = PAR ? lds_k0 : lds_k1;
+      char* v_cur = PAR ? lds_v1 : lds_v0;
+      char* v_nxt = PAR ? lds_v0 : lds_v1;
+      softmax(t);
+      wait_dma();
+      barrier();
+      issue(t, k_cur, v_nxt);
+      mfma_cluster(k_nxt, v_cur);
+      barrier();
+    };
+    for (int t = 0; t < n_steps; t += 2) {
+      iter0(t, std::integral_constant<int, 0>{});
+      if (t + 1 < n_steps) iter0(t + 1, std::integral_constant<int, 1>{});
+    }
+    barrier();  // phase 2 n_steps + 1: group 1's last MFMA cluster
+  } else {
+    barrier();  // phase 0: group 0's S_0
+    qk(lds_k0);
+    wait_dma();
+    barrier();
+    auto iter1 = [&](int t, auto par_tag) {
+      constexpr int PAR = decltype(par_tag)::value;
+      char* k_cur = PAR ? lds_k1 : lds_k0;
+      char* k_nxt = PAR ? lds_k0 : lds_k1;
+      char* v_cur = PAR ? lds_v1 : lds_v0;
+      char* v_nxt = PAR ? lds_v0 : lds_v1;
+      issue(t, k_cur, v_nxt);
+      softmax(t);
+      barrier();
+      mfma_cluster(k_nxt, v_cur);
+      wait_dma();
+      barrier();
+    };
+    for (int t = 0; t < n_steps; t += 2) {
+      iter1(t, std::integral_constant<int, 0>{});
+      if (t + 1 < n_steps) iter1(t + 1, std::integral_constant<int, 1>{});
+    }
+  }
+
+  // ---- merge the two key halves of each row block, O = acc / l ---------------------------
+  // Group 1 leaves (m, l, O^T) in LDS (the stages are free: every load has landed and
+  // every read has retired before the last barrier); group 0 merges and writes O.
+  float* xo = (float*)((wr < 2 ? lds_k0 : lds_k1) + (wr & 1) * (STAGE / 2));
+  float* xml = (float*)lds_v0 + wr * 128;
+  static_assert(DB * 16 * 64 * 4 <= STAGE / 2, "merge buffer must fit half a stage");
+  if (grp == 1) {
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) xo[(db * 16 + r) * 64 + lane] = o_acc[db][r];
+    }
+    xml[lane] = m_run;
+    xml[64 + lane] = l_part;
+  }
+  barrier();
+  if (grp == 1) return;
+  const float m1 = xml[lane];
+  const float l1 = xml[64 + lane];
+  const float m = vmax(m_run, m1);
+  const float a0 = fast_exp2((m_run - m) * c);
+  const float a1 = fast_exp2((m1 - m) * c);
+  float la, lb;
+  swap32(l_part * a0 + l1 * a1, la, lb);
+  const float l_tot = la + lb;
+  if (TAIL && my_q >= S) return;
+  const float inv = 1.0f / l_tot;
+  const float w0s = a0 * inv, w1s = a1 * inv;
+  uint16_t* orow = op + (int64_t)my_q * p.o_ss;
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      float o4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 4 * g + e;
+        o4[e] = o_acc[db][r] * w0s + xo[(db * 16 + r) * 64 + lane] * w1s;
+      }
+      const uint32_t w0 = DTy::pack(o4[0], o4[1]);
+      const uint32_t w1 = DTy::pack(o4[2], o4[3]);
+      const int d = 32 * db + 8 * g + 4 * hl;
+      *(u32x2*)(orow + d) = u32x2{w0, w1};
+    }
+  }
+}
+
+}  // namespace ta
+
+// One extern "C" entry per (dtype, D, causal, tail).
+// Name: ta_fwd_pp_<f16|bf16>_d<D>_c<0|1>_t<0|1>; 512 threads, one workgroup per CU.
+#define TA_PP_DEFINE(DTN, DT, D, C, T)                                                    \
+  extern "C" __global__ void __launch_bounds__(512)                                       \
+      __attribute__((amdgpu_waves_per_eu(2, 2))) ta_fwd_pp_##DTN##_d##D##_c##C##_t##T(     \
+          ta::FwdParams p) {                                                              \
+    ta::attn_fwd_pp_body<DT, D, (C != 0), (T != 0)>(p);                                   \
+  }
+
+#define TA_PP_DEFINE_CT(DTN, DT, D) \
+  TA_PP_DEFINE(DTN, DT, D, 0, 0)    \
+  TA_PP_DEFINE(DTN, DT, D, 0, 1)    \
+  TA_PP_DEFINE(DTN, DT, D, 1, 0)    \
+  TA_PP_DEFINE(DTN, DT, D, 1, 1)
+
+TA_PP_DEFINE_CT(f16, 0, 64)
+TA_PP_DEFINE_CT(f16, 0, 128)
+TA_PP_DEFINE_CT(bf16, 1, 64)
+TA_PP_DEFINE_CT(bf16, 1, 128)

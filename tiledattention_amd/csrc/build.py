@@ -5,6 +5,8 @@ Outputs (into ``tiledattention_amd/lib/`` unless told otherwise):
 * ``attn_fwd_m<TM>_n<TN>.hsaco`` for TM, TN in {64, 128}: each holds the 32 kernels of
   one tile shape (dtype x head dim x causal x tail x accumulation), compiled from
   ``attn_fwd.hip`` with ``hipcc --genco --offload-arch=gfx950``;
+* ``attn_fwd_pp.hsaco``: the eight-wave kernels (dtype x head dim x causal x tail) that
+  serve the (128, 64) tile shape with fp32 accumulation, from ``attn_fwd_pp.hip``;
 * ``libtiledattn.so``: the host library implementing ``include/tiledattn.h``.
 
 Run as ``python -m tiledattention_amd.csrc.build``.
@@ -66,6 +68,17 @@ def code_object_cmd(tm: int, tn: int, out_dir: Path) -> list[str]:
     ]
 
 
+def pp_code_object_cmd(out_dir: Path) -> list[str]:
+    return [
+        _hipcc(),
+        *HIP_FLAGS,
+        "--genco",
+        "-o",
+        str(out_dir / "attn_fwd_pp.hsaco"),
+        str(HERE / "attn_fwd_pp.hip"),
+    ]
+
+
 def library_cmd(out_dir: Path) -> list[str]:
     return [
         os.environ.get("CXX", "g++"),
@@ -91,7 +104,8 @@ def build(out_dir: Path | None = None, jobs: int | None = None) -> Path:
     """Compile every code object and the host library; return the output directory."""
     out = Path(out_dir) if out_dir is not None else LIB_DIR
     out.mkdir(parents=True, exist_ok=True)
-    cmds = [code_object_cmd(tm, tn, out) for tm, tn in TILES] + [library_cmd(out)]
+    cmds = [code_object_cmd(tm, tn, out) for tm, tn in TILES]
+    cmds += [pp_code_object_cmd(out), library_cmd(out)]
     workers = jobs or min(len(cmds), max(1, (os.cpu_count() or 2)))
     with cf.ThreadPoolExecutor(max_workers=workers) as pool:
         for fut in [pool.submit(_run, c) for c in cmds]:

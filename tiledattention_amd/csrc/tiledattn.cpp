@@ -3,9 +3,10 @@
 // Replaces the reference's launch boundary (src/tiledattention/kernels/flash_fwd.py:786-818,
 // torch-ext/torch_binding.cpp:6-19, tiledattention_cuda/tiledattention.cu:13-33) and its
 // kernel cache (src/tiledattention/kernels/compile_cache.py:10-37):
-//   * kernels are precompiled per (TILE_M, TILE_N) into gfx950 code objects
-//     attn_fwd_m<TM>_n<TN>.hsaco; one module per (device, TM, TN) is loaded on first use and
-//     kept, and resolved hipFunction_t handles are cached per (device, kernel name);
+//   * kernels are precompiled into gfx950 code objects: attn_fwd_m<TM>_n<TN>.hsaco per tile
+//     shape, and attn_fwd_pp.hsaco with the eight-wave kernels that serve the (128, 64)
+//     shape with fp32 accumulation; one module per (device, file) is loaded on first use
+//     and kept, and resolved hipFunction_t handles are cached per (device, kernel name);
 //   * the cache is guarded by a mutex (the reference's dict is unguarded);
 //   * launches go to the caller's stream under a device guard, like the reference's torch op
 //     (OptionalCUDAGuard + current stream, tiledattention.cu:29-31).
@@ -18,7 +19,6 @@
 #include <map>
 #include <mutex>
 #include <string>
-#include <tuple>
 
 #include "../../include/tiledattn.h"
 #include "attn_fwd_params.h"
@@ -27,7 +27,12 @@ namespace {
 
 thread_local std::string g_last_error;
 
+// Records the error text for ta_last_error().  A failed HIP call also leaves its code in
+// the runtime's per-thread last-error slot, where the caller's next error check (torch
+// checks after every kernel launch) would pick it up as its own; the status returned here
+// reports it instead, so the slot is cleared.
 ta_status fail(ta_status st, const char* fmt, ...) {
+  if (st == TA_EHIP || st == TA_ENOKERNEL) (void)hipGetLastError();
   char buf[512];
   va_list ap;
   va_start(ap, fmt);
@@ -39,7 +44,7 @@ ta_status fail(ta_status st, const char* fmt, ...) {
 
 std::mutex g_mu;
 std::string g_dir;   // code object directory; empty = next to this library
-std::map<std::tuple<int, int, int>, hipModule_t> g_modules;   // (device, tm, tn)
+std::map<std::pair<int, std::string>, hipModule_t> g_modules;  // (device, code object file)
 std::map<std::pair<int, std::string>, hipFunction_t> g_funcs;  // (device, kernel name)
 std::map<int, bool> g_arch_ok;                                 // device -> gfx950?
 
@@ -71,11 +76,27 @@ struct DeviceGuard {
   }
 };
 
-std::string kernel_name(int dtype, int d, int tm, int tn, int causal, int tail, int accum) {
+// Which kernel serves a launch: code object file, symbol and workgroup size.
+struct KernelId {
+  std::string file;
+  std::string name;
+  unsigned block;
+};
+
+KernelId kernel_id(int dtype, int d, int tm, int tn, int causal, int tail, int accum) {
+  const char* dt = dtype == TA_BF16 ? "bf16" : "f16";
   char buf[96];
-  snprintf(buf, sizeof(buf), "ta_fwd_%s_d%d_m%d_n%d_c%d_t%d_a%d", dtype == TA_BF16 ? "bf16" : "f16",
-           d, tm, tn, causal ? 1 : 0, tail ? 1 : 0, accum ? 1 : 0);
-  return buf;
+  if (tm == 128 && tn == 64 && accum == TA_ACC_FP32) {
+    // Eight waves: two per SIMD sharing the rows of a 32-row block, splitting every
+    // 128-key step between them (attn_fwd_pp.hip).
+    snprintf(buf, sizeof(buf), "ta_fwd_pp_%s_d%d_c%d_t%d", dt, d, causal ? 1 : 0, tail ? 1 : 0);
+    return {"attn_fwd_pp.hsaco", buf, 512u};
+  }
+  snprintf(buf, sizeof(buf), "ta_fwd_%s_d%d_m%d_n%d_c%d_t%d_a%d", dt, d, tm, tn, causal ? 1 : 0,
+           tail ? 1 : 0, accum ? 1 : 0);
+  char file[64];
+  snprintf(file, sizeof(file), "attn_fwd_m%d_n%d.hsaco", tm, tn);
+  return {file, buf, static_cast<unsigned>(tm * 2)};  // tm / 32 waves of 64
 }
 
 bool valid_tile(int t) { return t == 64 || t == 128; }
@@ -100,10 +121,8 @@ ta_status check_arch_locked(int device) {
 }
 
 // Caller holds g_mu and has made `device` current.
-ta_status get_function_locked(int device, int dtype, int d, int tm, int tn, int causal, int tail,
-                              int accum, hipFunction_t* out) {
-  std::string name = kernel_name(dtype, d, tm, tn, causal, tail, accum);
-  auto fk = std::make_pair(device, name);
+ta_status get_function_locked(int device, const KernelId& id, hipFunction_t* out) {
+  auto fk = std::make_pair(device, id.name);
   auto fit = g_funcs.find(fk);
   if (fit != g_funcs.end()) {
     *out = fit->second;
@@ -111,24 +130,23 @@ ta_status get_function_locked(int device, int dtype, int d, int tm, int tn, int 
   }
   ta_status st = check_arch_locked(device);
   if (st != TA_OK) return st;
-  auto mk = std::make_tuple(device, tm, tn);
+  auto mk = std::make_pair(device, id.file);
   hipModule_t mod = nullptr;
   auto mit = g_modules.find(mk);
   if (mit == g_modules.end()) {
-    std::string dir = g_dir.empty() ? default_dir() : g_dir;
-    char path[1024];
-    snprintf(path, sizeof(path), "%s/attn_fwd_m%d_n%d.hsaco", dir.c_str(), tm, tn);
-    hipError_t e = hipModuleLoad(&mod, path);
+    std::string path = (g_dir.empty() ? default_dir() : g_dir) + "/" + id.file;
+    hipError_t e = hipModuleLoad(&mod, path.c_str());
     if (e != hipSuccess)
-      return fail(TA_ENOKERNEL, "hipModuleLoad(%s): %s", path, hipGetErrorString(e));
+      return fail(TA_ENOKERNEL, "hipModuleLoad(%s): %s", path.c_str(), hipGetErrorString(e));
     g_modules[mk] = mod;
   } else {
     mod = mit->second;
   }
   hipFunction_t fn = nullptr;
-  hipError_t e = hipModuleGetFunction(&fn, mod, name.c_str());
+  hipError_t e = hipModuleGetFunction(&fn, mod, id.name.c_str());
   if (e != hipSuccess)
-    return fail(TA_ENOKERNEL, "hipModuleGetFunction(%s): %s", name.c_str(), hipGetErrorString(e));
+    return fail(TA_ENOKERNEL, "hipModuleGetFunction(%s): %s", id.name.c_str(),
+                hipGetErrorString(e));
   g_funcs[fk] = fn;
   *out = fn;
   return TA_OK;
@@ -195,8 +213,8 @@ ta_status ta_prepare(int32_t device, int32_t dtype, int32_t head_dim, int32_t ti
   if (guard.err != hipSuccess)
     return fail(TA_EHIP, "set device %d: %s", device, hipGetErrorString(guard.err));
   hipFunction_t fn;
-  return get_function_locked(device, dtype, head_dim, tile_m, tile_n, causal != 0, aligned == 0,
-                             accum, &fn);
+  return get_function_locked(
+      device, kernel_id(dtype, head_dim, tile_m, tile_n, causal != 0, aligned == 0, accum), &fn);
 }
 
 ta_status ta_sdpa_fwd(const ta_fwd_args* a, void* stream) {
@@ -235,14 +253,15 @@ ta_status ta_sdpa_fwd(const ta_fwd_args* a, void* stream) {
     return fail(TA_EINVAL, "grid too large (B*H*ceil(S/TM) must fit in int32)");
 
   const bool aligned = (a->S % a->tile_m == 0) && (a->S % a->tile_n == 0);
+  const KernelId id =
+      kernel_id(a->dtype, (int)a->D, a->tile_m, a->tile_n, a->causal, !aligned, a->accum);
   hipFunction_t fn = nullptr;
   {
     std::lock_guard<std::mutex> lock(g_mu);
     DeviceGuard guard(a->device);
     if (guard.err != hipSuccess)
       return fail(TA_EHIP, "set device %d: %s", a->device, hipGetErrorString(guard.err));
-    ta_status s = get_function_locked(a->device, a->dtype, (int)a->D, a->tile_m, a->tile_n,
-                                      a->causal, !aligned, a->accum, &fn);
+    ta_status s = get_function_locked(a->device, id, &fn);
     if (s != TA_OK) return s;
   }
 
@@ -267,8 +286,7 @@ ta_status ta_sdpa_fwd(const ta_fwd_args* a, void* stream) {
     return fail(TA_EHIP, "set device %d: %s", a->device, hipGetErrorString(guard.err));
   void* params[] = {&p};
   const unsigned grid = static_cast<unsigned>(n_bh * n_qblk);
-  const unsigned block = static_cast<unsigned>(a->tile_m * 2);  // tile_m / 32 waves of 64
-  hipError_t e = hipModuleLaunchKernel(fn, grid, 1, 1, block, 1, 1, 0,
+  hipError_t e = hipModuleLaunchKernel(fn, grid, 1, 1, id.block, 1, 1, 0,
                                        static_cast<hipStream_t>(stream), params, nullptr);
   if (e != hipSuccess) return fail(TA_EHIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
   return TA_OK;
