@@ -19,9 +19,9 @@
 // * K/V go HBM -> LDS directly (buffer loads with the LDS-write form, 16 bytes a lane,
 //   1 KiB a wave instruction), two stages each, with 16-byte chunks XOR-swizzled per row so
 //   the K reads (b128) and the transposed V reads (ds_read_b64_tr_b16) are free of bank
-//   conflicts.  The loads of step u + 1's K and step u's V are issued at the start of
-//   global phase 2u and waited for by the issuing wave before the barrier that ends phase
-//   2u + 1; both land in stages last read in phase 2u - 1.
+//   conflicts.  Each wave group loads and reads only its own 64-key halves of the stages;
+//   a group's loads for the next step but one are spread over its MFMA cluster and waited
+//   for at the end of its next softmax cluster.
 // * Operand layouts are those of the 128 x 64 kernel (attn_fwd.hip): scores transposed so
 //   a lane owns one query, row reductions in-lane plus v_permlane32_swap, P packed from the
 //   score registers straight into the B operand of the P.V MFMA, exp2 with scale*log2(e)
@@ -34,6 +34,7 @@
 
 #include "attn_fwd_common.h"
 #include "attn_fwd_params.h"
+
 
 namespace ta {
 
@@ -62,7 +63,7 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   constexpr int RB = 2 * D;          // bytes per LDS row
   constexpr int STAGE = TK * RB;     // bytes of one K or V stage
   constexpr int RPL = 1024 / RB;     // rows one wave instruction fills
-  constexpr int NLD = STAGE / 1024 / 8;  // load instructions per wave per tensor per step
+  constexpr int NLD = STAGE / 1024 / 8;  // loads per wave per tensor per step (own half)
   static_assert(STAGE % (8 * 1024) == 0, "stage must split over the eight waves");
   using DTy = DType<DT>;
 
@@ -128,28 +129,33 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   const int koff = 64 * grp;  // this wave's keys in a step: [TK * t + koff, + 64)
 
   // ---- staging: HBM -> LDS directly -------------------------------------------------
-  // Wave w fills the 1 KiB chunks g = w + 8 i of a stage: lane l writes physical chunk
-  // l % CPR of row g * RPL + l / CPR, so it loads logical chunk (l % CPR) ^ swz(row) of that
-  // row.  swz depends on g only through g & 3 (K, D = 128) or g & 1 (K, D = 64), both fixed
-  // by w, so one per-lane byte offset (plus i * 8 * RPL rows) serves every load of a tensor.
-  // One buffer resource per step starts at the step's first key; rows past S are outside
-  // it and read as zero.
-  const int ld_row = wave * RPL + lane / CPR;
+  // A stage is 1 KiB chunks g; lane l of the wave instruction that fills chunk g writes
+  // physical chunk l % CPR of row g * RPL + l / CPR, so it loads logical chunk
+  // (l % CPR) ^ swz(row) of that row.  Each wave group reads only its own half of a stage
+  // (rows koff .. koff + 63) and loads it itself: wave (grp, wr) fills the chunks
+  // g = 64 grp / RPL + wr + 4 i.  swz depends on g only through g & 3 (K, D = 128) or g & 1
+  // (K, D = 64), fixed by wr, so one per-lane byte offset plus 4 i RPL rows serves every
+  // load of a tensor.  One buffer resource per step starts at the step's first key; rows
+  // past S are outside it and read as zero, and a step past the last gets an empty
+  // resource (its loads write zeros into a stage half nobody reads any more).
+  const int ld_g0 = koff / RPL + wr;  // first chunk this wave fills
+  const int ld_row = ld_g0 * RPL + lane / CPR;
   const int ld_pc = lane % CPR;
   const int kvo = ld_row * k_rb + ((ld_pc ^ pp_swz_k<D>(ld_row)) << 4);
   const int vvo = ld_row * v_rb + ((ld_pc ^ pp_swz_v<D>(ld_row)) << 4);
   auto dma = [&](const uint16_t* gbase, int64_t row_stride, int rb, int vo, int t, char* stage) {
     const int row0 = t * TK;
-    const __amdgpu_buffer_rsrc_t r = row_rsrc(gbase + (int64_t)row0 * row_stride, S - row0, rb);
+    const int rows = t < n_steps ? S - row0 : 0;
+    const __amdgpu_buffer_rsrc_t r = row_rsrc(gbase + (int64_t)row0 * row_stride, rows, rb);
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          r, (__attribute__((address_space(3))) void*)(stage + (wave + 8 * i) * 1024), 16,
-          vo + i * 8 * RPL * rb, 0, 0, 0);
+          r, (__attribute__((address_space(3))) void*)(stage + (ld_g0 + 4 * i) * 1024), 16,
+          vo + i * 4 * RPL * rb, 0, 0, 0);
     }
   };
-  // Wait for this wave's direct-to-LDS loads (vmcnt = 0), before the barrier that
-  // publishes them.
+  // Wait for this wave's direct-to-LDS loads (vmcnt = 0; expcnt and lgkmcnt left at their
+  // maxima) before the barrier that publishes them to the rest of its group.
   auto wait_dma = [&]() { __builtin_amdgcn_s_waitcnt(0x0F70); };
 
   // ---- per-lane LDS read offsets --------------------------------------------------------
@@ -294,23 +300,25 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   };
 
   // Issue order of the MFMA cluster: AHEAD LDS reads first, then each MFMA followed by the
-  // reads of the MFMA AHEAD places later (1 for a K operand, 2 for a transposed V operand).
-  auto mfma_cluster_order = [&]() {
+  // reads of the MFMA AHEAD places later (1 for a K operand, 2 for a transposed V operand)
+  // and, on every (NQ + NP) / nv-th MFMA, one of the cluster's nv loads into LDS.
+  auto mfma_cluster_order = [&](int nv) {
     constexpr int NQ = KB * DK;      // QK^T MFMAs
     constexpr int NP = KB * 2 * DB;  // P.V MFMAs
     constexpr int AHEAD = 4;
+    const int every = nv ? (NQ + NP) / nv : 0;
     __builtin_amdgcn_sched_group_barrier(0x100, AHEAD, 0);
 #pragma unroll
-    for (int i = 0; i < NQ - AHEAD; ++i) {
+    for (int i = 0; i < NQ + NP; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      const int j = i + AHEAD;  // MFMA whose operands are read now
+      if (j < NQ) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      } else if (j < NQ + NP) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+      if (every && i % every == 0) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
     }
-#pragma unroll
-    for (int i = 0; i < NP; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, AHEAD, 0);
   };
 
   // Workgroup barrier without a memory fence: a fence would also wait for this wave's
@@ -330,12 +338,13 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   // Global phases: phase 0 = group 0 computes S_0 (group 1 idles); phase 2t + 1 = group 0's
   // softmax of step t with group 1's MFMA cluster of step t - 1 (S_0 for t = 0); phase
   // 2t + 2 = group 0's MFMA cluster of step t (S_{t+1}, P_t.V_t) with group 1's softmax of
-  // step t.  Every phase ends at a workgroup barrier.  The loads of K_{u+1} and V_u start
-  // in phase 2u (group 0 at the start of its MFMA cluster, group 1 at the start of its
-  // softmax) and are waited for by the issuing wave before the barrier that ends phase
-  // 2u + 1; they go to stages last read in phase 2u - 1.  The two groups run separate
-  // copies of the loop so that every wait sits at a fixed place in each copy (the
-  // compiler then sees that no load is in flight into a stage a cluster reads).
+  // step t.  Every phase ends at a workgroup barrier.
+  //
+  // A group reads only its own halves of the stages: its half of K_u in the MFMA cluster of
+  // step u - 1 and its half of V_u in the MFMA cluster of step u.  It loads its halves of
+  // K_{t+2} and V_{t+1} during its MFMA cluster of step t (into the halves that cluster's
+  // predecessor read last) and waits for them at the end of its next softmax cluster.
+  // Both groups run the same sequence, group 1 one phase later.
   //
   // Drain the Q-fragment loads first, on every path into the loop, so the waitcnt
   // insertion does not carry a pending-load state into the loop.
@@ -343,67 +352,58 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   dma(kp, p.k_ss, k_rb, kvo, 0, lds_k0);
   wait_dma();
   barrier();
-  if (n_steps > 1) dma(kp, p.k_ss, k_rb, kvo, 1, lds_k1);
-  dma(vp, p.v_ss, v_rb, vvo, 0, lds_v0);
-
-  // Stages of step t with parity PAR: K_t (consumed, receives K_{t+2}), K_{t+1}, V_t, and
-  // the stage receiving V_{t+1}.
-  auto issue = [&](int t, char* k_cur, char* v_nxt) {
-    if (t + 2 < n_steps) dma(kp, p.k_ss, k_rb, kvo, t + 2, k_cur);
-    if (t + 1 < n_steps) dma(vp, p.v_ss, v_rb, vvo, t + 1, v_nxt);
+  // S_0, then this group's halves of K_1 and V_0 (waited for at the end of its first
+  // softmax cluster, like the loads of every MFMA cluster).
+  auto first = [&]() {
+    qk(lds_k0);
+    dma(kp, p.k_ss, k_rb, kvo, 1, lds_k1);
+    dma(vp, p.v_ss, v_rb, vvo, 0, lds_v0);
   };
-  // MFMA cluster of step t: S of step t + 1 (past the last step it reads a stale stage
-  // and is never used) and P.V of step t, one straight-line block whose LDS reads run
-  // AHEAD MFMAs in front of their consumers.
-  auto mfma_cluster = [&](const char* k_nxt, const char* v_cur) {
+
+  // Step t with stage parity PAR: the stages of K_t (consumed; receives K_{t+2}), K_{t+1},
+  // V_t and V_{t-1} (consumed; receives V_{t+1}).
+  auto iter = [&](int t, auto par_tag) {
+    constexpr int PAR = decltype(par_tag)::value;
+    char* k_cur = PAR ? lds_k1 : lds_k0;
+    char* k_nxt = PAR ? lds_k0 : lds_k1;
+    char* v_cur = PAR ? lds_v1 : lds_v0;
+    char* v_nxt = PAR ? lds_v0 : lds_v1;
+    softmax(t);
+    wait_dma();  // this group's halves of K_{t+1} and V_t (issued one MFMA cluster ago)
+    barrier();
+    // MFMA cluster at raised priority, so that the softmax wave on the same SIMD does not
+    // delay its issue: S of step t + 1 (past the last step it reads a stale or zero stage
+    // and is never used) and P.V of step t, one straight-line block whose LDS reads run
+    // AHEAD MFMAs in front of their consumers, with this wave's loads of K_{t+2} and
+    // V_{t+1} spread over it.
+    __builtin_amdgcn_s_setprio(1);
     qk(k_nxt);
     pv(v_cur);
-    mfma_cluster_order();
+    dma(kp, p.k_ss, k_rb, kvo, t + 2, k_cur);
+    dma(vp, p.v_ss, v_rb, vvo, t + 1, v_nxt);
+    mfma_cluster_order(2 * NLD);
+    __builtin_amdgcn_s_setprio(0);
+    barrier();
   };
   if (grp == 0) {
-    qk(lds_k0);
+    first();
     barrier();
-    auto iter0 = [&](int t, auto par_tag) {
-      constexpr int PAR = decltype(par_tag)::value;
-      char* k_cur = PAR ? lds_k1 : lds_k0;
-      char* k_nxt = PAR ? lds_k0 : lds_k1;
-      char* v_cur = PAR ? lds_v1 : lds_v0;
-      char* v_nxt = PAR ? lds_v0 : lds_v1;
-      softmax(t);
-      wait_dma();
-      barrier();
-      issue(t, k_cur, v_nxt);
-      mfma_cluster(k_nxt, v_cur);
-      barrier();
-    };
     for (int t = 0; t < n_steps; t += 2) {
-      iter0(t, std::integral_constant<int, 0>{});
-      if (t + 1 < n_steps) iter0(t + 1, std::integral_constant<int, 1>{});
+      iter(t, std::integral_constant<int, 0>{});
+      if (t + 1 < n_steps) iter(t + 1, std::integral_constant<int, 1>{});
     }
     barrier();  // phase 2 n_steps + 1: group 1's last MFMA cluster
   } else {
     barrier();  // phase 0: group 0's S_0
-    qk(lds_k0);
-    wait_dma();
+    first();
     barrier();
-    auto iter1 = [&](int t, auto par_tag) {
-      constexpr int PAR = decltype(par_tag)::value;
-      char* k_cur = PAR ? lds_k1 : lds_k0;
-      char* k_nxt = PAR ? lds_k0 : lds_k1;
-      char* v_cur = PAR ? lds_v1 : lds_v0;
-      char* v_nxt = PAR ? lds_v0 : lds_v1;
-      issue(t, k_cur, v_nxt);
-      softmax(t);
-      barrier();
-      mfma_cluster(k_nxt, v_cur);
-      wait_dma();
-      barrier();
-    };
     for (int t = 0; t < n_steps; t += 2) {
-      iter1(t, std::integral_constant<int, 0>{});
-      if (t + 1 < n_steps) iter1(t + 1, std::integral_constant<int, 1>{});
+      iter(t, std::integral_constant<int, 0>{});
+      if (t + 1 < n_steps) iter(t + 1, std::integral_constant<int, 1>{});
     }
   }
+  wait_dma();  // the zero-filling loads of the last two steps, before the merge reuses LDS
+  barrier();
 
   // ---- merge the two key halves of each row block, O = acc / l ---------------------------
   // Group 1 leaves (m, l, O^T) in LDS (the stages are free: every load has landed and
