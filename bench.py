@@ -133,7 +133,7 @@ def main() -> int:
     import torch
 
     from oracle import oracle as O
-    from tiledattention_amd import sdpa
+    from tiledattention_amd import _lib, sdpa
     from tiledattention_amd.kernels import flash_fwd
 
     dev = torch.device("cuda:0")
@@ -160,12 +160,19 @@ def main() -> int:
     _log(f"ms/step {ms_step:.4f}  kernel mean {kern_ms:.4f} ms (median {statistics.median(per):.4f})  "
          f"{value:.1f} TFLOP/s  kernel {achieved:.1f} TFLOP/s ({achieved / PEAK_TFLOPS:.1%} of peak)")
 
+    # The kernel this configuration launches (the C ABI's choice, mirrored in _lib); the
+    # committed HBM-traffic figure is used only if it was measured on that kernel.
+    tm, tn = flash_fwd._default_tile_config_for_shape_gfx950(seq_len=s, head_dim=d, causal=causal)
+    _, kernel = _lib.kernel_symbol(dtype=_lib.TA_BF16, head_dim=d, tile_m=tm, tile_n=tn,
+                                   causal=causal, tail=(s % tm != 0 or s % tn != 0),
+                                   accum=_lib.TA_ACC_FP32)
     traffic = None
     tp = Path(args.traffic_json)
     if tp.exists():
         try:
             rec = json.loads(tp.read_text()).get(f"c3_s{s}")
-            traffic = rec["hbm_bytes_per_launch"] if rec else None
+            if rec and rec.get("kernel") == kernel:
+                traffic = rec["hbm_bytes_per_launch"]
         except (ValueError, KeyError, TypeError):
             traffic = None
 
@@ -187,7 +194,6 @@ def main() -> int:
             _log(f"sweep S={ss}: {sweep[str(ss)]}")
             del qs, ks, vs
 
-    tm, tn = flash_fwd._default_tile_config_for_shape_gfx950(seq_len=s, head_dim=d, causal=causal)
     line = {
         "metric": "SDPA fwd TFLOP/s vs seq len (fp16/bf16, D=64/128) + % of MI355X MFMA peak",
         "value": round(value, 2),
@@ -204,7 +210,7 @@ def main() -> int:
         "config": {
             "workload": f"C3: sdpa fwd B={b} H={h} S={s} D={d} bf16 causal, seed {seed}",
             "B": b, "H": h, "S": s, "D": d, "causal": causal,
-            "tile_m": tm, "tile_n": tn, "accum": "fp32",
+            "tile_m": tm, "tile_n": tn, "accum": "fp32", "kernel": kernel,
             "flops_per_step": flops,
             "reference_value_gb10": REFERENCE_GB10_C3_S8192 if s == 8192 else None,
         },

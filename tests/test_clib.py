@@ -138,3 +138,18 @@ def test_code_objects_built_for_gfx950():
             else ("ta_fwd_bf16_d128", "ta_fwd_f16_d64")
         for name in names:
             assert name.encode() in data
+
+
+@pytest.mark.parametrize("tiles", _lib.TILE_SHAPES)
+@pytest.mark.parametrize("accum", [_lib.TA_ACC_FP32, _lib.TA_ACC_INPUT])
+def test_kernel_symbol_names_exist_in_code_objects(tiles, accum):
+    """The Python mirror of the C ABI's kernel choice names symbols the code objects hold."""
+    for dtype in (_lib.TA_FP16, _lib.TA_BF16):
+        for d in (64, 128):
+            for causal in (False, True):
+                for tail in (False, True):
+                    f, sym = _lib.kernel_symbol(dtype=dtype, head_dim=d, tile_m=tiles[0],
+                                                tile_n=tiles[1], causal=causal, tail=tail,
+                                                accum=accum)
+                    data = (_lib.lib_dir() / f).read_bytes()
+                    assert sym.encode() + b"\x00" in data, (f, sym)

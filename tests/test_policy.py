@@ -10,6 +10,7 @@ from __future__ import annotations
 import pytest
 
 from tiledattention_amd._errors import DTypeNotSupportedError, InvalidShapeError
+from tiledattention_amd import _lib
 from tiledattention_amd.kernels import flash_fwd as ff
 
 
@@ -217,16 +218,20 @@ def test_dtype_codes():
 
 
 # ---------------------------------------------------------------- workgroup order (this build)
-@pytest.mark.parametrize("n,causal,tiles,expected", [
-    (512, True, (128, 64), 2),    # C3 S=8192: all 512 workgroups resident (2 per CU)
-    (1024, True, (128, 64), 1),   # C5: two rounds -> heavy first
-    (256, True, (128, 128), 2),
-    (512, True, (128, 128), 1),
-    (512, False, (128, 64), 1),
-    (12, True, (128, 64), 0),     # does not split over the 8 XCDs
+@pytest.mark.parametrize("n,causal,tiles,accum,expected", [
+    (512, True, (128, 64), "fp32", 1),   # C3 S=8192: eight-wave kernel, one per CU -> heavy first
+    (256, True, (128, 64), "fp32", 2),   # every workgroup resident
+    (512, True, (128, 64), "input", 2),  # four-wave kernel: all 512 resident (2 per CU)
+    (1024, True, (128, 64), "input", 1),
+    (256, True, (128, 128), "fp32", 2),
+    (512, True, (128, 128), "fp32", 1),
+    (512, False, (128, 64), "fp32", 1),
+    (12, True, (128, 64), "fp32", 0),    # does not split over the 8 XCDs
 ])
-def test_sched_default(n, causal, tiles, expected):
-    assert ff._resolve_sched(n_blocks=n, causal=causal, tile_m=tiles[0], tile_n=tiles[1]) == expected
+def test_sched_default(n, causal, tiles, accum, expected):
+    code = _lib.TA_ACC_FP32 if accum == "fp32" else _lib.TA_ACC_INPUT
+    assert ff._resolve_sched(n_blocks=n, causal=causal, tile_m=tiles[0], tile_n=tiles[1],
+                             accum_code=code) == expected
 
 
 def test_sched_env(monkeypatch):

@@ -221,8 +221,9 @@ def _default_tile_config_for_shape(*, seq_len: int, head_dim: int, causal: bool)
 def _default_tile_config_for_shape_gfx950(*, seq_len: int, head_dim: int, causal: bool) -> tuple[int, int]:
     """Default (TILE_M, TILE_N) on gfx950 when neither env knob is set.
 
-    128 query rows (4 waves) per workgroup and 64-key tiles: two workgroups fit on a CU
-    (64 KiB of LDS each at D = 128) and the K/V staging fits in registers.
+    128 query rows per workgroup.  With fp32 accumulation this shape runs the eight-wave
+    kernel (two waves per SIMD splitting every 128-key step, one workgroup per CU); with
+    input-dtype accumulation the four-wave kernel with 64-key tiles (two workgroups per CU).
     """
     del seq_len, head_dim, causal
     return 128, 64
@@ -241,16 +242,26 @@ def _resolve_sync_mode() -> str:
 _CU_COUNT = 256  # MI355X
 
 
-def _resolve_sched(*, n_blocks: int, causal: bool, tile_m: int, tile_n: int) -> int:
-    """Workgroup order.  XCD grouping needs the grid to split evenly over the 8 XCDs; the
-    complementary causal order pays off only when every workgroup is resident at once
-    (two per CU for the 128x64 tile, one otherwise), because it relies on which
-    workgroups share a CU."""
+def _workgroups_per_cu(*, tile_m: int, tile_n: int, accum_code: int) -> int:
+    """Workgroups of one launch resident on a CU at once: two for the four-wave 128x64
+    kernel (input-dtype accumulation), one otherwise (the eight-wave 128x64 kernel and the
+    other tile shapes fill a CU's LDS or registers)."""
+    if (tile_m, tile_n) == (128, 64) and accum_code == _lib.TA_ACC_INPUT:
+        return 2
+    return 1
+
+
+def _resolve_sched(*, n_blocks: int, causal: bool, tile_m: int, tile_n: int,
+                   accum_code: int = _lib.TA_ACC_FP32) -> int:
+    """Workgroup order.  XCD grouping needs the grid to split evenly over the 8 XCDs.  Causal
+    tiles go heaviest first (each CU takes the next tile as its last one ends, pairing heavy
+    with light ones); when every workgroup is resident at once there is no "next", and the
+    complementary order (sched 2) places heavy and light tiles on the same CU instead."""
     raw = os.getenv("TILEDATTN_SCHED", "").strip()
     if raw == "":
         if n_blocks % 8 != 0:
             return 0
-        resident = _CU_COUNT * (2 if (tile_m, tile_n) == (128, 64) else 1)
+        resident = _CU_COUNT * _workgroups_per_cu(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code)
         return 2 if causal and n_blocks <= resident else 1
     if raw not in {"0", "1", "2"}:
         raise ValueError(f"Unsupported TILEDATTN_SCHED={raw!r}. Use 0, 1 or 2.")
@@ -398,7 +409,8 @@ def run_flash_fwd(
     args.tile_m, args.tile_n = tile_m, tile_n
     args.accum = accum_code
     args.device = device_index
-    args.sched = _resolve_sched(n_blocks=bh * n_qblk, causal=causal, tile_m=tile_m, tile_n=tile_n)
+    args.sched = _resolve_sched(n_blocks=bh * n_qblk, causal=causal, tile_m=tile_m, tile_n=tile_n,
+                                accum_code=accum_code)
 
     stream = torch_mod.cuda.current_stream(device)
     if sync_mode == "strict":
