@@ -52,7 +52,8 @@ typedef struct ta_fwd_args {
   const void* k;
   const void* v;
   void* o;
-  int64_t B, H, S, D; /* D must be 64 or 128 (callers zero-pad other head dims) */
+  int64_t B, H, S, D; /* D: 64, 128, 160 or 256 (callers zero-pad other head dims);
+                         160 and 256 need tile_n = 64 */
   int64_t q_stride[4]; /* element strides for (B,H,S,D); stride[3] must be 1 */
   int64_t k_stride[4];
   int64_t v_stride[4];

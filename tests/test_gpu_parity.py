@@ -141,6 +141,45 @@ def test_head_dim_padding(gpu, d):
         check_close(as_f32(out), oracle_f32(q, k, v, causal=causal), "float16", what=f"pad D={d}")
 
 
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("d", [160, 256])
+@pytest.mark.parametrize("tiles", [(None, None), (64, 64), (128, 64)])
+def test_wide_head_dims(gpu, dtype, d, tiles):
+    """Native D = 160 / 256 kernels (64-key tiles), causal and not, a ragged length."""
+    q, k, v = inputs((1, 2, 300, d), dtype, 1000 + d)
+    tm, tn = tiles
+    for causal in (False, True):
+        say(f"wide D={d} {dtype} (1,2,300,{d}) causal={causal} tiles=({tm},{tn})")
+        out = run_gpu(q, k, v, causal=causal, tile_m=tm, tile_n=tn)
+        assert out.shape == (1, 2, 300, d)
+        check_close(as_f32(out), oracle_f32(q, k, v, causal=causal), dtype, what=f"D={d}")
+
+
+@pytest.mark.parametrize("d", [144, 200])
+def test_wide_head_dim_padding(gpu, d):
+    """D in (128, 256] outside {160, 256}: padded to the next wide kernel."""
+    q, k, v = inputs((2, 1, 257, d), "bfloat16", 2000 + d)
+    for causal in (False, True):
+        say(f"wide pad bf16 (2,1,257,{d}) causal={causal}")
+        out = run_gpu(q, k, v, causal=causal)
+        check_close(as_f32(out), oracle_f32(q, k, v, causal=causal), "bfloat16", what=f"pad D={d}")
+
+
+def test_wide_head_dim_input_dtype_accumulation(gpu):
+    q, k, v = inputs((1, 2, 256, 160), "float16", 3160)
+    say("wide D=160 fp16 accumulation (1,2,256,160) causal")
+    out = run_gpu(q, k, v, causal=True, accum_mode="fp16")
+    check_close(as_f32(out), oracle_f32(q, k, v, causal=True), "float16", tol=LOWP_TOL["float16"],
+                what="D=160 fp16 accum")
+
+
+def test_wide_head_dim_rejects_128_key_tiles(gpu):
+    q, k, v = inputs((1, 1, 64, 160), "float16", 5)
+    say("wide D=160 with TILE_N=128 -> ValueError before launch")
+    with pytest.raises(ValueError, match="TILE_N=128"):
+        run_gpu(q, k, v, causal=False, tile_m=64, tile_n=128)
+
+
 def test_chunked_head_dim_knob_matches_unchunked(gpu):
     """TILEDATTN_CHUNKED_HEAD_DIMS=96 computes the same attention as the unchunked path."""
     q, k, v = inputs((1, 2, 256, 96), "bfloat16", 96)
@@ -239,8 +278,8 @@ def test_invalid_knobs_raise_before_launch(gpu):
                      ({"tile_m": -64}, "must be positive")]:
         with knobs(**env), pytest.raises(ValueError, match=msg):
             sdpa(q, q, q)
-    with pytest.raises(Exception, match="head dimension D=160"):
-        sdpa(*(torch.zeros((1, 1, 8, 160), dtype=torch.float16, device="cuda"),) * 3)
+    with pytest.raises(Exception, match="head dimension D=300"):
+        sdpa(*(torch.zeros((1, 1, 8, 300), dtype=torch.float16, device="cuda"),) * 3)
 
 
 # ---------------------------------------------------------------- known-answer tests on the GPU

@@ -130,12 +130,13 @@ def test_reference_head_dim_padding_rule(d, expected):
 
 @pytest.mark.parametrize("d,expected", [
     (1, (64, 63)), (32, (64, 32)), (64, (64, 0)), (65, (128, 63)), (96, (128, 32)), (128, (128, 0)),
+    (129, (160, 31)), (160, (160, 0)), (161, (256, 95)), (192, (256, 64)), (256, (256, 0)),
 ])
 def test_gfx950_head_dim_padding(d, expected):
     assert ff._resolve_kernel_head_dim_gfx950(d) == expected
 
 
-@pytest.mark.parametrize("d", [0, 129, 160, 256])
+@pytest.mark.parametrize("d", [0, -1, 257, 512])
 def test_gfx950_head_dim_rejects(d):
     with pytest.raises(InvalidShapeError):
         ff._resolve_kernel_head_dim_gfx950(d)

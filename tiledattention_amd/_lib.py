@@ -37,7 +37,7 @@ def kernel_symbol(*, dtype: int, head_dim: int, tile_m: int, tile_n: int, causal
     rule as kernel_id() in csrc/tiledattn.cpp (used to label measurements)."""
     dt = "bf16" if dtype == TA_BF16 else "f16"
     c, t = int(bool(causal)), int(bool(tail))
-    if (tile_m, tile_n) == (128, 64) and accum == TA_ACC_FP32:
+    if (tile_m, tile_n) == (128, 64) and accum == TA_ACC_FP32 and head_dim <= 128:
         return "attn_fwd_pp.hsaco", f"ta_fwd_pp_{dt}_d{head_dim}_c{c}_t{t}"
     return (f"attn_fwd_m{tile_m}_n{tile_n}.hsaco",
             f"ta_fwd_{dt}_d{head_dim}_m{tile_m}_n{tile_n}_c{c}_t{t}_a{int(accum != TA_ACC_FP32)}")

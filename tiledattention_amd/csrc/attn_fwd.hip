@@ -48,15 +48,19 @@
 namespace ta {
 
 // LDS rows are padded so that every LDS address is a per-lane base plus an immediate
-// offset and both read patterns are free of bank conflicts on the 64-bank LDS:
-// * K (stride 2D + 16 bytes = 4 banks mod 64): one b128 read pass covers 16 consecutive
-//   rows at one 16-byte column -> 16 disjoint 4-bank groups;
-// * V (stride 2D + 64 bytes = 16 banks mod 64): one b64 transposed read pass covers 4
-//   consecutive rows x 64 bytes -> 4 disjoint 16-bank groups.
+// offset and both read patterns are free of bank conflicts on the 64-bank LDS (16 units of
+// 16 bytes per 256-byte bank row):
+// * K: stride 2D + 16 bytes, an odd number of 16-byte units (D is a multiple of 16): one
+//   b128 read pass covers 16 consecutive rows at one 16-byte column -> 16 distinct units;
+// * V: stride 2D padded to 4 (mod 8) units (2D + 64 bytes for D = 64, 128, 256; 2D for
+//   D = 160): one b64 transposed read pass covers 4 consecutive rows x 4 units -> 16
+//   distinct units.
 template <int D>
 struct LdsLayout {
-  static constexpr int KS = 2 * D + 16;  // K row stride, bytes
-  static constexpr int VS = 2 * D + 64;  // V row stride, bytes
+  static_assert(D % 16 == 0, "head dim must be a multiple of 16");
+  static constexpr int KS = 2 * D + 16;                        // K row stride, bytes
+  static constexpr int VS = 2 * D + 16 * ((12 - (D / 8) % 8) % 8);  // V row stride, bytes
+  static_assert((KS / 16) % 2 == 1 && (VS / 16) % 8 == 4, "conflict-free strides");
 };
 
 template <int DT, int D, int TM, int TN, bool CAUSAL, bool TAIL, bool LOWP>
@@ -68,8 +72,9 @@ __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
   constexpr int DB = D / 32;         // 32-wide d blocks of O
   constexpr int CPR = D / 8;         // 16-byte chunks per row
   constexpr int LD = TN * CPR / NT;  // 16-byte chunks per thread per tensor per tile
-  constexpr int RPP = NT / CPR;      // rows covered by one staging pass
-  static_assert((TN * CPR) % NT == 0 && NT % CPR == 0, "tile must split evenly over threads");
+  // Rows one staging pass covers when a pass is whole rows (CPR divides NT), else 0.
+  constexpr int RPP = (NT % CPR == 0) ? NT / CPR : 0;
+  static_assert((TN * CPR) % NT == 0, "tile must split evenly over threads");
   using L = LdsLayout<D>;
   constexpr int K_BYTES = TN * L::KS;
   constexpr int STAGE = K_BYTES + TN * L::VS;
@@ -135,15 +140,27 @@ __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
   const int wave_kv_end = CAUSAL ? min(S, wq0 + 32) : S;
 
   // ---- staging: HBM -> VGPR -> LDS --------------------------------------------------
-  // Thread t moves 16-byte chunks t, t + NT, ... of each tile: row (t / CPR) + i * RPP,
-  // column chunk t % CPR.  Global side: buffer loads at a fixed per-thread byte offset
-  // from a per-tile resource; LDS side: a fixed per-thread base plus immediates.
-  const int st_row = tid / CPR;
+  // Thread t moves 16-byte chunks t, t + NT, ... of each tile: chunk c is row c / CPR,
+  // column chunk c % CPR.  When a pass is whole rows (CPR divides NT) every chunk of a
+  // thread sits in one column, RPP rows apart: a fixed per-thread byte offset plus
+  // immediates on both sides.  Otherwise (D = 160) each chunk's row and column are
+  // computed once.  Global side: buffer loads from a per-tile resource.
+  const int st_row = tid / CPR;  // whole-row passes: first row and column of the thread
   const int st_ch = tid % CPR;
   const int st_koff = st_row * k_rb + st_ch * 16;
   const int st_voff = st_row * v_rb + st_ch * 16;
   const int st_klds = st_row * L::KS + st_ch * 16;
   const int st_vlds = K_BYTES + st_row * L::VS + st_ch * 16;
+  // Byte offset of chunk i of this thread: `base` + i rows-per-pass for whole-row passes,
+  // else from the chunk's own row and column (`lds` adds the V tile's LDS base).
+  auto st_off = [&](int i, int base, int stride, int lds) {
+    if constexpr (RPP != 0) {
+      return base + i * RPP * stride;
+    } else {
+      const int c = tid + i * NT;
+      return lds + (c / CPR) * stride + (c % CPR) * 16;
+    }
+  };
   u32x4 stk[LD], stv[LD];
   auto load_tile = [&](int kt) {
     const int rows = S - kt * TN;
@@ -151,16 +168,16 @@ __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
     const __amdgpu_buffer_rsrc_t vr = row_rsrc(vp + (int64_t)kt * TN * p.v_ss, rows, v_rb);
 #pragma unroll
     for (int i = 0; i < LD; ++i) {
-      stk[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, st_koff + i * RPP * k_rb, 0, 0));
-      stv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, st_voff + i * RPP * v_rb, 0, 0));
+      stk[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, st_off(i, st_koff, k_rb, 0), 0, 0));
+      stv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, st_off(i, st_voff, v_rb, 0), 0, 0));
     }
   };
   auto store_tile = [&](int stage) {
     char* base = smem + stage * STAGE;
 #pragma unroll
     for (int i = 0; i < LD; ++i) {
-      *(u32x4*)(base + st_klds + i * RPP * L::KS) = stk[i];
-      *(u32x4*)(base + st_vlds + i * RPP * L::VS) = stv[i];
+      *(u32x4*)(base + st_off(i, st_klds, L::KS, 0)) = stk[i];
+      *(u32x4*)(base + st_off(i, st_vlds, L::VS, K_BYTES)) = stv[i];
     }
   };
 
@@ -392,7 +409,8 @@ __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
 
 // Waves per SIMD the register allocation is sized for: two when two workgroups fit a CU
 // by LDS (TM = 128, TN = 64: 8 waves per CU), so one wave's MFMAs overlap the other's
-// softmax; one otherwise.
+// softmax; one otherwise, and always one for head dims above 128 (whose O, Q and staging
+// registers need the whole register file, and whose tiles fill most of the LDS).
 #if TA_TILE_M == 128 && TA_TILE_N == 64
 #define TA_WAVES_PER_SIMD 2
 #else
@@ -404,24 +422,33 @@ __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
 #define TA_NAME2(DTN, D, M, N, C, T, A) ta_fwd_##DTN##_d##D##_m##M##_n##N##_c##C##_t##T##_a##A
 #define TA_NAME(DTN, D, M, N, C, T, A) TA_NAME2(DTN, D, M, N, C, T, A)
 
-#define TA_DEFINE(DTN, DT, D, C, T, A)                                                      \
+#define TA_DEFINE(DTN, DT, D, C, T, A, WPS)                                                 \
   extern "C" __global__ void __launch_bounds__(TA_TILE_M * 2)                               \
-      __attribute__((amdgpu_waves_per_eu(TA_WAVES_PER_SIMD, TA_WAVES_PER_SIMD)))            \
+      __attribute__((amdgpu_waves_per_eu(WPS, WPS)))                                        \
       TA_NAME(DTN, D, TA_TILE_M, TA_TILE_N, C, T, A)(ta::FwdParams p) {                     \
     ta::attn_fwd_body<DT, D, TA_TILE_M, TA_TILE_N, (C != 0), (T != 0), (A != 0)>(p);         \
   }
 
-#define TA_DEFINE_CTA(DTN, DT, D) \
-  TA_DEFINE(DTN, DT, D, 0, 0, 0)  \
-  TA_DEFINE(DTN, DT, D, 0, 0, 1)  \
-  TA_DEFINE(DTN, DT, D, 0, 1, 0)  \
-  TA_DEFINE(DTN, DT, D, 0, 1, 1)  \
-  TA_DEFINE(DTN, DT, D, 1, 0, 0)  \
-  TA_DEFINE(DTN, DT, D, 1, 0, 1)  \
-  TA_DEFINE(DTN, DT, D, 1, 1, 0)  \
-  TA_DEFINE(DTN, DT, D, 1, 1, 1)
+#define TA_DEFINE_CTA(DTN, DT, D, WPS) \
+  TA_DEFINE(DTN, DT, D, 0, 0, 0, WPS)  \
+  TA_DEFINE(DTN, DT, D, 0, 0, 1, WPS)  \
+  TA_DEFINE(DTN, DT, D, 0, 1, 0, WPS)  \
+  TA_DEFINE(DTN, DT, D, 0, 1, 1, WPS)  \
+  TA_DEFINE(DTN, DT, D, 1, 0, 0, WPS)  \
+  TA_DEFINE(DTN, DT, D, 1, 0, 1, WPS)  \
+  TA_DEFINE(DTN, DT, D, 1, 1, 0, WPS)  \
+  TA_DEFINE(DTN, DT, D, 1, 1, 1, WPS)
 
-TA_DEFINE_CTA(f16, 0, 64)
-TA_DEFINE_CTA(f16, 0, 128)
-TA_DEFINE_CTA(bf16, 1, 64)
-TA_DEFINE_CTA(bf16, 1, 128)
+TA_DEFINE_CTA(f16, 0, 64, TA_WAVES_PER_SIMD)
+TA_DEFINE_CTA(f16, 0, 128, TA_WAVES_PER_SIMD)
+TA_DEFINE_CTA(bf16, 1, 64, TA_WAVES_PER_SIMD)
+TA_DEFINE_CTA(bf16, 1, 128, TA_WAVES_PER_SIMD)
+
+// Head dims 160 and 256: 64-key tiles only (two stages of padded K and V rows take 84 KiB
+// and 141 KiB of LDS; 128-key tiles would not fit).
+#if TA_TILE_N == 64
+TA_DEFINE_CTA(f16, 0, 160, 1)
+TA_DEFINE_CTA(f16, 0, 256, 1)
+TA_DEFINE_CTA(bf16, 1, 160, 1)
+TA_DEFINE_CTA(bf16, 1, 256, 1)
+#endif

@@ -86,7 +86,7 @@ struct KernelId {
 KernelId kernel_id(int dtype, int d, int tm, int tn, int causal, int tail, int accum) {
   const char* dt = dtype == TA_BF16 ? "bf16" : "f16";
   char buf[96];
-  if (tm == 128 && tn == 64 && accum == TA_ACC_FP32) {
+  if (tm == 128 && tn == 64 && accum == TA_ACC_FP32 && d <= 128) {
     // Eight waves: two per SIMD sharing the rows of a 32-row block, splitting every
     // 128-key step between them (attn_fwd_pp.hip).
     snprintf(buf, sizeof(buf), "ta_fwd_pp_%s_d%d_c%d_t%d", dt, d, causal ? 1 : 0, tail ? 1 : 0);
@@ -100,6 +100,21 @@ KernelId kernel_id(int dtype, int d, int tm, int tn, int causal, int tail, int a
 }
 
 bool valid_tile(int t) { return t == 64 || t == 128; }
+
+bool valid_head_dim(int64_t d) { return d == 64 || d == 128 || d == 160 || d == 256; }
+
+// Head dims above 128 exist only with 64-key tiles (two stages of wider rows fill the LDS).
+ta_status check_shape(int64_t d, int tile_m, int tile_n) {
+  if (!valid_head_dim(d))
+    return fail(TA_EUNSUPPORTED, "head_dim %lld (kernels exist for 64, 128, 160 and 256)",
+                (long long)d);
+  if (!valid_tile(tile_m) || !valid_tile(tile_n))
+    return fail(TA_EUNSUPPORTED, "tile (%d, %d) (supported: 64 or 128 each)", tile_m, tile_n);
+  if (d > 128 && tile_n != 64)
+    return fail(TA_EUNSUPPORTED, "tile_n %d with head_dim %lld (head dims above 128 need tile_n 64)",
+                tile_n, (long long)d);
+  return TA_OK;
+}
 
 // Caller holds g_mu and has made `device` current.
 ta_status check_arch_locked(int device) {
@@ -203,10 +218,8 @@ ta_status ta_set_code_object_dir(const char* dir) {
 ta_status ta_prepare(int32_t device, int32_t dtype, int32_t head_dim, int32_t tile_m,
                      int32_t tile_n, int32_t causal, int32_t accum, int32_t aligned) {
   if (dtype != TA_FP16 && dtype != TA_BF16) return fail(TA_EINVAL, "dtype %d", dtype);
-  if (head_dim != 64 && head_dim != 128)
-    return fail(TA_EUNSUPPORTED, "head_dim %d (kernels exist for 64 and 128)", head_dim);
-  if (!valid_tile(tile_m) || !valid_tile(tile_n))
-    return fail(TA_EUNSUPPORTED, "tile (%d, %d) (supported: 64 or 128 each)", tile_m, tile_n);
+  ta_status shape_st = check_shape(head_dim, tile_m, tile_n);
+  if (shape_st != TA_OK) return shape_st;
   if (accum != TA_ACC_FP32 && accum != TA_ACC_INPUT) return fail(TA_EINVAL, "accum %d", accum);
   std::lock_guard<std::mutex> lock(g_mu);
   DeviceGuard guard(device);
@@ -225,11 +238,8 @@ ta_status ta_sdpa_fwd(const ta_fwd_args* a, void* stream) {
   if (a->causal != 0 && a->causal != 1) return fail(TA_EINVAL, "causal %d", a->causal);
   if (a->sched < 0 || a->sched > 2) return fail(TA_EINVAL, "sched %d", a->sched);
   if (a->B < 0 || a->H < 0 || a->S < 0) return fail(TA_EINVAL, "negative shape");
-  if (a->D != 64 && a->D != 128)
-    return fail(TA_EUNSUPPORTED, "head_dim %lld (kernels exist for 64 and 128)", (long long)a->D);
-  if (!valid_tile(a->tile_m) || !valid_tile(a->tile_n))
-    return fail(TA_EUNSUPPORTED, "tile (%d, %d) (supported: 64 or 128 each)", a->tile_m,
-                a->tile_n);
+  ta_status shape_st = check_shape(a->D, a->tile_m, a->tile_n);
+  if (shape_st != TA_OK) return shape_st;
   if (a->B == 0 || a->H == 0 || a->S == 0) return TA_OK;
   if (!a->q || !a->k || !a->v || !a->o) return fail(TA_EINVAL, "null tensor pointer");
   if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->o))

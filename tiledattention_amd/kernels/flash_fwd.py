@@ -56,7 +56,8 @@ _CHUNKED_HEAD_DIM_PARTS = {
     160: (128, 32),
 }
 _SUPPORTED_TILES = frozenset({64, 128})
-_KERNEL_HEAD_DIMS = (64, 128)
+_KERNEL_HEAD_DIMS = (64, 128, 160, 256)
+_WIDE_HEAD_DIM_TILE_N = 64  # head dims above 128 run with 64-key tiles only
 _SYNC_MODES = ("strict", "post", "async")
 
 
@@ -144,9 +145,11 @@ def _resolve_kernel_head_dim(head_dim: int) -> tuple[int, int]:
 def _resolve_kernel_head_dim_gfx950(head_dim: int) -> tuple[int, int]:
     """Head dim of the gfx950 kernel that runs ``head_dim``, and the zero padding to add.
 
-    Kernels exist for D = 64 and 128.  Smaller head dims are zero-padded to the next of
-    them, which leaves Q K^T unchanged and only adds zero output columns that are sliced
-    off (the reference pads the same way, to a power of two, flash_fwd.py:149-163).
+    Kernels exist for D = 64, 128, 160 and 256.  Other head dims are zero-padded to the next
+    of them, which leaves Q K^T unchanged and only adds zero output columns that are sliced
+    off (the reference pads the same way, to a power of two, flash_fwd.py:149-163; its
+    160 = 128 + 32 chunk plan, :21-24, computes the same contraction as the native D = 160
+    kernel here).  Above 256 there is no kernel.
     """
     if head_dim <= 0:
         raise InvalidShapeError("head dimension D must be positive.")
@@ -154,7 +157,7 @@ def _resolve_kernel_head_dim_gfx950(head_dim: int) -> tuple[int, int]:
         if head_dim <= kd:
             return kd, kd - head_dim
     raise InvalidShapeError(
-        f"head dimension D={head_dim} is not supported: the gfx950 kernels cover D <= 128."
+        f"head dimension D={head_dim} is not supported: the gfx950 kernels cover D <= 256."
     )
 
 
@@ -348,6 +351,13 @@ def run_flash_fwd(
 
     chunk_plan = _resolve_chunk_plan(head_dim)
     kernel_head_dim, pad_dim = _resolve_kernel_head_dim_gfx950(head_dim)
+    if kernel_head_dim > 128 and tile_n != _WIDE_HEAD_DIM_TILE_N:
+        if os.getenv("TILEDATTN_TILE_M") or os.getenv("TILEDATTN_TILE_N"):
+            raise ValueError(
+                f"TILEDATTN_TILE_N={tile_n} is not supported for head dimension D={head_dim} "
+                f"on gfx950: head dims above 128 run with TILE_N=64."
+            )
+        tile_n = _WIDE_HEAD_DIM_TILE_N
     dtype_code = _dtype_code_for_torch_dtype(q.dtype)
 
     device = q.device
