@@ -89,6 +89,39 @@ ta_status ta_prepare(int32_t device, int32_t dtype, int32_t head_dim, int32_t ti
  * launch. */
 ta_status ta_sdpa_fwd(const ta_fwd_args* args, void* stream);
 
+/* Split key ranges: no counterpart in the reference, whose grid is one program per
+ * (query block, b*h) (flash_fwd.py:806-809).  With few (b, h) slices, or causal rows whose
+ * lengths differ by S / 128 key steps, that grid leaves compute units idle while the
+ * longest rows finish.  The split path cuts every 128-row query block's keys into chunks of
+ * `chunk_steps` steps of 128 keys, runs one workgroup per chunk, and merges the chunks of a
+ * block (log-sum-exp weights) in a second kernel on the same stream.  It exists for tile
+ * (128, 64) with fp32 accumulation and D <= 128; the result matches ta_sdpa_fwd within
+ * fp32 rounding of the merge. */
+
+/* Chunk length (key steps) this library would use for `args` on its device: 0 when the
+ * unsplit grid is as fast (large grids, configurations without a split kernel).  Computed
+ * from a model of the dispatch of the grid over the device's compute units; cached per
+ * (S, B*H, causal, CU count).  Reads only the shape, dtype, tile, accum and device fields
+ * (tensor pointers and strides may be unset). */
+ta_status ta_split_plan(const ta_fwd_args* args, int32_t* chunk_steps);
+
+/* The model behind ta_split_plan for a device with `compute_units` CUs, without touching
+ * a device: chunk length for a (128, 64)-tile fp32-accumulation forward of sequence length
+ * S over n_bh (b, h) slices, 0 for no split or invalid sizes. */
+int32_t ta_split_plan_model(int64_t S, int64_t n_bh, int32_t causal, int32_t compute_units);
+
+/* Device workspace (bytes, 256-byte aligned base required) that ta_sdpa_fwd_split needs
+ * for `chunk_steps`; 0 when that chunk length splits nothing.  Needs no device; reads only
+ * the shape, dtype, tile and accum fields. */
+ta_status ta_split_workspace_size(const ta_fwd_args* args, int32_t chunk_steps, int64_t* bytes);
+
+/* Enqueue one SDPA forward with split key ranges on `stream`.  chunk_steps = 0, or a
+ * chunk length that splits nothing, is exactly ta_sdpa_fwd.  The workspace is owned by the
+ * caller, needs no initialisation, and must not be used by another call until this one's
+ * work on `stream` has finished. */
+ta_status ta_sdpa_fwd_split(const ta_fwd_args* args, int32_t chunk_steps, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+
 /* Unload every cached module on every device (compile_cache.reset_cache_for_tests). */
 ta_status ta_cache_reset(void);
 

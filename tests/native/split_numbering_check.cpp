@@ -1,0 +1,130 @@
+// Host-only check of the eight-wave kernel's grid numbering (attn_fwd_split.h): for every
+// block id of the whole-row and split grids, over a range of shapes, chunk lengths and
+// both issue orders, the items must cover every key step of every (b, h, query block)
+// exactly once, partial slots must be unique, in range and used exactly by the blocks of
+// more than one chunk, and the merge grid must name exactly those blocks with their
+// chunks' slots in key order.  Prints "ok <cases>" or the first failure.
+#include <algorithm>
+#include <cstdio>
+#include <map>
+#include <set>
+#include <tuple>
+#include <vector>
+
+#include "attn_fwd_split.h"
+
+static int fails = 0;
+#define CHECK(cond, ...)                                             \
+  do {                                                               \
+    if (!(cond)) {                                                   \
+      if (fails++ < 10) {                                            \
+        printf("FAIL %s:%d: %s: ", __FILE__, __LINE__, #cond);       \
+        printf(__VA_ARGS__);                                         \
+        printf("\n");                                                \
+      }                                                              \
+    }                                                                \
+  } while (0)
+
+static void check_case(int S, int n_bh, bool causal, int c, int sched) {
+  const int nq = (S + ta::kPPRows - 1) / ta::kPPRows;
+  const int len = (S + ta::kPPKeys - 1) / ta::kPPKeys;
+  auto steps_of = [&](int qt) {
+    // key steps a query block needs: causal rows stop at the block's last row
+    if (!causal) return len;
+    const int kv_end = (qt + 1) * ta::kPPRows < S ? (qt + 1) * ta::kPPRows : S;
+    return (kv_end + ta::kPPKeys - 1) / ta::kPPKeys;
+  };
+  ta::SplitLayout l;
+  const bool split = ta::split_layout(S, causal, c, &l);
+  // whole-row grid
+  if (c == 0) {
+    std::vector<int> seen((size_t)n_bh * nq, 0);
+    for (int blk = 0; blk < n_bh * nq; ++blk) {
+      const ta::WorkItem w = ta::whole_item(blk, n_bh, nq, sched, causal);
+      CHECK(w.bh >= 0 && w.bh < n_bh && w.qt >= 0 && w.qt < nq, "blk %d", blk);
+      if (w.bh >= 0 && w.bh < n_bh && w.qt >= 0 && w.qt < nq) seen[(size_t)w.bh * nq + w.qt]++;
+      CHECK(w.slot == -1 && w.t_beg == 0 && w.t_end == -1, "blk %d", blk);
+    }
+    for (size_t i = 0; i < seen.size(); ++i) CHECK(seen[i] == 1, "S=%d tile %zu seen %d", S, i, seen[i]);
+    return;
+  }
+  if (!split) {
+    // no split: every block fits in one chunk
+    for (int qt = 0; qt < nq; ++qt) CHECK(steps_of(qt) <= c, "S=%d c=%d qt=%d", S, c, qt);
+    return;
+  }
+  // split grid: coverage of key steps
+  std::map<std::pair<int, int>, std::vector<std::tuple<int, int, int>>> chunks;  // (bh,qt) -> (beg,end,slot)
+  std::set<int> slots;
+  const int total = (int)(n_bh * l.items);
+  for (int blk = 0; blk < total; ++blk) {
+    const ta::WorkItem w = ta::split_item(blk, n_bh, (int)l.items, sched, causal, c, (int)l.ns,
+                                          (int)l.slots, S);
+    CHECK(w.bh >= 0 && w.bh < n_bh && w.qt >= 0 && w.qt < nq, "S=%d c=%d blk %d bh %d qt %d", S, c, blk, w.bh, w.qt);
+    CHECK(w.t_beg >= 0 && w.t_beg < w.t_end && w.t_end <= steps_of(w.qt) && w.t_end - w.t_beg <= c,
+          "S=%d c=%d blk %d [%d,%d) steps %d", S, c, blk, w.t_beg, w.t_end, steps_of(w.qt));
+    if (w.slot >= 0) {
+      CHECK(w.slot < n_bh * l.slots, "slot %d of %lld", w.slot, (long long)(n_bh * l.slots));
+      CHECK(slots.insert(w.slot).second, "slot %d reused", w.slot);
+    }
+    chunks[{w.bh, w.qt}].emplace_back(w.t_beg, w.t_end, w.slot);
+  }
+  CHECK((int)chunks.size() == n_bh * nq, "S=%d c=%d blocks %zu of %d", S, c, chunks.size(), n_bh * nq);
+  std::map<std::pair<int, int>, std::vector<int>> split_blocks;  // -> slots in key order
+  for (auto& kv : chunks) {
+    auto v = kv.second;
+    std::sort(v.begin(), v.end());
+    int at = 0;
+    for (auto& t : v) {
+      CHECK(std::get<0>(t) == at, "S=%d c=%d bh %d qt %d gap at %d", S, c, kv.first.first, kv.first.second, at);
+      at = std::get<1>(t);
+    }
+    CHECK(at == steps_of(kv.first.second), "S=%d c=%d qt %d ends at %d", S, c, kv.first.second, at);
+    if (v.size() == 1) {
+      CHECK(std::get<2>(v[0]) == -1, "single chunk with slot %d", std::get<2>(v[0]));
+    } else {
+      std::vector<int> sl;
+      for (auto& t : v) {
+        CHECK(std::get<2>(t) >= 0, "chunk of a split block without a slot");
+        sl.push_back(std::get<2>(t));
+      }
+      split_blocks[kv.first] = sl;
+    }
+  }
+  CHECK((int64_t)slots.size() <= n_bh * l.slots, "slots");
+  // merge grid
+  std::set<std::pair<int, int>> merged;
+  for (int blk = 0; blk < n_bh * l.merge; ++blk) {
+    const ta::MergeItem m = ta::merge_item(blk, nq, causal, c, (int)l.ns, (int)l.slots);
+    auto it = split_blocks.find({m.bh, m.qt});
+    CHECK(it != split_blocks.end(), "merge blk %d names unsplit block (%d, %d)", blk, m.bh, m.qt);
+    if (it == split_blocks.end()) continue;
+    CHECK((int)it->second.size() == m.ns, "merge ns %d vs %zu", m.ns, it->second.size());
+    for (int i = 0; i < m.ns && i < (int)it->second.size(); ++i)
+      CHECK(it->second[i] == m.slot0 + i, "merge slot %d vs %d", m.slot0 + i, it->second[i]);
+    CHECK(merged.insert({m.bh, m.qt}).second, "block merged twice");
+  }
+  CHECK(merged.size() == split_blocks.size(), "S=%d c=%d merged %zu of %zu", S, c, merged.size(), split_blocks.size());
+}
+
+int main() {
+  int cases = 0;
+  const int seqs[] = {1, 100, 128, 129, 255, 256, 300, 1000, 1024, 2048, 2100, 4096, 8192, 16384};
+  const int bhs[] = {1, 2, 3, 4, 6, 8, 16};
+  for (int S : seqs)
+    for (int n_bh : bhs)
+      for (int causal = 0; causal < 2; ++causal)
+        for (int sched = 0; sched < 2; ++sched) {
+          const int len = (S + 127) / 128;
+          for (int c = 0; c <= len + 1; c += (c < 8 ? 1 : 1 + c / 4)) {
+            check_case(S, n_bh, causal != 0, c, sched);
+            ++cases;
+          }
+        }
+  if (fails) {
+    printf("%d failures\n", fails);
+    return 1;
+  }
+  printf("ok %d\n", cases);
+  return 0;
+}

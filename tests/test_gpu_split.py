@@ -1,0 +1,166 @@
+"""GPU parity of split key ranges (ta_sdpa_fwd_split: the split eight-wave kernel plus the
+merge kernel) against the CPU oracle, and against the whole-row path on the same inputs.
+
+Every case names itself on stdout before touching the GPU.  Chunk lengths are forced with
+TILEDATTN_SPLIT so that every numbering shape runs: one-step chunks (every block split as
+far as it goes), chunks that leave a remainder, non-causal and causal grids, ragged S
+(masked last key step inside the last chunk), both dtypes and both head dims, strided
+inputs, and the C5 outlier variant that stresses the rescale across chunk boundaries.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from tests.parity_util import as_f32, check_close, inputs, knobs, oracle_f32, run_gpu, sample_rows, say
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("shape,dtype,causal,chunks", [
+    ((1, 8, 1024, 128), "bfloat16", True, (1, 2, 3)),
+    ((1, 2, 1000, 64), "float16", True, (1, 3)),
+    ((2, 3, 777, 128), "float16", False, (1, 2, 5)),
+    ((1, 8, 2048, 64), "bfloat16", False, (4,)),
+    ((1, 4, 2304, 128), "float16", True, (5,)),
+    ((1, 1, 129, 128), "bfloat16", True, (1,)),
+    ((1, 1, 129, 64), "float16", False, (1,)),
+])
+def test_forced_chunks_match_oracle(gpu, shape, dtype, causal, chunks):
+    q, k, v = inputs(shape, dtype, 300 + shape[2])
+    ref = oracle_f32(q, k, v, causal=causal)
+    for chunk in chunks:
+        say(f"split {dtype} {shape} causal={causal} chunk={chunk}")
+        # the automatic accumulation policy picks input-dtype accumulation for some of these
+        # shapes, which has no split kernel
+        out = run_gpu(q, k, v, causal=causal, split=chunk, accum_mode="fp32")
+        check_close(as_f32(out), ref, dtype, what=f"split chunk={chunk}")
+
+
+@pytest.mark.parametrize("shape", [(1, 8, 2048, 128), (1, 1, 8192, 128), (1, 2, 4096, 128)])
+def test_split_and_whole_rows_agree(gpu, shape):
+    """bf16 causal, seed 1234, forced 8-step chunks (C3's shape) and the automatic plan
+    (which splits the B*H = 1 and 2 shapes): both paths meet the oracle's tolerance and
+    differ from each other only by the rounding of the merge."""
+    from tiledattention_amd.kernels import flash_fwd
+
+    s, n_bh = shape[2], shape[1]
+    q, k, v = inputs(shape, "bfloat16", 1234)
+    rows = None if s <= 2048 else sample_rows(s, 128)
+    ref = oracle_f32(q, k, v, causal=True, rows=rows)
+    split = 8 if n_bh == 8 else "auto"
+    say(f"bf16 causal {shape} split={split}")
+    auto = run_gpu(q, k, v, causal=True, split=split)
+    if n_bh < 8:
+        assert any(key[0] == s and key[1] == n_bh and key[2] == 1 and c > 0
+                   for key, c in flash_fwd._SPLIT_PLANS.items()), flash_fwd._SPLIT_PLANS
+    say(f"bf16 causal {shape} split=off")
+    whole = run_gpu(q, k, v, causal=True, split="off")
+    a, w = as_f32(auto, rows), as_f32(whole, rows)
+    check_close(a, ref, "bfloat16", what=f"{shape} split {split}")
+    check_close(w, ref, "bfloat16", what=f"{shape} whole rows")
+    # one bf16 rounding step apart at most (|o| < 2 here, so 2^-7 per unit of |o|)
+    diff = np.abs(a - w)
+    assert float(diff.max()) <= 2.0 ** -7 * max(1.0, float(np.abs(w).max())), float(diff.max())
+    assert float(diff.mean()) < 1e-3
+
+
+def test_outlier_keys_across_chunks(gpu):
+    """C5b's outlier variant (1% of k entries x20) at S=2048: the running maxima differ
+    strongly between chunks, so the merge's log-sum-exp weights span many octaves."""
+    q, k, v = inputs((1, 8, 2048, 128), "float16", 1234, outlier_frac=0.01, outlier_gain=20.0,
+                     outlier_seed=1235)
+    ref = oracle_f32(q, k, v, causal=True)
+    for chunk in (1, 4):
+        say(f"split fp16 outliers (1,8,2048,128) causal chunk={chunk}")
+        out = run_gpu(q, k, v, causal=True, split=chunk, accum_mode="fp32")
+        check_close(as_f32(out), ref, "float16", what=f"outliers chunk={chunk}")
+
+
+def test_strided_inputs_and_scale(gpu):
+    """[B,S,H,D]-strided views (no copy: unit last stride, 16-byte rows) and an explicit scale."""
+    import torch
+
+    from tiledattention_amd import sdpa
+
+    q, k, v = inputs((2, 4, 640, 64), "bfloat16", 77)
+    ref = oracle_f32(q, k, v, causal=True, scale=0.3)
+    dev = torch.device("cuda:0")
+    qs, ks, vs = (t.transpose(1, 2).contiguous().to(dev).transpose(1, 2) for t in (q, k, v))
+    assert not qs.is_contiguous()
+    say("split bf16 strided (2,4,640,64) causal scale=0.3 chunk=2")
+    with knobs(split=2, accum_mode="fp32"):
+        out = sdpa(qs, ks, vs, causal=True, scale=0.3)
+    torch.cuda.synchronize()
+    check_close(as_f32(out), ref, "bfloat16", what="strided split")
+
+
+def test_cabi_chunk_zero_is_the_whole_row_launch(gpu):
+    """ta_sdpa_fwd_split with chunk 0 (or a chunk that splits nothing) is ta_sdpa_fwd: the
+    outputs are bit-identical."""
+    import torch
+
+    from tiledattention_amd import _lib
+
+    lib = _lib.load()
+    q, k, v = inputs((1, 2, 512, 128), "float16", 5)
+    dev = torch.device("cuda:0")
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    outs = [torch.full_like(qd, float("nan")) for _ in range(3)]
+
+    def args(o):
+        a = _lib.FwdArgs()
+        a.q, a.k, a.v, a.o = qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), o.data_ptr()
+        a.B, a.H, a.S, a.D = 1, 2, 512, 128
+        for name, t in (("q_stride", qd), ("k_stride", kd), ("v_stride", vd), ("o_stride", o)):
+            getattr(a, name)[:] = tuple(t.stride())
+        a.scale, a.causal, a.dtype = 128 ** -0.5, 1, _lib.TA_FP16
+        a.tile_m, a.tile_n, a.accum, a.device, a.sched = 128, 64, _lib.TA_ACC_FP32, 0, 1
+        return a
+
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    say("C-ABI fp16 (1,2,512,128) causal: ta_sdpa_fwd vs ta_sdpa_fwd_split chunk 0 and chunk 4")
+    assert lib.ta_sdpa_fwd(ctypes.byref(args(outs[0])), ctypes.c_void_p(stream)) == _lib.TA_OK
+    assert lib.ta_sdpa_fwd_split(ctypes.byref(args(outs[1])), 0, None, 0, ctypes.c_void_p(stream)) == _lib.TA_OK
+    # 512 keys = 4 steps: a 4-step chunk splits nothing and needs no workspace
+    assert lib.ta_sdpa_fwd_split(ctypes.byref(args(outs[2])), 4, None, 0, ctypes.c_void_p(stream)) == _lib.TA_OK
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    check_close(as_f32(outs[0]), oracle_f32(q, k, v, causal=True), "float16", what="C-ABI whole rows")
+
+
+def test_cabi_split_with_caller_workspace(gpu):
+    """The C ABI with a caller-owned workspace (torch allocation), reused by two calls of
+    different shapes in a row on one stream; the workspace starts as garbage."""
+    import torch
+
+    from tiledattention_amd import _lib
+
+    lib = _lib.load()
+    dev = torch.device("cuda:0")
+    ws = torch.full((64 << 20,), 0x7f, dtype=torch.uint8, device=dev)  # NaN-ish bytes
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    for shape, causal, chunk in (((1, 4, 1536, 128), 1, 2), ((1, 2, 700, 64), 0, 1)):
+        q, k, v = inputs(shape, "bfloat16", 11 + shape[2])
+        qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+        o = torch.empty_like(qd)
+        a = _lib.FwdArgs()
+        a.q, a.k, a.v, a.o = qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), o.data_ptr()
+        a.B, a.H, a.S, a.D = shape
+        for name, t in (("q_stride", qd), ("k_stride", kd), ("v_stride", vd), ("o_stride", o)):
+            getattr(a, name)[:] = tuple(t.stride())
+        a.scale, a.causal, a.dtype = shape[3] ** -0.5, causal, _lib.TA_BF16
+        a.tile_m, a.tile_n, a.accum, a.device, a.sched = 128, 64, _lib.TA_ACC_FP32, 0, 1
+        need = ctypes.c_int64(0)
+        assert lib.ta_split_workspace_size(ctypes.byref(a), chunk, ctypes.byref(need)) == _lib.TA_OK
+        assert 0 < need.value <= ws.numel()
+        say(f"C-ABI split bf16 {shape} causal={causal} chunk={chunk} workspace={need.value}")
+        st = lib.ta_sdpa_fwd_split(ctypes.byref(a), chunk, ctypes.c_void_p(ws.data_ptr()), need.value,
+                                   ctypes.c_void_p(stream))
+        assert st == _lib.TA_OK, _lib.last_error(lib)
+        torch.cuda.synchronize()
+        check_close(as_f32(o), oracle_f32(q, k, v, causal=bool(causal)), "bfloat16",
+                    what=f"C-ABI split {shape}")

@@ -1,0 +1,220 @@
+"""Split key ranges on the CPU: the grid numbering the kernels and the host share
+(tiledattention_amd/csrc/attn_fwd_split.h, checked by a host-only C++ program), the
+library's dispatch model and workspace sizes through the C ABI, and the
+``TILEDATTN_SPLIT`` knob.  No kernel is launched here."""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from tiledattention_amd import _lib
+from tiledattention_amd.kernels import flash_fwd
+
+ROOT = Path(__file__).resolve().parents[1]
+MI355X_CUS = 256
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.library_path().exists():
+        pytest.fail("libtiledattn.so is not built: run __graft_entry__.build() first")
+    return _lib.load()
+
+
+def test_grid_numbering_covers_every_key_step_once(tmp_path):
+    """Whole-row and split grids over 1888 (S, B*H, causal, chunk, order) cases: every key
+    step of every (b, h, query block) is computed by exactly one workgroup, partial slots
+    are unique and in range, and the merge grid names exactly the split blocks with their
+    chunks' slots in key order."""
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("g++ not available")
+    exe = tmp_path / "split_numbering_check"
+    subprocess.run(
+        [gxx, "-O1", "-std=c++17", "-Wall", "-Werror", f"-I{ROOT / 'tiledattention_amd' / 'csrc'}",
+         "-o", str(exe), str(ROOT / "tests" / "native" / "split_numbering_check.cpp")],
+        check=True, capture_output=True, text=True,
+    )
+    res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert res.returncode == 0, res.stdout[-2000:]
+    assert res.stdout.startswith("ok ")
+
+
+def _args(*, S, B=1, H=8, D=128, causal=1, tile_m=128, tile_n=64, accum=_lib.TA_ACC_FP32, dtype=_lib.TA_BF16):
+    a = _lib.FwdArgs()
+    a.B, a.H, a.S, a.D = B, H, S, D
+    a.scale, a.causal, a.dtype = 0.125, causal, dtype
+    a.tile_m, a.tile_n, a.accum, a.device, a.sched = tile_m, tile_n, accum, 0, 1
+    return a
+
+
+def _slots(S: int, causal: bool, chunk: int) -> int:
+    """Chunks of the query blocks that have more than one chunk, per (b, h)."""
+    steps_total = math.ceil(S / 128)
+    total = 0
+    for qt in range(math.ceil(S / 128)):
+        steps = min(qt + 1, steps_total) if causal else steps_total
+        ns = math.ceil(steps / chunk)
+        if ns > 1:
+            total += ns
+    return total
+
+
+@pytest.mark.parametrize("S", [129, 1000, 1024, 2048, 4096, 5000])
+@pytest.mark.parametrize("causal", [0, 1])
+@pytest.mark.parametrize("chunk", [1, 2, 3, 7, 16])
+@pytest.mark.parametrize("D", [64, 128])
+def test_workspace_size_is_one_fp32_partial_per_chunk_of_a_split_block(lib, S, causal, chunk, D):
+    a = _args(S=S, B=2, H=3, D=D, causal=causal)
+    out = ctypes.c_int64(-1)
+    assert lib.ta_split_workspace_size(ctypes.byref(a), chunk, ctypes.byref(out)) == _lib.TA_OK
+    rows = 6 * _slots(S, bool(causal), chunk) * 128
+    expect = (rows * D * 4 + 255) // 256 * 256 + rows * 4 if rows else 0
+    assert out.value == expect
+
+
+def test_workspace_size_edge_cases(lib):
+    out = ctypes.c_int64(-1)
+    assert lib.ta_split_workspace_size(ctypes.byref(_args(S=4096)), 0, ctypes.byref(out)) == _lib.TA_OK
+    assert out.value == 0
+    assert lib.ta_split_workspace_size(ctypes.byref(_args(S=4096)), -1, ctypes.byref(out)) == _lib.TA_EINVAL
+    # a chunk as long as the longest row splits nothing
+    assert lib.ta_split_workspace_size(ctypes.byref(_args(S=4096)), 32, ctypes.byref(out)) == _lib.TA_OK
+    assert out.value == 0
+    for kw in (dict(tile_m=64), dict(tile_n=128), dict(accum=_lib.TA_ACC_INPUT), dict(D=160)):
+        st = lib.ta_split_workspace_size(ctypes.byref(_args(S=4096, **kw)), 4, ctypes.byref(out))
+        assert st == _lib.TA_EUNSUPPORTED, kw
+        assert "split key ranges" in _lib.last_error(lib)
+    assert lib.ta_split_workspace_size(None, 4, ctypes.byref(out)) == _lib.TA_EINVAL
+
+
+def test_split_launch_rejects_bad_workspace_before_any_device_call(lib):
+    a = _args(S=4096)
+    a.q = a.k = a.v = a.o = 0x10000
+    for name in ("q_stride", "k_stride", "v_stride", "o_stride"):
+        getattr(a, name)[:] = (8 * 4096 * 128, 4096 * 128, 128, 1)
+    need = ctypes.c_int64(0)
+    assert lib.ta_split_workspace_size(ctypes.byref(a), 4, ctypes.byref(need)) == _lib.TA_OK
+    assert need.value > 0
+    st = lib.ta_sdpa_fwd_split(ctypes.byref(a), 4, ctypes.c_void_p(0x100000), need.value - 4, None)
+    assert st == _lib.TA_EINVAL and "workspace of" in _lib.last_error(lib)
+    st = lib.ta_sdpa_fwd_split(ctypes.byref(a), 4, None, need.value, None)
+    assert st == _lib.TA_EINVAL and "workspace of" in _lib.last_error(lib)
+    st = lib.ta_sdpa_fwd_split(ctypes.byref(a), 4, ctypes.c_void_p(0x100010), need.value, None)
+    assert st == _lib.TA_EINVAL and "256-byte" in _lib.last_error(lib)
+    st = lib.ta_sdpa_fwd_split(ctypes.byref(a), -2, ctypes.c_void_p(0x100000), need.value, None)
+    assert st == _lib.TA_EINVAL
+    a.tile_m = 64
+    st = lib.ta_sdpa_fwd_split(ctypes.byref(a), 4, ctypes.c_void_p(0x100000), need.value, None)
+    assert st == _lib.TA_EUNSUPPORTED
+
+
+def _plan(lib, S, n_bh, causal, cus=MI355X_CUS):
+    return lib.ta_split_plan_model(S, n_bh, causal, cus)
+
+
+def test_plan_model_splits_small_grids_and_leaves_large_ones(lib):
+    # Measured on the MI355X (B*H, S): splitting made B*H = 1 or 2 with long rows 1.3-2.5x
+    # faster (e.g. causal (1, 8192): 84 -> 34 us), while for B*H = 8 (the C3 sweep) the best
+    # chunk gained at most 10 % and most chunks lost; the model picks only the former.
+    for n_bh, S, causal in ((1, 8192, 1), (1, 16384, 1), (2, 4096, 1), (2, 8192, 1),
+                            (2, 4096, 0), (1, 8192, 0)):
+        c = _plan(lib, S, n_bh, causal)
+        assert 0 < c < S // 128, (n_bh, S, causal, c)
+        out = ctypes.c_int64(0)
+        a = _args(S=S, B=1, H=n_bh, causal=causal)
+        assert lib.ta_split_workspace_size(ctypes.byref(a), c, ctypes.byref(out)) == _lib.TA_OK
+        assert out.value > 0  # the chosen chunk splits something
+    for S in (1024, 2048, 4096, 8192, 16384):
+        assert _plan(lib, S, 8, 1) == 0, S
+    # grids of many waves balance by themselves
+    assert _plan(lib, 4096, 64, 1) == 0
+    assert _plan(lib, 4096, 64, 0) == 0
+    assert _plan(lib, 8192, 32, 0) == 0
+    # nothing to split: a single key step
+    assert _plan(lib, 128, 1, 1) == 0 and _plan(lib, 100, 1, 0) == 0
+    # invalid sizes
+    assert _plan(lib, 0, 8, 1) == 0 and _plan(lib, 4096, 0, 1) == 0 and _plan(lib, 4096, 8, 1, 0) == 0
+
+
+def test_plan_model_uses_the_compute_unit_count(lib):
+    # On a device an eighth the size the same grid is several waves deep: no split.
+    assert _plan(lib, 8192, 1, 1, MI355X_CUS) > 0
+    assert _plan(lib, 8192, 1, 1, 32) == 0
+
+
+# ---------------------------------------------------------------- TILEDATTN_SPLIT knob
+
+@pytest.mark.parametrize("raw,capable,expect", [
+    ("off", True, 0), ("0", True, 0), ("OFF", False, 0), ("auto", False, 0), ("", False, 0),
+    ("3", True, 3), (" 12 ", True, 12), ("0", False, 0),
+])
+def test_split_knob(monkeypatch, raw, capable, expect):
+    monkeypatch.setenv("TILEDATTN_SPLIT", raw)
+    assert flash_fwd._resolve_split(None, _args(S=4096), capable=capable) == expect
+
+
+@pytest.mark.parametrize("raw,capable,msg", [
+    ("-1", True, ">= 0"), ("x", True, "'auto', 'off' or an integer"), ("1.5", True, "integer"),
+    ("4", False, "tile (128, 64)"),
+])
+def test_split_knob_rejects(monkeypatch, raw, capable, msg):
+    monkeypatch.setenv("TILEDATTN_SPLIT", raw)
+    with pytest.raises(ValueError, match=msg.replace("(", r"\(").replace(")", r"\)")):
+        flash_fwd._resolve_split(None, _args(S=4096), capable=capable)
+
+
+def test_split_capability_rule():
+    ok = dict(tile_m=128, tile_n=64, accum_code=_lib.TA_ACC_FP32, kernel_head_dim=128)
+    assert flash_fwd._split_capable(**ok)
+    assert flash_fwd._split_capable(**{**ok, "kernel_head_dim": 64})
+    assert not flash_fwd._split_capable(**{**ok, "kernel_head_dim": 160})
+    assert not flash_fwd._split_capable(**{**ok, "tile_m": 64})
+    assert not flash_fwd._split_capable(**{**ok, "tile_n": 128})
+    assert not flash_fwd._split_capable(**{**ok, "accum_code": _lib.TA_ACC_INPUT})
+
+
+def test_split_kernel_symbols_exist_in_code_object():
+    data = (_lib.lib_dir() / "attn_fwd_pp.hsaco").read_bytes()
+    for dtype, dt in ((_lib.TA_FP16, "f16"), (_lib.TA_BF16, "bf16")):
+        for d in (64, 128):
+            for causal in (0, 1):
+                for tail in (0, 1):
+                    f, sym = _lib.kernel_symbol(dtype=dtype, head_dim=d, tile_m=128, tile_n=64,
+                                                causal=bool(causal), tail=bool(tail),
+                                                accum=_lib.TA_ACC_FP32, split=True)
+                    assert f == "attn_fwd_pp.hsaco"
+                    assert sym.encode() + b"\x00" in data, sym
+                assert f"ta_fwd_merge_{dt}_d{d}_c{causal}".encode() + b"\x00" in data
+    with pytest.raises(ValueError):
+        _lib.kernel_symbol(dtype=0, head_dim=128, tile_m=64, tile_n=64, causal=True, tail=False,
+                           accum=_lib.TA_ACC_FP32, split=True)
+
+
+# ---------------------------------------------------------------- launch-plan cache keys
+
+def test_knob_snapshot_follows_the_environment(monkeypatch):
+    """Launch plans are cached per knob values, so the snapshot must see every change made
+    through os.environ (the reference re-reads its knobs on every call)."""
+    for name in flash_fwd._KNOBS:
+        monkeypatch.delenv(name, raising=False)
+    base = flash_fwd._knob_snapshot()
+    assert base == (None,) * len(flash_fwd._KNOBS)
+    for i, name in enumerate(flash_fwd._KNOBS):
+        monkeypatch.setenv(name, "7")
+        snap = flash_fwd._knob_snapshot()
+        assert snap[i] is not None and snap != base, name
+        monkeypatch.delenv(name)
+        assert flash_fwd._knob_snapshot() == base
+    # every TILEDATTN_* knob the host path reads is part of the key
+    src = (ROOT / "tiledattention_amd" / "kernels" / "flash_fwd.py").read_text()
+    import re
+
+    read = set(re.findall(r'"(TILEDATTN_[A-Z_]+)"', src))
+    assert read == set(flash_fwd._KNOBS)

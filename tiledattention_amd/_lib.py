@@ -32,13 +32,17 @@ TILE_SHAPES = ((64, 64), (64, 128), (128, 64), (128, 128))
 
 
 def kernel_symbol(*, dtype: int, head_dim: int, tile_m: int, tile_n: int, causal: bool,
-                  tail: bool, accum: int) -> tuple[str, str]:
+                  tail: bool, accum: int, split: bool = False) -> tuple[str, str]:
     """(code object file, kernel symbol) the C ABI launches for a configuration; the same
-    rule as kernel_id() in csrc/tiledattn.cpp (used to label measurements)."""
+    rule as kernel_id() in csrc/tiledattn.cpp (used to label measurements).  ``split``
+    names the split-key-range kernel (its merge kernel is ta_fwd_merge_<dt>_d<D>_c<c>)."""
     dt = "bf16" if dtype == TA_BF16 else "f16"
     c, t = int(bool(causal)), int(bool(tail))
     if (tile_m, tile_n) == (128, 64) and accum == TA_ACC_FP32 and head_dim <= 128:
-        return "attn_fwd_pp.hsaco", f"ta_fwd_pp_{dt}_d{head_dim}_c{c}_t{t}"
+        kind = "pp_split" if split else "pp"
+        return "attn_fwd_pp.hsaco", f"ta_fwd_{kind}_{dt}_d{head_dim}_c{c}_t{t}"
+    if split:
+        raise ValueError("split key ranges exist for tile (128, 64), fp32 accumulation, D <= 128")
     return (f"attn_fwd_m{tile_m}_n{tile_n}.hsaco",
             f"ta_fwd_{dt}_d{head_dim}_m{tile_m}_n{tile_n}_c{c}_t{t}_a{int(accum != TA_ACC_FP32)}")
 
@@ -48,6 +52,10 @@ EXPORTED_SYMBOLS = (
     "ta_set_code_object_dir",
     "ta_prepare",
     "ta_sdpa_fwd",
+    "ta_split_plan",
+    "ta_split_plan_model",
+    "ta_split_workspace_size",
+    "ta_sdpa_fwd_split",
     "ta_cache_reset",
     "ta_cache_size",
     "ta_last_error",
@@ -113,6 +121,15 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ta_prepare.restype = i32
     lib.ta_sdpa_fwd.argtypes = [ctypes.POINTER(FwdArgs), ctypes.c_void_p]
     lib.ta_sdpa_fwd.restype = i32
+    lib.ta_split_plan.argtypes = [ctypes.POINTER(FwdArgs), ctypes.POINTER(i32)]
+    lib.ta_split_plan.restype = i32
+    lib.ta_split_plan_model.argtypes = [ctypes.c_int64, ctypes.c_int64, i32, i32]
+    lib.ta_split_plan_model.restype = i32
+    lib.ta_split_workspace_size.argtypes = [ctypes.POINTER(FwdArgs), i32, ctypes.POINTER(ctypes.c_int64)]
+    lib.ta_split_workspace_size.restype = i32
+    lib.ta_sdpa_fwd_split.argtypes = [ctypes.POINTER(FwdArgs), i32, ctypes.c_void_p, ctypes.c_int64,
+                                      ctypes.c_void_p]
+    lib.ta_sdpa_fwd_split.restype = i32
     lib.ta_cache_reset.argtypes = []
     lib.ta_cache_reset.restype = i32
     lib.ta_cache_size.argtypes = []

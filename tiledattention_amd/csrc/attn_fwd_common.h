@@ -12,6 +12,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef short s16x4 __attribute__((__vector_size__(4 * sizeof(short))));
@@ -84,6 +85,7 @@ __device__ static inline void swap32(float x, float& a, float& b) {
 }
 
 __device__ static inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ static inline float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 
 // IEEE 754-2019 maximum (NaN-propagating): lowers to v_maximum3_f32 on gfx950 without the
 // operand canonicalisation fmaxf needs in IEEE mode.

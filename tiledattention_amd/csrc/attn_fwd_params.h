@@ -20,6 +20,13 @@ struct FwdParams {
   int32_t n_bh;        // B * H
   float scale_log2;    // softmax scale * log2(e)
   int32_t sched;       // block -> tile order: 0 plain, 1 XCD-grouped
+  // Split key ranges (split kernels and the merge kernel only; see SplitLayout).
+  float* part_o;       // [slots][128][D] fp32 partial outputs, each normalised by its own l
+  float* part_lse;     // [slots][128] log2 of the partial's softmax denominator, m*c + log2(l)
+  int32_t split_c;     // key steps (of 128 keys) per chunk
+  int32_t split_items; // work items per (b, h)
+  int32_t split_ns;    // chunks per query block (non-causal; causal derives it per block)
+  int32_t split_slots; // partial slots per (b, h)
 };
 
 }  // namespace ta

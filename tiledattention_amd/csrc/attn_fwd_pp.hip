@@ -34,6 +34,7 @@
 
 #include "attn_fwd_common.h"
 #include "attn_fwd_params.h"
+#include "attn_fwd_split.h"
 
 
 namespace ta {
@@ -52,7 +53,7 @@ __device__ static inline int pp_swz_v(int row) {
   return D == 128 ? ((row & 3) << 2) : (((row >> 1) & 1) << 2);
 }
 
-template <int DT, int D, bool CAUSAL, bool TAIL>
+template <int DT, int D, bool CAUSAL, bool TAIL, bool SPLIT>
 __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   constexpr int TM = 128;            // query rows per workgroup
   constexpr int TK = 128;            // keys per workgroup step (64 per wave group)
@@ -65,6 +66,7 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   constexpr int RPL = 1024 / RB;     // rows one wave instruction fills
   constexpr int NLD = STAGE / 1024 / 8;  // loads per wave per tensor per step (own half)
   static_assert(STAGE % (8 * 1024) == 0, "stage must split over the eight waves");
+  static_assert(TM == kPPRows && TK == kPPKeys, "grid numbering assumes 128 x 128 steps");
   using DTy = DType<DT>;
 
   // One array per (tensor, stage): the stage of every access is a compile-time constant
@@ -83,21 +85,23 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   const int l32 = lane & 31;
   const int hl = lane >> 5;
 
-  // ---- block -> (bh, q tile) ------------------------------------------------------
-  // One workgroup per CU (LDS and registers); the hardware hands block ids to the 8 XCDs
-  // round-robin, so with sched >= 1 consecutive logical tiles are regrouped onto one XCD
-  // (one head's K/V in one L2).  Causal tiles are issued heaviest first: each CU takes the
-  // next tile when its current one ends, which pairs heavy with light tiles.
+  // ---- block -> (bh, q tile, key steps) -------------------------------------------
+  // One workgroup per CU (LDS and registers).  The numbering (attn_fwd_split.h) regroups
+  // block ids per XCD with sched >= 1 (one head's K/V in one L2) and issues causal tiles
+  // heaviest first, so each CU takes the next tile when its current one ends and heavy
+  // tiles pair with light ones.  Split items cover a chunk of key steps of a block and
+  // leave a partial (slot >= 0) when the block has more than one chunk.
   const int nq = p.n_qblk;
-  const int total = nq * p.n_bh;
-  int lin = blockIdx.x;
-  if (p.sched >= 1 && (total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
-  const int bh = lin / nq;
-  const int j = lin - bh * nq;
-  const int qt = CAUSAL ? nq - 1 - j : j;
+  const int S = p.S;
+  const WorkItem wi = SPLIT ? split_item(blockIdx.x, p.n_bh, p.split_items, p.sched, CAUSAL,
+                                         p.split_c, p.split_ns, p.split_slots, S)
+                            : whole_item(blockIdx.x, p.n_bh, nq, p.sched, CAUSAL);
+  const int bh = wi.bh;
+  const int qt = wi.qt;
+  const int t_beg = wi.t_beg;
+  const int slot = wi.slot;
   const int b = bh / p.H;
   const int h = bh - b * p.H;
-  const int S = p.S;
 
   const uint16_t* __restrict__ qp = p.q + b * p.q_sb + h * p.q_sh;
   const uint16_t* __restrict__ kp = p.k + b * p.k_sb + h * p.k_sh;
@@ -111,8 +115,9 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   const int my_q = wq0 + l32;    // this lane's query row
 
   // ---- Q fragment: B operand of S^T = K Q^T, kept for the whole key loop ------------
+  // (loaded in the prologue, between the first key stage and the next stages)
   u32x4 qf[DK];
-  {
+  auto load_q = [&]() {
     const bool ok = !TAIL || my_q < S;
     const uint16_t* row = qp + (int64_t)(ok ? my_q : 0) * p.q_ss;
 #pragma unroll
@@ -120,11 +125,12 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
       u32x4 v = *(const u32x4*)(row + 16 * kk + 8 * hl);
       qf[kk] = ok ? v : u32x4{0, 0, 0, 0};
     }
-  }
+  };
 
   // ---- key range --------------------------------------------------------------------
-  const int kv_end = CAUSAL ? min(S, q0 + TM) : S;
-  const int n_steps = (kv_end + TK - 1) / TK;
+  // Steps [t_beg, t_end) of TK keys; without a split, every step up to the last key the
+  // block needs.
+  const int t_end = SPLIT ? wi.t_end : ((CAUSAL ? min(S, q0 + TM) : S) + TK - 1) / TK;
   const int wave_kv_end = CAUSAL ? min(S, wq0 + 32) : S;
   const int koff = 64 * grp;  // this wave's keys in a step: [TK * t + koff, + 64)
 
@@ -145,7 +151,7 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   const int vvo = ld_row * v_rb + ((ld_pc ^ pp_swz_v<D>(ld_row)) << 4);
   auto dma = [&](const uint16_t* gbase, int64_t row_stride, int rb, int vo, int t, char* stage) {
     const int row0 = t * TK;
-    const int rows = t < n_steps ? S - row0 : 0;
+    const int rows = t < t_end ? S - row0 : 0;
     const __amdgpu_buffer_rsrc_t r = row_rsrc(gbase + (int64_t)row0 * row_stride, rows, rb);
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
@@ -346,19 +352,21 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   // predecessor read last) and waits for them at the end of its next softmax cluster.
   // Both groups run the same sequence, group 1 one phase later.
   //
-  // Drain the Q-fragment loads first, on every path into the loop, so the waitcnt
-  // insertion does not carry a pending-load state into the loop.
-  __builtin_amdgcn_s_waitcnt(0);
-  dma(kp, p.k_ss, k_rb, kvo, 0, lds_k0);
-  wait_dma();
+  // Prologue: every wave issues its share of K_0, its Q fragment, and its group's halves of
+  // K_1 and V_0, then waits until at most the last 2 NLD loads (K_1 and V_0) are in flight:
+  // K_0 and Q have landed, and the latencies of all four overlap.  The Q fragment is
+  // complete before the loop on every path, so the waitcnt insertion carries no pending
+  // load into it.  K_1 and V_0 are waited for at the end of the group's first softmax
+  // cluster, like the loads of every MFMA cluster.
+  static_assert(2 * NLD < 16, "vmcnt field");
+  dma(kp, p.k_ss, k_rb, kvo, t_beg, lds_k0);
+  load_q();
+  dma(kp, p.k_ss, k_rb, kvo, t_beg + 1, lds_k1);
+  dma(vp, p.v_ss, v_rb, vvo, t_beg, lds_v0);
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * NLD));
   barrier();
-  // S_0, then this group's halves of K_1 and V_0 (waited for at the end of its first
-  // softmax cluster, like the loads of every MFMA cluster).
-  auto first = [&]() {
-    qk(lds_k0);
-    dma(kp, p.k_ss, k_rb, kvo, 1, lds_k1);
-    dma(vp, p.v_ss, v_rb, vvo, 0, lds_v0);
-  };
+  // S_0.
+  auto first = [&]() { qk(lds_k0); };
 
   // Step t with stage parity PAR: the stages of K_t (consumed; receives K_{t+2}), K_{t+1},
   // V_t and V_{t-1} (consumed; receives V_{t+1}).
@@ -388,18 +396,18 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   if (grp == 0) {
     first();
     barrier();
-    for (int t = 0; t < n_steps; t += 2) {
+    for (int t = t_beg; t < t_end; t += 2) {
       iter(t, std::integral_constant<int, 0>{});
-      if (t + 1 < n_steps) iter(t + 1, std::integral_constant<int, 1>{});
+      if (t + 1 < t_end) iter(t + 1, std::integral_constant<int, 1>{});
     }
     barrier();  // phase 2 n_steps + 1: group 1's last MFMA cluster
   } else {
     barrier();  // phase 0: group 0's S_0
     first();
     barrier();
-    for (int t = 0; t < n_steps; t += 2) {
+    for (int t = t_beg; t < t_end; t += 2) {
       iter(t, std::integral_constant<int, 0>{});
-      if (t + 1 < n_steps) iter(t + 1, std::integral_constant<int, 1>{});
+      if (t + 1 < t_end) iter(t + 1, std::integral_constant<int, 1>{});
     }
   }
   wait_dma();  // the zero-filling loads of the last two steps, before the merge reuses LDS
@@ -422,8 +430,16 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   }
   barrier();
   if (grp == 1) return;
+  // Group 1's O^T: every LDS read issued before the first use, so their latencies overlap.
+  float x1[DB][16];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) x1[db][r] = xo[(db * 16 + r) * 64 + lane];
+  }
   const float m1 = xml[lane];
   const float l1 = xml[64 + lane];
+  __builtin_amdgcn_sched_barrier(0);
   const float m = vmax(m_run, m1);
   const float a0 = fast_exp2((m_run - m) * c);
   const float a1 = fast_exp2((m1 - m) * c);
@@ -433,6 +449,26 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   if (TAIL && my_q >= S) return;
   const float inv = 1.0f / l_tot;
   const float w0s = a0 * inv, w1s = a1 * inv;
+  if (SPLIT && slot >= 0) {
+    // One chunk of a split block: its output normalised by its own l, in fp32, and
+    // log2 of its softmax denominator in units of the scaled scores, m c + log2(l).
+    float* prow = p.part_o + ((int64_t)slot * TM + (my_q - q0)) * D;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        f32x4 o4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * g + e;
+          o4[e] = o_acc[db][r] * w0s + x1[db][r] * w1s;
+        }
+        *(f32x4*)(prow + 32 * db + 8 * g + 4 * hl) = o4;
+      }
+    }
+    if (hl == 0) p.part_lse[(int64_t)slot * TM + (my_q - q0)] = m * c + fast_log2(l_tot);
+    return;
+  }
   uint16_t* orow = op + (int64_t)my_q * p.o_ss;
 #pragma unroll
   for (int db = 0; db < DB; ++db) {
@@ -442,7 +478,7 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int r = 4 * g + e;
-        o4[e] = o_acc[db][r] * w0s + xo[(db * 16 + r) * 64 + lane] * w1s;
+        o4[e] = o_acc[db][r] * w0s + x1[db][r] * w1s;
       }
       const uint32_t w0 = DTy::pack(o4[0], o4[1]);
       const uint32_t w1 = DTy::pack(o4[2], o4[3]);
@@ -452,22 +488,85 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   }
 }
 
+// Merge of the chunks of one split query block (after the split kernel on the same
+// stream): per row, with L_i the chunks' log-sum-exps, O = sum_i 2^(L_i - max L) O_i /
+// sum_i 2^(L_i - max L), the same rescale the online softmax applies between key tiles,
+// here folded into one pass over the chunks (running max, weights rescaled when it grows).
+// One thread per (row, 16-byte output chunk): a workgroup of 256 threads covers 256 / (D/8)
+// rows, so a split block takes 128 / (256 / (D/8)) workgroups; the partial reads of the
+// chunks are independent and contiguous across the D/8 threads of a row, and a row is
+// written by those threads as one contiguous run.
+template <int DT, int D, bool CAUSAL>
+__device__ __forceinline__ void attn_merge_body(const FwdParams& p) {
+  constexpr int TM = kPPRows;
+  constexpr int CH = D / 8;        // 16-byte output chunks per row
+  constexpr int RPW = 256 / CH;    // rows per workgroup
+  constexpr int WPB = TM / RPW;    // workgroups per split block
+  static_assert(256 % CH == 0 && TM % RPW == 0, "workgroups must cover whole rows");
+  using DTy = DType<DT>;
+  const int blk = blockIdx.x / WPB;
+  const MergeItem mi = merge_item(blk, p.n_qblk, CAUSAL, p.split_c, p.split_ns, p.split_slots);
+  const int row = (blockIdx.x - blk * WPB) * RPW + threadIdx.x / CH;
+  const int c8 = threadIdx.x % CH;
+  const int q = mi.qt * TM + row;
+  if (q >= p.S) return;
+  const int b = mi.bh / p.H;
+  const int h = mi.bh - b * p.H;
+  const float* lse = p.part_lse + (int64_t)mi.slot0 * TM + row;
+  const float* po = p.part_o + ((int64_t)mi.slot0 * TM + row) * D + 8 * c8;
+  float mx = lse[0];
+  f32x4 acc0 = *(const f32x4*)po;
+  f32x4 acc1 = *(const f32x4*)(po + 4);
+  float wsum = 1.0f;
+  for (int i = 1; i < mi.ns; ++i) {
+    const float li = lse[i * TM];
+    const f32x4 x0 = *(const f32x4*)(po + (int64_t)i * TM * D);
+    const f32x4 x1 = *(const f32x4*)(po + (int64_t)i * TM * D + 4);
+    const float m_new = vmax(mx, li);
+    const float a = fast_exp2(mx - m_new);  // rescale of what is summed so far
+    const float w = fast_exp2(li - m_new);
+    mx = m_new;
+    wsum = wsum * a + w;
+    acc0 = acc0 * a + w * x0;
+    acc1 = acc1 * a + w * x1;
+  }
+  const float inv = 1.0f / wsum;
+  const u32x4 o = {DTy::pack(acc0[0] * inv, acc0[1] * inv), DTy::pack(acc0[2] * inv, acc0[3] * inv),
+                   DTy::pack(acc1[0] * inv, acc1[1] * inv), DTy::pack(acc1[2] * inv, acc1[3] * inv)};
+  *(u32x4*)(p.o + b * p.o_sb + h * p.o_sh + (int64_t)q * p.o_ss + 8 * c8) = o;
+}
+
 }  // namespace ta
 
-// One extern "C" entry per (dtype, D, causal, tail).
-// Name: ta_fwd_pp_<f16|bf16>_d<D>_c<0|1>_t<0|1>; 512 threads, one workgroup per CU.
+// Two extern "C" entries per (dtype, D, causal, tail): the whole-row kernel
+// ta_fwd_pp_<f16|bf16>_d<D>_c<0|1>_t<0|1> and the split-key-range kernel
+// ta_fwd_pp_split_<...>; 512 threads, one workgroup per CU.
 #define TA_PP_DEFINE(DTN, DT, D, C, T)                                                    \
   extern "C" __global__ void __launch_bounds__(512)                                       \
       __attribute__((amdgpu_waves_per_eu(2, 2))) ta_fwd_pp_##DTN##_d##D##_c##C##_t##T(     \
           ta::FwdParams p) {                                                              \
-    ta::attn_fwd_pp_body<DT, D, (C != 0), (T != 0)>(p);                                   \
+    ta::attn_fwd_pp_body<DT, D, (C != 0), (T != 0), false>(p);                            \
+  }                                                                                       \
+  extern "C" __global__ void __launch_bounds__(512)                                       \
+      __attribute__((amdgpu_waves_per_eu(2, 2)))                                          \
+      ta_fwd_pp_split_##DTN##_d##D##_c##C##_t##T(ta::FwdParams p) {                        \
+    ta::attn_fwd_pp_body<DT, D, (C != 0), (T != 0), true>(p);                             \
+  }
+
+// Merge kernels of the split path: ta_fwd_merge_<f16|bf16>_d<D>_c<0|1>, 256 threads.
+#define TA_MERGE_DEFINE(DTN, DT, D, C)                                                     \
+  extern "C" __global__ void __launch_bounds__(256) ta_fwd_merge_##DTN##_d##D##_c##C(      \
+      ta::FwdParams p) {                                                                  \
+    ta::attn_merge_body<DT, D, (C != 0)>(p);                                              \
   }
 
 #define TA_PP_DEFINE_CT(DTN, DT, D) \
   TA_PP_DEFINE(DTN, DT, D, 0, 0)    \
   TA_PP_DEFINE(DTN, DT, D, 0, 1)    \
   TA_PP_DEFINE(DTN, DT, D, 1, 0)    \
-  TA_PP_DEFINE(DTN, DT, D, 1, 1)
+  TA_PP_DEFINE(DTN, DT, D, 1, 1)    \
+  TA_MERGE_DEFINE(DTN, DT, D, 0)    \
+  TA_MERGE_DEFINE(DTN, DT, D, 1)
 
 TA_PP_DEFINE_CT(f16, 0, 64)
 TA_PP_DEFINE_CT(f16, 0, 128)

@@ -1,0 +1,178 @@
+// Work numbering of the eight-wave kernel's grid (attn_fwd_pp.hip): which query block and
+// which key steps a workgroup takes, for the whole-row grid and for split key ranges, and
+// which partials the merge kernel combines.  Compiled into the kernels, the host launcher
+// (grid sizes, workspace, dispatch model) and a host-only test, so all of them use one
+// numbering.
+#pragma once
+#include <stdint.h>
+
+#if defined(__HIPCC__)
+#define TA_HD __host__ __device__
+#else
+#define TA_HD
+#endif
+
+namespace ta {
+
+constexpr int kPPRows = 128;  // query rows per block
+constexpr int kPPKeys = 128;  // keys per step
+
+// Split key ranges with chunks of C steps: a query block with `len` key steps is cut
+// into ns = ceil(len / C) chunks counted back from its last step (chunk 0 takes the
+// remainder), one work item each.  Causal block qt has qt + 1 steps, so blocks
+// [a C, (a + 1) C) have a + 1 chunks each; non-causal blocks all have the same ns.
+struct SplitLayout {
+  int64_t items = 0;  // work items per (b, h)
+  int64_t ns = 0;     // chunks per block (non-causal; 0 for causal)
+  int64_t slots = 0;  // partial slots per (b, h)
+  int64_t merge = 0;  // blocks of more than one chunk per (b, h)
+};
+
+// Items of causal blocks [0, x).
+TA_HD inline int64_t split_causal_items(int64_t x, int64_t c) {
+  const int64_t a = x / c, b = x - a * c;
+  return c * a * (a + 1) / 2 + b * (a + 1);
+}
+
+// False when chunks of c steps split nothing (every block fits in one chunk).
+TA_HD inline bool split_layout(int64_t S, bool causal, int64_t c, SplitLayout* out) {
+  const int64_t nq = (S + kPPRows - 1) / kPPRows;
+  const int64_t len = (S + kPPKeys - 1) / kPPKeys;
+  if (c < 1) return false;
+  if (causal) {
+    if (nq <= c) return false;
+    out->items = split_causal_items(nq, c);
+    out->ns = 0;
+    out->slots = out->items - c;  // blocks 0 .. C-1 are one chunk each
+    out->merge = nq - c;
+  } else {
+    const int64_t ns = (len + c - 1) / c;
+    if (ns <= 1) return false;
+    out->items = nq * ns;
+    out->ns = ns;
+    out->slots = out->items;
+    out->merge = nq;
+  }
+  return true;
+}
+
+// Block id -> (b*h, rank r of the item within its head, 0 = issued first) for a grid of
+// n_bh * per_head items with sched >= 1 and a total divisible by 8.  The hardware hands
+// block ids to the 8 XCDs round-robin (XCD = id % 8, k-th block of that XCD = id / 8), and
+// each XCD runs its blocks in k order on whichever CU frees first:
+// * n_bh = 1, 2 or 4: head h gets XCDs [h X, (h + 1) X), X = 8 / n_bh, and its items are
+//   dealt out round-robin over them in rank order, so every XCD gets heavy and light items
+//   of one head (balanced work, the head's K/V in those XCDs' L2);
+// * otherwise each XCD gets a contiguous run of total / 8 items, whole heads when 8 | n_bh.
+TA_HD inline void xcd_order(int blk, int n_bh, int per_head, int* bh, int* r) {
+  const int total = n_bh * per_head;
+  const int x = blk & 7, k = blk >> 3;
+  if (n_bh < 8 && (8 % n_bh) == 0) {
+    const int X = 8 / n_bh;
+    *bh = x / X;
+    *r = k * X + (x - *bh * X);
+  } else {
+    const int lin = x * (total >> 3) + k;
+    *bh = lin / per_head;
+    *r = lin - *bh * per_head;
+  }
+}
+
+struct WorkItem {
+  int bh;     // b * H + h
+  int qt;     // query block
+  int t_beg;  // key steps [t_beg, t_end); t_end = -1 for "every step the block needs"
+  int t_end;
+  int slot;   // partial slot, or -1 when the item is the block's only chunk
+};
+
+// Whole-row grid: one item per (b, h, query block); causal blocks are ranked heaviest
+// (longest key range) first.  sched >= 1 (with 8 | total) maps block ids per XCD as
+// xcd_order describes; otherwise block ids run head by head.
+TA_HD inline WorkItem whole_item(int blk, int n_bh, int nq, int sched, bool causal) {
+  const int total = nq * n_bh;
+  WorkItem w;
+  int j;
+  if (sched >= 1 && (total & 7) == 0) {
+    xcd_order(blk, n_bh, nq, &w.bh, &j);
+  } else {
+    w.bh = blk / nq;
+    j = blk - w.bh * nq;
+  }
+  w.qt = causal ? nq - 1 - j : j;
+  w.t_beg = 0;
+  w.t_end = -1;
+  w.slot = -1;
+  return w;
+}
+
+// Split grid: `items` per (b, h), ranked from the heaviest block down; sched >= 1 (with
+// 8 | total) maps block ids per XCD as xcd_order describes, otherwise block ids run
+// item-major across heads (heavy items of every head first).  A block of more than one
+// chunk leaves chunk `part` in slot bh * slots + (item - C) (causal) or bh * slots + item
+// (non-causal).
+TA_HD inline WorkItem split_item(int blk, int n_bh, int items, int sched, bool causal, int c,
+                                 int ns_nc, int slots, int S) {
+  const int total = items * n_bh;
+  int r;
+  WorkItem w;
+  if (sched >= 1 && (total & 7) == 0) {
+    xcd_order(blk, n_bh, items, &w.bh, &r);
+  } else {
+    r = blk / n_bh;
+    w.bh = blk - r * n_bh;
+  }
+  const int item = items - 1 - r;  // counted from the lightest block up
+  int len, ns, part;
+  if (causal) {
+    int a = 0;
+    while (c * (a + 1) * (a + 2) / 2 <= item) ++a;
+    const int off = item - c * a * (a + 1) / 2;
+    const int q = off / (a + 1);
+    w.qt = a * c + q;
+    part = off - q * (a + 1);
+    ns = a + 1;
+    len = w.qt + 1;
+    w.slot = item - c;
+  } else {
+    ns = ns_nc;
+    w.qt = item / ns;
+    part = item - w.qt * ns;
+    len = (S + kPPKeys - 1) / kPPKeys;
+    w.slot = item;
+  }
+  w.t_beg = part == 0 ? 0 : len - (ns - part) * c;
+  w.t_end = len - (ns - 1 - part) * c;
+  w.slot = ns > 1 ? w.bh * slots + w.slot : -1;
+  return w;
+}
+
+struct MergeItem {
+  int bh;
+  int qt;
+  int ns;     // chunks
+  int slot0;  // slot of chunk 0; chunk i is in slot0 + i
+};
+
+// Merge grid: one block per (b, h, split query block): causal blocks qt >= C, or every
+// non-causal block.
+TA_HD inline MergeItem merge_item(int blk, int nq, bool causal, int c, int ns_nc, int slots) {
+  const int nsb = causal ? nq - c : nq;
+  MergeItem m;
+  m.bh = blk / nsb;
+  const int idx = blk - m.bh * nsb;
+  if (causal) {
+    m.qt = c + idx;
+    const int a = m.qt / c;
+    m.ns = a + 1;
+    m.slot0 = (int)split_causal_items(m.qt, c) - c;
+  } else {
+    m.qt = idx;
+    m.ns = ns_nc;
+    m.slot0 = m.qt * ns_nc;
+  }
+  m.slot0 += m.bh * slots;
+  return m;
+}
+
+}  // namespace ta

@@ -13,15 +13,21 @@
 #include <dlfcn.h>
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <functional>
 #include <map>
 #include <mutex>
+#include <queue>
 #include <string>
+#include <tuple>
+#include <vector>
 
 #include "../../include/tiledattn.h"
 #include "attn_fwd_params.h"
+#include "attn_fwd_split.h"
 
 namespace {
 
@@ -169,6 +175,173 @@ ta_status get_function_locked(int device, const KernelId& id, hipFunction_t* out
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// ---- split key ranges ------------------------------------------------------------------
+// The eight-wave kernel (128 query rows, steps of 128 keys) can cut each query block's key
+// range into chunks of C steps counted back from its last step; every chunk is one
+// workgroup, and blocks of more than one chunk are combined by the merge kernel from
+// fp32 partials in a caller-provided workspace.  The numbering below is the one the
+// kernels derive from their block id (attn_fwd_pp.hip).
+using ta::SplitLayout;
+using ta::split_layout;
+constexpr int kSplitRows = ta::kPPRows;
+
+// Workspace: fp32 partial outputs [slots][128][D], then the log-sum-exps [slots][128].
+int64_t split_ws_bytes(int64_t n_bh, int64_t d, const SplitLayout& l) {
+  const int64_t rows = n_bh * l.slots * kSplitRows;
+  const int64_t o_bytes = (rows * d * 4 + 255) / 256 * 256;
+  return o_bytes + rows * 4;
+}
+
+// Finish time of the slowest CU when the grid (split with chunks of c steps, or the
+// whole-row grid for c = 0) is dispatched onto `ncu` CUs holding one workgroup each, in
+// units of one key step of a lightly loaded chip.  The hardware hands block ids to the 8
+// XCDs round-robin and each XCD starts its blocks in id order on whichever CU frees first.
+// An item costs its steps, slower the more CUs the grid keeps busy (clock and memory
+// contention), plus a fixed cost (launch, Q and first K/V loads, pipeline fill and drain,
+// merge of the two key halves, output stores); a split grid adds the merge kernel, whose
+// cost grows with the partial slots it reads.  Constants fitted to MI355X timings of the
+// eight-wave kernel (B*H 1-16, S 1024-16384, causal and not).
+double simulate_split(int64_t S, int64_t n_bh, bool causal, int64_t c, int ncu) {
+  const double kItem = 10.0, kLoad = 0.5, kMerge = 6.0, kMergeSlot = 1.0;
+  const int nq = (int)((S + ta::kPPRows - 1) / ta::kPPRows);
+  const int len = (int)((S + ta::kPPKeys - 1) / ta::kPPKeys);
+  SplitLayout l;
+  const bool split = split_layout(S, causal, c, &l);
+  const int64_t total = split ? n_bh * l.items : n_bh * nq;
+  const int xcds = 8;
+  const int per_xcd = std::max(1, ncu / xcds);
+  const double step = 1.0 + kLoad * (double)std::min<int64_t>(total, ncu) / ncu;
+  std::vector<std::priority_queue<double, std::vector<double>, std::greater<double>>> cu(xcds);
+  for (auto& q : cu)
+    for (int i = 0; i < per_xcd; ++i) q.push(0.0);
+  for (int64_t blk = 0; blk < total; ++blk) {
+    const ta::WorkItem w =
+        split ? ta::split_item((int)blk, (int)n_bh, (int)l.items, 1, causal, (int)c, (int)l.ns,
+                               (int)l.slots, (int)S)
+              : ta::whole_item((int)blk, (int)n_bh, nq, 1, causal);
+    const int t_end = w.t_end >= 0 ? w.t_end : (causal ? w.qt + 1 : len);
+    auto& q = cu[blk % xcds];
+    const double t = q.top();
+    q.pop();
+    q.push(t + (t_end - w.t_beg) * step + kItem);
+  }
+  double worst = 0.0;
+  for (auto& q : cu) {
+    while (q.size() > 1) q.pop();
+    worst = std::max(worst, q.top());
+  }
+  return worst + (split ? kMerge + kMergeSlot * (double)(n_bh * l.slots) / ncu : 0.0);
+}
+
+std::map<int, int> g_cu_count;  // device -> compute units
+std::map<std::tuple<int64_t, int64_t, int, int>, int32_t> g_plans;
+
+// Caller holds g_mu and has made `device` current.
+ta_status cu_count_locked(int device, int* out) {
+  auto it = g_cu_count.find(device);
+  if (it != g_cu_count.end()) {
+    *out = it->second;
+    return TA_OK;
+  }
+  int n = 0;
+  hipError_t e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device);
+  if (e != hipSuccess)
+    return fail(TA_EHIP, "hipDeviceGetAttribute(%d): %s", device, hipGetErrorString(e));
+  g_cu_count[device] = n;
+  *out = n;
+  return TA_OK;
+}
+
+// Chunk length (key steps) with the earliest simulated finish, or 0 when no split beats
+// the whole-row grid by 20 % (the model's error on the fitted timings stays below that).
+// Grids of several waves of workgroups balance by themselves and are not split.
+int32_t plan_split(int64_t S, int64_t n_bh, bool causal, int ncu) {
+  const int64_t nq = (S + kSplitRows - 1) / kSplitRows;
+  const int64_t len = (S + ta::kPPKeys - 1) / ta::kPPKeys;
+  if (ncu < 8 || n_bh * nq > 4 * (int64_t)ncu) return 0;
+  const double base = simulate_split(S, n_bh, causal, 0, ncu);
+  double best = base * 0.8;
+  int32_t best_c = 0;
+  for (int64_t c = 1; c < len; ++c) {
+    SplitLayout l;
+    if (!split_layout(S, causal, c, &l)) continue;
+    if (l.items * n_bh > 8 * (int64_t)ncu) continue;  // more items than waves help
+    const double t = simulate_split(S, n_bh, causal, c, ncu);
+    if (t < best) {
+      best = t;
+      best_c = (int32_t)c;
+    }
+  }
+  return best_c;
+}
+
+// Checks shared by every entry point that takes ta_fwd_args.  Fills the grid size.  The
+// planning queries (launch = false) need only the shape fields, not tensors or strides.
+ta_status validate_args(const ta_fwd_args* a, int64_t* n_bh_out, int64_t* n_qblk_out,
+                        bool launch = true) {
+  if (a == nullptr) return fail(TA_EINVAL, "args is NULL");
+  if (a->dtype != TA_FP16 && a->dtype != TA_BF16) return fail(TA_EINVAL, "dtype %d", a->dtype);
+  if (a->accum != TA_ACC_FP32 && a->accum != TA_ACC_INPUT)
+    return fail(TA_EINVAL, "accum %d", a->accum);
+  if (a->causal != 0 && a->causal != 1) return fail(TA_EINVAL, "causal %d", a->causal);
+  if (a->sched < 0 || a->sched > 2) return fail(TA_EINVAL, "sched %d", a->sched);
+  if (a->B < 0 || a->H < 0 || a->S < 0) return fail(TA_EINVAL, "negative shape");
+  ta_status shape_st = check_shape(a->D, a->tile_m, a->tile_n);
+  if (shape_st != TA_OK) return shape_st;
+  *n_bh_out = a->B * a->H;
+  *n_qblk_out = 0;
+  if (a->B == 0 || a->H == 0 || a->S == 0) return TA_OK;
+  if (a->S > 0x7fffffffLL || a->H > 0x7fffffffLL) return fail(TA_EINVAL, "S or H too large");
+  const int64_t n_bh = a->B * a->H;
+  const int64_t n_qblk = (a->S + a->tile_m - 1) / a->tile_m;
+  if (n_bh > 0x7fffffffLL || n_bh * n_qblk > 0x7fffffffLL)
+    return fail(TA_EINVAL, "grid too large (B*H*ceil(S/TM) must fit in int32)");
+  if (!launch) {
+    *n_qblk_out = n_qblk;
+    return TA_OK;
+  }
+  if (!a->q || !a->k || !a->v || !a->o) return fail(TA_EINVAL, "null tensor pointer");
+  if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->o))
+    return fail(TA_EINVAL, "q/k/v/o must be 16-byte aligned");
+  const int64_t* st[4] = {a->q_stride, a->k_stride, a->v_stride, a->o_stride};
+  const char* nm[4] = {"q", "k", "v", "o"};
+  for (int i = 0; i < 4; ++i) {
+    if (st[i][3] != 1) return fail(TA_EINVAL, "%s: last-dim stride must be 1", nm[i]);
+    for (int j = 0; j < 3; ++j)
+      if (st[i][j] < 0 || (st[i][j] & 7) != 0)
+        return fail(TA_EINVAL, "%s: stride[%d]=%lld must be a non-negative multiple of 8", nm[i], j,
+                    (long long)st[i][j]);
+  }
+  // K and V are read with buffer instructions whose byte range is 32-bit.
+  if (a->S * a->k_stride[2] * 2 > 0x7fffffffLL || a->S * a->v_stride[2] * 2 > 0x7fffffffLL)
+    return fail(TA_EINVAL, "k/v: S * row stride must stay below 2^31 bytes per (b, h) slice");
+  *n_qblk_out = n_qblk;
+  return TA_OK;
+}
+
+void fill_params(const ta_fwd_args* a, int64_t n_bh, int64_t n_qblk, ta::FwdParams* p) {
+  memset(p, 0, sizeof(*p));
+  p->q = static_cast<const uint16_t*>(a->q);
+  p->k = static_cast<const uint16_t*>(a->k);
+  p->v = static_cast<const uint16_t*>(a->v);
+  p->o = static_cast<uint16_t*>(a->o);
+  p->q_sb = a->q_stride[0]; p->q_sh = a->q_stride[1]; p->q_ss = a->q_stride[2];
+  p->k_sb = a->k_stride[0]; p->k_sh = a->k_stride[1]; p->k_ss = a->k_stride[2];
+  p->v_sb = a->v_stride[0]; p->v_sh = a->v_stride[1]; p->v_ss = a->v_stride[2];
+  p->o_sb = a->o_stride[0]; p->o_sh = a->o_stride[1]; p->o_ss = a->o_stride[2];
+  p->H = static_cast<int32_t>(a->H);
+  p->S = static_cast<int32_t>(a->S);
+  p->n_qblk = static_cast<int32_t>(n_qblk);
+  p->n_bh = static_cast<int32_t>(n_bh);
+  p->scale_log2 = static_cast<float>(static_cast<double>(a->scale) * 1.4426950408889634);
+  p->sched = a->sched;
+}
+
+// Whether the split path exists for this configuration (the eight-wave kernel).
+bool split_capable(const ta_fwd_args* a) {
+  return a->tile_m == kSplitRows && a->tile_n == 64 && a->accum == TA_ACC_FP32 && a->D <= 128;
+}
+
 }  // namespace
 
 extern "C" {
@@ -231,36 +404,9 @@ ta_status ta_prepare(int32_t device, int32_t dtype, int32_t head_dim, int32_t ti
 }
 
 ta_status ta_sdpa_fwd(const ta_fwd_args* a, void* stream) {
-  if (a == nullptr) return fail(TA_EINVAL, "args is NULL");
-  if (a->dtype != TA_FP16 && a->dtype != TA_BF16) return fail(TA_EINVAL, "dtype %d", a->dtype);
-  if (a->accum != TA_ACC_FP32 && a->accum != TA_ACC_INPUT)
-    return fail(TA_EINVAL, "accum %d", a->accum);
-  if (a->causal != 0 && a->causal != 1) return fail(TA_EINVAL, "causal %d", a->causal);
-  if (a->sched < 0 || a->sched > 2) return fail(TA_EINVAL, "sched %d", a->sched);
-  if (a->B < 0 || a->H < 0 || a->S < 0) return fail(TA_EINVAL, "negative shape");
-  ta_status shape_st = check_shape(a->D, a->tile_m, a->tile_n);
-  if (shape_st != TA_OK) return shape_st;
-  if (a->B == 0 || a->H == 0 || a->S == 0) return TA_OK;
-  if (!a->q || !a->k || !a->v || !a->o) return fail(TA_EINVAL, "null tensor pointer");
-  if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->o))
-    return fail(TA_EINVAL, "q/k/v/o must be 16-byte aligned");
-  const int64_t* st[4] = {a->q_stride, a->k_stride, a->v_stride, a->o_stride};
-  const char* nm[4] = {"q", "k", "v", "o"};
-  for (int i = 0; i < 4; ++i) {
-    if (st[i][3] != 1) return fail(TA_EINVAL, "%s: last-dim stride must be 1", nm[i]);
-    for (int j = 0; j < 3; ++j)
-      if (st[i][j] < 0 || (st[i][j] & 7) != 0)
-        return fail(TA_EINVAL, "%s: stride[%d]=%lld must be a non-negative multiple of 8", nm[i], j,
-                    (long long)st[i][j]);
-  }
-  if (a->S > 0x7fffffffLL || a->H > 0x7fffffffLL) return fail(TA_EINVAL, "S or H too large");
-  // K and V are read with buffer instructions whose byte range is 32-bit.
-  if (a->S * a->k_stride[2] * 2 > 0x7fffffffLL || a->S * a->v_stride[2] * 2 > 0x7fffffffLL)
-    return fail(TA_EINVAL, "k/v: S * row stride must stay below 2^31 bytes per (b, h) slice");
-  const int64_t n_bh = a->B * a->H;
-  const int64_t n_qblk = (a->S + a->tile_m - 1) / a->tile_m;
-  if (n_bh > 0x7fffffffLL || n_bh * n_qblk > 0x7fffffffLL)
-    return fail(TA_EINVAL, "grid too large (B*H*ceil(S/TM) must fit in int32)");
+  int64_t n_bh = 0, n_qblk = 0;
+  ta_status vst = validate_args(a, &n_bh, &n_qblk);
+  if (vst != TA_OK || n_qblk == 0) return vst;
 
   const bool aligned = (a->S % a->tile_m == 0) && (a->S % a->tile_n == 0);
   const KernelId id =
@@ -276,20 +422,7 @@ ta_status ta_sdpa_fwd(const ta_fwd_args* a, void* stream) {
   }
 
   ta::FwdParams p;
-  p.q = static_cast<const uint16_t*>(a->q);
-  p.k = static_cast<const uint16_t*>(a->k);
-  p.v = static_cast<const uint16_t*>(a->v);
-  p.o = static_cast<uint16_t*>(a->o);
-  p.q_sb = a->q_stride[0]; p.q_sh = a->q_stride[1]; p.q_ss = a->q_stride[2];
-  p.k_sb = a->k_stride[0]; p.k_sh = a->k_stride[1]; p.k_ss = a->k_stride[2];
-  p.v_sb = a->v_stride[0]; p.v_sh = a->v_stride[1]; p.v_ss = a->v_stride[2];
-  p.o_sb = a->o_stride[0]; p.o_sh = a->o_stride[1]; p.o_ss = a->o_stride[2];
-  p.H = static_cast<int32_t>(a->H);
-  p.S = static_cast<int32_t>(a->S);
-  p.n_qblk = static_cast<int32_t>(n_qblk);
-  p.n_bh = static_cast<int32_t>(n_bh);
-  p.scale_log2 = static_cast<float>(static_cast<double>(a->scale) * 1.4426950408889634);
-  p.sched = a->sched;
+  fill_params(a, n_bh, n_qblk, &p);
 
   DeviceGuard guard(a->device);
   if (guard.err != hipSuccess)
@@ -298,6 +431,114 @@ ta_status ta_sdpa_fwd(const ta_fwd_args* a, void* stream) {
   const unsigned grid = static_cast<unsigned>(n_bh * n_qblk);
   hipError_t e = hipModuleLaunchKernel(fn, grid, 1, 1, id.block, 1, 1, 0,
                                        static_cast<hipStream_t>(stream), params, nullptr);
+  if (e != hipSuccess) return fail(TA_EHIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
+  return TA_OK;
+}
+
+ta_status ta_split_plan(const ta_fwd_args* a, int32_t* chunk_steps) {
+  if (chunk_steps == nullptr) return fail(TA_EINVAL, "chunk_steps is NULL");
+  *chunk_steps = 0;
+  int64_t n_bh = 0, n_qblk = 0;
+  ta_status vst = validate_args(a, &n_bh, &n_qblk, false);
+  if (vst != TA_OK || n_qblk == 0 || !split_capable(a)) return vst;
+  std::lock_guard<std::mutex> lock(g_mu);
+  DeviceGuard guard(a->device);
+  if (guard.err != hipSuccess)
+    return fail(TA_EHIP, "set device %d: %s", a->device, hipGetErrorString(guard.err));
+  int ncu = 0;
+  ta_status cst = cu_count_locked(a->device, &ncu);
+  if (cst != TA_OK) return cst;
+  const auto key = std::make_tuple(a->S, n_bh, (int)a->causal, ncu);
+  auto it = g_plans.find(key);
+  if (it == g_plans.end())
+    it = g_plans.emplace(key, plan_split(a->S, n_bh, a->causal != 0, ncu)).first;
+  *chunk_steps = it->second;
+  return TA_OK;
+}
+
+int32_t ta_split_plan_model(int64_t S, int64_t n_bh, int32_t causal, int32_t compute_units) {
+  if (S <= 0 || n_bh <= 0 || compute_units <= 0 || S > 0x7fffffffLL || n_bh > 0x7fffffffLL)
+    return 0;
+  return plan_split(S, n_bh, causal != 0, compute_units);
+}
+
+ta_status ta_split_workspace_size(const ta_fwd_args* a, int32_t chunk_steps, int64_t* bytes) {
+  if (bytes == nullptr) return fail(TA_EINVAL, "bytes is NULL");
+  *bytes = 0;
+  if (chunk_steps < 0) return fail(TA_EINVAL, "chunk_steps %d", chunk_steps);
+  int64_t n_bh = 0, n_qblk = 0;
+  ta_status vst = validate_args(a, &n_bh, &n_qblk, false);
+  if (vst != TA_OK || n_qblk == 0 || chunk_steps == 0) return vst;
+  if (!split_capable(a))
+    return fail(TA_EUNSUPPORTED, "split key ranges need tile (128, 64), fp32 accumulation, D <= 128");
+  SplitLayout l;
+  if (split_layout(a->S, a->causal != 0, chunk_steps, &l)) *bytes = split_ws_bytes(n_bh, a->D, l);
+  return TA_OK;
+}
+
+ta_status ta_sdpa_fwd_split(const ta_fwd_args* a, int32_t chunk_steps, void* workspace,
+                            int64_t workspace_bytes, void* stream) {
+  if (chunk_steps < 0) return fail(TA_EINVAL, "chunk_steps %d", chunk_steps);
+  int64_t n_bh = 0, n_qblk = 0;
+  ta_status vst = validate_args(a, &n_bh, &n_qblk);
+  if (vst != TA_OK || n_qblk == 0) return vst;
+  SplitLayout l;
+  if (chunk_steps == 0 || !split_layout(a->S, a->causal != 0, chunk_steps, &l))
+    return ta_sdpa_fwd(a, stream);
+  if (!split_capable(a))
+    return fail(TA_EUNSUPPORTED, "split key ranges need tile (128, 64), fp32 accumulation, D <= 128");
+  const int64_t need = split_ws_bytes(n_bh, a->D, l);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(TA_EINVAL, "workspace of %lld bytes needed, %lld given", (long long)need,
+                (long long)(workspace == nullptr ? 0 : workspace_bytes));
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+    return fail(TA_EINVAL, "workspace must be 256-byte aligned");
+  if (n_bh * l.items > 0x7fffffffLL || n_bh * l.slots * kSplitRows > 0x7fffffffLL ||
+      n_bh * l.merge * kSplitRows > 0x7fffffffLL)
+    return fail(TA_EINVAL, "split grid too large");
+
+  const bool aligned = (a->S % a->tile_m == 0) && (a->S % a->tile_n == 0);
+  const char* dt = a->dtype == TA_BF16 ? "bf16" : "f16";
+  char name[96];
+  snprintf(name, sizeof(name), "ta_fwd_pp_split_%s_d%d_c%d_t%d", dt, (int)a->D, a->causal ? 1 : 0,
+           aligned ? 0 : 1);
+  const KernelId sid{"attn_fwd_pp.hsaco", name, 512u};
+  snprintf(name, sizeof(name), "ta_fwd_merge_%s_d%d_c%d", dt, (int)a->D, a->causal ? 1 : 0);
+  const KernelId mid{"attn_fwd_pp.hsaco", name, 256u};
+  hipFunction_t sfn = nullptr, mfn = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_mu);
+    DeviceGuard guard(a->device);
+    if (guard.err != hipSuccess)
+      return fail(TA_EHIP, "set device %d: %s", a->device, hipGetErrorString(guard.err));
+    ta_status s = get_function_locked(a->device, sid, &sfn);
+    if (s == TA_OK) s = get_function_locked(a->device, mid, &mfn);
+    if (s != TA_OK) return s;
+  }
+
+  ta::FwdParams p;
+  fill_params(a, n_bh, n_qblk, &p);
+  const int64_t rows = n_bh * l.slots * kSplitRows;
+  p.part_o = static_cast<float*>(workspace);
+  p.part_lse = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                        (rows * a->D * 4 + 255) / 256 * 256);
+  p.split_c = chunk_steps;
+  p.split_items = static_cast<int32_t>(l.items);
+  p.split_ns = static_cast<int32_t>(l.ns);
+  p.split_slots = static_cast<int32_t>(l.slots);
+
+  DeviceGuard guard(a->device);
+  if (guard.err != hipSuccess)
+    return fail(TA_EHIP, "set device %d: %s", a->device, hipGetErrorString(guard.err));
+  void* params[] = {&p};
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  hipError_t e = hipModuleLaunchKernel(sfn, static_cast<unsigned>(n_bh * l.items), 1, 1, 512, 1,
+                                       1, 0, hs, params, nullptr);
+  if (e != hipSuccess) return fail(TA_EHIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
+  // merge: one thread per (row, 16-byte output chunk), 256 threads a workgroup
+  const int64_t merge_wgs = n_bh * l.merge * (kSplitRows / (256 / (a->D / 8)));
+  e = hipModuleLaunchKernel(mfn, static_cast<unsigned>(merge_wgs), 1, 1, 256, 1, 1, 0, hs, params,
+                            nullptr);
   if (e != hipSuccess) return fail(TA_EHIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
   return TA_OK;
 }

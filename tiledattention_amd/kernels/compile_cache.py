@@ -21,6 +21,7 @@ KernelKey = tuple[object, ...]
 
 _KERNEL_CACHE: dict[KernelKey, KernelCallable] = {}
 _CACHE_LOCK = Lock()
+_generation = 0  # bumped by every reset; callers holding kernels across calls compare it
 
 
 def get_kernel(key: KernelKey, factory: Callable[[], KernelCallable]) -> KernelCallable:
@@ -38,12 +39,19 @@ def cache_size() -> int:
         return len(_KERNEL_CACHE)
 
 
+def generation() -> int:
+    """Number of resets so far: a kernel obtained under another generation is stale."""
+    return _generation
+
+
 def reset_cache_for_tests() -> None:
     """Empty the cache and unload the native modules if the library is loaded."""
     from .. import _lib
 
+    global _generation
     with _CACHE_LOCK:
         _KERNEL_CACHE.clear()
+        _generation += 1
         lib = _lib.loaded()
         if lib is not None:
             lib.ta_cache_reset()

@@ -30,6 +30,12 @@ Environment knobs are re-read on every call, as in the reference:
 ``TILEDATTN_SCHED`` (this build only)
     Workgroup-to-tile order: ``0`` plain, ``1`` XCD-grouped, ``2`` XCD-grouped with causal
     heavy/light complementary order; default: see ``_resolve_sched``.
+``TILEDATTN_SPLIT`` (this build only)
+    Split key ranges (``ta_sdpa_fwd_split``): ``auto`` (default) asks the library's
+    dispatch model (``ta_split_plan``), ``0``/``off`` never splits, a positive integer
+    forces chunks of that many 128-key steps.  Splitting exists for tile (128, 64) with
+    fp32 accumulation and kernel head dims up to 128; forcing it elsewhere raises
+    ``ValueError``.
 """
 
 from __future__ import annotations
@@ -40,6 +46,7 @@ from typing import Any
 
 from .. import _lib, _runtime
 from .._errors import DTypeNotSupportedError, InvalidShapeError, TiledAttentionError
+from . import compile_cache as _compile_cache
 from .compile_cache import get_kernel
 
 _DEFAULT_TM = 64
@@ -288,6 +295,50 @@ class _Launcher:
         st = self.lib.ta_sdpa_fwd(ctypes.byref(args), ctypes.c_void_p(stream))
         _raise_for_status(self.lib, st)
 
+    def split(self, args: _lib.FwdArgs, chunk_steps: int, workspace: int, workspace_bytes: int,
+              stream: int) -> None:
+        st = self.lib.ta_sdpa_fwd_split(ctypes.byref(args), chunk_steps, ctypes.c_void_p(workspace),
+                                        workspace_bytes, ctypes.c_void_p(stream))
+        _raise_for_status(self.lib, st)
+
+
+# (S, B*H, causal, device) -> chunk steps chosen by the library's dispatch model.
+_SPLIT_PLANS: dict[tuple[int, int, int, int], int] = {}
+
+
+def _split_capable(*, tile_m: int, tile_n: int, accum_code: int, kernel_head_dim: int) -> bool:
+    """Split key ranges exist for the eight-wave kernel only: tile (128, 64), fp32
+    accumulation, kernel head dim <= 128."""
+    return (tile_m, tile_n) == (128, 64) and accum_code == _lib.TA_ACC_FP32 and kernel_head_dim <= 128
+
+
+def _resolve_split(lib, args: _lib.FwdArgs, *, capable: bool) -> int:
+    """``TILEDATTN_SPLIT`` -> chunk length in 128-key steps (0 = whole rows)."""
+    raw = os.getenv("TILEDATTN_SPLIT", "").strip().lower()
+    if raw in ("", "auto"):
+        if not capable:
+            return 0
+        key = (int(args.S), int(args.B * args.H), int(args.causal), int(args.device))
+        chunk = _SPLIT_PLANS.get(key)
+        if chunk is None:
+            out = ctypes.c_int32(0)
+            _raise_for_status(lib, lib.ta_split_plan(ctypes.byref(args), ctypes.byref(out)))
+            chunk = _SPLIT_PLANS[key] = int(out.value)
+        return chunk
+    if raw in ("0", "off"):
+        return 0
+    try:
+        chunk = int(raw)
+    except ValueError as exc:
+        raise ValueError(f"TILEDATTN_SPLIT must be 'auto', 'off' or an integer, got {raw!r}.") from exc
+    if chunk < 0:
+        raise ValueError(f"TILEDATTN_SPLIT must be >= 0, got {chunk}.")
+    if chunk and not capable:
+        raise ValueError(
+            "TILEDATTN_SPLIT needs tile (128, 64), fp32 accumulation and a head dim of at most 128."
+        )
+    return chunk
+
 
 def _raise_for_status(lib, status: int) -> None:
     if status == _lib.TA_OK:
@@ -305,36 +356,63 @@ def _raise_for_status(lib, status: int) -> None:
 
 
 def _kernel_ready(torch_mod, t, kernel_head_dim: int, pad_dim: int):
-    """Tensor in a layout the kernel reads directly: [B,H,S,kernel_D], unit last stride, 16-byte rows."""
+    """Tensor in a layout the kernel reads directly: [B,H,S,kernel_D], unit last stride,
+    16-byte rows at a 16-byte aligned address (a fresh dense copy otherwise)."""
     if pad_dim > 0:
         return torch_mod.nn.functional.pad(t, (0, pad_dim)).contiguous()
-    st = t.stride()
-    ok = (
-        st[3] == 1
-        and all(s % 8 == 0 for s in st[:3])
-        and t.data_ptr() % 16 == 0
-        and t.shape[3] == kernel_head_dim
-    )
-    return t if ok else t.contiguous()
+    if _strides_ok(t.stride(), t.shape[3], kernel_head_dim) and t.data_ptr() % 16 == 0:
+        return t
+    # contiguous() returns a dense but misaligned view unchanged; a clone is a new block
+    return t.clone(memory_format=torch_mod.contiguous_format)
 
 
-def run_flash_fwd(
-    q,
-    k,
-    v,
-    *,
-    causal: bool,
-    scale: float,
-):
-    """Run the gfx950 SDPA forward on validated [B,H,S,D] fp16/bf16 tensors; returns o.
+def _strides_ok(stride, head_dim: int, kernel_head_dim: int) -> bool:
+    return stride[3] == 1 and all(x % 8 == 0 for x in stride[:3]) and head_dim == kernel_head_dim
 
-    Follows flash_fwd.py:821-973: resolve knobs, pad the head dim if needed, allocate the
-    output, pick the kernel through the cache, launch, apply the sync mode, and return
-    ``[B,H,S,D]`` (a view sliced back to D when padded).  K is read row-major in place; no
-    transposed view or per-call copy is made unless the inputs' strides require one.
-    """
-    torch_mod = _runtime.get_torch_module()
-    lib = _runtime.get_native_library()
+
+# Knobs this module reads, re-read on every call as in the reference.  A launch plan is
+# cached per (shapes, strides, dtype, device, causal, knob values), so a changed knob
+# builds a new plan exactly where the reference would change its behaviour.
+_KNOBS = (
+    "TILEDATTN_TILE_M", "TILEDATTN_TILE_N", "TILEDATTN_ACCUM_MODE", "TILEDATTN_SYNC_MODE",
+    "TILEDATTN_DISABLE_ALIGNED_FASTPATH", "TILEDATTN_KERNEL_OPT_LEVEL",
+    "TILEDATTN_KERNEL_OCCUPANCY", "TILEDATTN_KERNEL_NUM_CTAS", "TILEDATTN_CHUNKED_HEAD_DIMS",
+    "TILEDATTN_SCHED", "TILEDATTN_SPLIT",
+)
+# os.environ keeps its encoded mapping in ``_data`` (CPython, POSIX); reading it directly
+# skips the per-key encode/decode of os.getenv.  Assignments through os.environ (and
+# os.putenv-free tools such as pytest's monkeypatch) update it.
+_ENV_DATA = getattr(os.environ, "_data", None)
+_KNOB_KEYS = tuple(os.environ.encodekey(n) for n in _KNOBS) if hasattr(os.environ, "encodekey") else None
+
+
+def _knob_snapshot() -> tuple:
+    if _ENV_DATA is not None and _KNOB_KEYS is not None:
+        return tuple(map(_ENV_DATA.get, _KNOB_KEYS))
+    return tuple(map(os.environ.get, _KNOBS))
+
+
+class _LaunchPlan:
+    """Everything a launch needs that does not depend on the tensors' addresses or the scale."""
+
+    __slots__ = ("generation", "empty", "out_shape", "head_dim", "pad_dim", "kernel_head_dim",
+                 "copy", "args", "kernel", "chunk", "ws_bytes", "sync_mode", "device",
+                 "device_index", "dtype")
+
+
+_PLANS: dict[tuple, _LaunchPlan] = {}
+_PLANS_MAX = 512
+
+
+def _raw_stream(torch_mod, device_index: int) -> int:
+    get_raw = getattr(torch_mod._C, "_cuda_getCurrentRawStream", None)
+    if get_raw is not None:
+        return int(get_raw(device_index))
+    return int(torch_mod.cuda.current_stream(device_index).cuda_stream)
+
+
+def _build_plan(torch_mod, lib, q, k, v, causal: bool) -> _LaunchPlan:
+    """Resolve knobs and policies for a call (flash_fwd.py:821-969), up to the launch."""
     opt_level, occupancy, num_ctas = _resolve_kernel_options()
     sync_mode = _resolve_sync_mode()
 
@@ -360,16 +438,18 @@ def run_flash_fwd(
         tile_n = _WIDE_HEAD_DIM_TILE_N
     dtype_code = _dtype_code_for_torch_dtype(q.dtype)
 
-    device = q.device
-    out_shape = (batch, heads, seq_len, kernel_head_dim)
-    if bh == 0 or seq_len == 0:
-        out = torch_mod.empty(out_shape, dtype=q.dtype, device=device)
-        return out[..., :head_dim] if pad_dim > 0 else out
-
-    qk = _kernel_ready(torch_mod, q, kernel_head_dim, pad_dim)
-    kk = _kernel_ready(torch_mod, k, kernel_head_dim, pad_dim)
-    vk = _kernel_ready(torch_mod, v, kernel_head_dim, pad_dim)
-    out = torch_mod.empty(out_shape, dtype=q.dtype, device=device)
+    plan = _LaunchPlan()
+    plan.generation = _compile_cache.generation()
+    plan.device = q.device
+    plan.dtype = q.dtype
+    plan.head_dim = head_dim
+    plan.pad_dim = pad_dim
+    plan.kernel_head_dim = kernel_head_dim
+    plan.out_shape = (batch, heads, seq_len, kernel_head_dim)
+    plan.sync_mode = sync_mode
+    plan.empty = bh == 0 or seq_len == 0
+    if plan.empty:
+        return plan
 
     use_aligned_fastpath = _should_use_aligned_noncausal_fastpath(
         seq_len=seq_len,
@@ -388,7 +468,8 @@ def run_flash_fwd(
         kernel_variant = "direct"
     aligned = int(seq_len % tile_m == 0 and seq_len % tile_n == 0)
     accum_code = _lib.TA_ACC_INPUT if accum_mode == "fp16" else _lib.TA_ACC_FP32
-    device_index = device.index if device.index is not None else torch_mod.cuda.current_device()
+    device_index = q.device.index if q.device.index is not None else torch_mod.cuda.current_device()
+    plan.device_index = device_index
 
     kernel_key = (
         tile_m,
@@ -405,15 +486,20 @@ def run_flash_fwd(
         device_index,
     )
     config = (dtype_code, kernel_head_dim, tile_m, tile_n, int(causal), accum_code, aligned)
-    kernel = get_kernel(kernel_key, lambda: _Launcher(lib, device_index, config))
+    plan.kernel = get_kernel(kernel_key, lambda: _Launcher(lib, device_index, config))
 
+    # Which inputs the kernel cannot read in place (padding or strides); addresses are
+    # checked per call.
+    plan.copy = tuple(pad_dim > 0 or not _strides_ok(t.stride(), head_dim, kernel_head_dim)
+                      for t in (q, k, v))
     n_qblk = (seq_len + tile_m - 1) // tile_m
     args = _lib.FwdArgs()
-    args.q, args.k, args.v, args.o = qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), out.data_ptr()
     args.B, args.H, args.S, args.D = batch, heads, seq_len, kernel_head_dim
-    for name, t in (("q_stride", qk), ("k_stride", kk), ("v_stride", vk), ("o_stride", out)):
-        getattr(args, name)[:] = tuple(t.stride())
-    args.scale = float(scale)
+    contiguous = (heads * seq_len * kernel_head_dim, seq_len * kernel_head_dim, kernel_head_dim, 1)
+    for name, t, cp in (("q_stride", q, plan.copy[0]), ("k_stride", k, plan.copy[1]),
+                        ("v_stride", v, plan.copy[2])):
+        getattr(args, name)[:] = contiguous if cp else tuple(t.stride())
+    args.o_stride[:] = contiguous
     args.causal = int(causal)
     args.dtype = dtype_code
     args.tile_m, args.tile_n = tile_m, tile_n
@@ -422,11 +508,71 @@ def run_flash_fwd(
     args.sched = _resolve_sched(n_blocks=bh * n_qblk, causal=causal, tile_m=tile_m, tile_n=tile_n,
                                 accum_code=accum_code)
 
-    stream = torch_mod.cuda.current_stream(device)
-    if sync_mode == "strict":
-        torch_mod.cuda.synchronize(device)
-    kernel(args, stream.cuda_stream)
-    if sync_mode in {"strict", "post"}:
-        stream.synchronize()
+    capable = _split_capable(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code,
+                             kernel_head_dim=kernel_head_dim)
+    plan.chunk = _resolve_split(lib, args, capable=capable)
+    plan.ws_bytes = 0
+    if plan.chunk:
+        ws_bytes = ctypes.c_int64(0)
+        _raise_for_status(lib, lib.ta_split_workspace_size(ctypes.byref(args), plan.chunk,
+                                                           ctypes.byref(ws_bytes)))
+        plan.ws_bytes = int(ws_bytes.value)
+        if plan.ws_bytes and not os.getenv("TILEDATTN_SCHED", "").strip():
+            args.sched = 1  # the split grid regroups per XCD whenever it divides evenly
+    plan.args = args
+    return plan
 
-    return out[..., :head_dim] if pad_dim > 0 else out
+
+def run_flash_fwd(
+    q,
+    k,
+    v,
+    *,
+    causal: bool,
+    scale: float,
+):
+    """Run the gfx950 SDPA forward on validated [B,H,S,D] fp16/bf16 tensors; returns o.
+
+    Follows flash_fwd.py:821-973: resolve knobs, pad the head dim if needed, allocate the
+    output, pick the kernel through the cache, launch, apply the sync mode, and return
+    ``[B,H,S,D]`` (a view sliced back to D when padded).  K is read row-major in place; no
+    transposed view or per-call copy is made unless the inputs' strides require one.  The
+    resolution is cached per configuration and knob values (``_build_plan``); a call then
+    allocates the output, fills the tensor addresses and scale, and launches.
+    """
+    torch_mod = _runtime.get_torch_module()
+    key = (q.shape, q.stride(), k.stride(), v.stride(), q.dtype, q.device, causal, _knob_snapshot())
+    plan = _PLANS.get(key)
+    if plan is None or plan.generation != _compile_cache.generation():
+        plan = _build_plan(torch_mod, _runtime.get_native_library(), q, k, v, causal)
+        if len(_PLANS) >= _PLANS_MAX:
+            _PLANS.clear()
+        _PLANS[key] = plan
+
+    out = torch_mod.empty(plan.out_shape, dtype=plan.dtype, device=plan.device)
+    if not plan.empty:
+        kd, pad = plan.kernel_head_dim, plan.pad_dim
+        qk = _kernel_ready(torch_mod, q, kd, pad) if plan.copy[0] or q.data_ptr() % 16 else q
+        kk = _kernel_ready(torch_mod, k, kd, pad) if plan.copy[1] or k.data_ptr() % 16 else k
+        vk = _kernel_ready(torch_mod, v, kd, pad) if plan.copy[2] or v.data_ptr() % 16 else v
+        args = _lib.FwdArgs.from_buffer_copy(plan.args)
+        if qk is not q or kk is not k or vk is not v:
+            for name, t in (("q_stride", qk), ("k_stride", kk), ("v_stride", vk)):
+                getattr(args, name)[:] = tuple(t.stride())
+        args.q, args.k, args.v, args.o = qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), out.data_ptr()
+        args.scale = scale
+        if plan.sync_mode == "strict":
+            torch_mod.cuda.synchronize(plan.device)
+        stream = _raw_stream(torch_mod, plan.device_index)
+        if plan.ws_bytes:
+            # torch's caching allocator returns 512-byte aligned blocks, stream-ordered: the
+            # block is reused only by work enqueued after this launch on the same stream.
+            workspace = torch_mod.empty(plan.ws_bytes, dtype=torch_mod.uint8, device=plan.device)
+            plan.kernel.split(args, plan.chunk, workspace.data_ptr(), plan.ws_bytes, stream)
+        else:
+            plan.kernel(args, stream)
+        if plan.sync_mode in {"strict", "post"}:
+            torch_mod.cuda.current_stream(plan.device).synchronize()
+
+    return out[..., :plan.head_dim] if plan.pad_dim > 0 else out
+
