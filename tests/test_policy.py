@@ -100,7 +100,7 @@ def test_default_accum_mode_table(s, d, causal, expected):
 
 
 @pytest.mark.parametrize("raw,expected", [
-    (None, "fp16"), ("", "fp16"), ("auto", "fp16"), (" AUTO ", "fp16"),
+    (None, "fp32"), ("", "fp32"), ("auto", "fp32"), (" AUTO ", "fp32"),
     ("fp32", "fp32"), (" FP32", "fp32"), ("fp16", "fp16"), ("Fp16 ", "fp16"),
 ])
 def test_resolve_accum_mode(monkeypatch, raw, expected):
@@ -108,8 +108,15 @@ def test_resolve_accum_mode(monkeypatch, raw, expected):
         monkeypatch.delenv("TILEDATTN_ACCUM_MODE", raising=False)
     else:
         monkeypatch.setenv("TILEDATTN_ACCUM_MODE", raw)
-    # shape where auto picks the input dtype: non-causal, D=64, S>=1024
+    # a shape where the reference's auto rule picks the input dtype (non-causal, D=64,
+    # S>=1024); on gfx950 auto resolves to fp32 (faster and more accurate here)
+    assert ff._default_accum_mode_for_shape(seq_len=2048, head_dim=64, causal=False) == "fp16"
     assert ff._resolve_accum_mode(seq_len=2048, head_dim=64, causal=False) == expected
+
+
+@pytest.mark.parametrize("s,d,causal", [(2048, 64, False), (64, 64, True), (8192, 128, False), (1024, 160, False)])
+def test_gfx950_auto_accumulation_is_fp32(s, d, causal):
+    assert ff._default_accum_mode_for_shape_gfx950(seq_len=s, head_dim=d, causal=causal) == "fp32"
 
 
 @pytest.mark.parametrize("raw", ["bf16", "fp8", "32"])

