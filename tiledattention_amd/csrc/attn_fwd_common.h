@@ -26,6 +26,8 @@ constexpr float kNegLarge = -1.0e30f;
 constexpr float kMasked = -__builtin_huge_valf();
 // Lazy-rescale threshold in log2 units: P = 2^(s*c - m*c) stays <= 2^8.
 constexpr float kRescaleLog2 = 8.0f;
+constexpr float kRescaleBound = 256.0f;  // 2^kRescaleLog2
+static_assert(kRescaleBound == (float)(1 << (int)kRescaleLog2), "bound = 2^threshold");
 
 template <int DT>
 struct DType;

@@ -254,48 +254,60 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
         }
       }
     }
-    float mxa = kMasked, mxb = kMasked;
+    // P = 2^(s c - m c) packed into pk, and the sum of the rounded P: four independent
+    // partial sums so the dot2 chain is short.
+    auto make_p = [&](float mc) {
+      float l4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int bk = 0; bk < KB; ++bk) {
+      for (int bk = 0; bk < KB; ++bk) {
 #pragma unroll
-      for (int r = 0; r < 16; r += 4) {
-        mxa = vmax3(mxa, s[bk][r], s[bk][r + 1]);
-        mxb = vmax3(mxb, s[bk][r + 2], s[bk][r + 3]);
-      }
-    }
-    float mx;
-    {
-      float a0, a1;
-      swap32(vmax(mxa, mxb), a0, a1);
-      mx = vmax(a0, a1);
-    }
-    const bool need = (mx - m_run) * c > kRescaleLog2;
-    if (__ballot(need)) {
-      const float m_new = need ? mx : m_run;
-      const float alpha = fast_exp2((m_run - m_new) * c);
-      m_run = m_new;
-#pragma unroll
-      for (int db = 0; db < DB; ++db) o_acc[db] *= alpha;
-      l_part *= alpha;
-    }
-    const float mc = m_run * c;
-    float la = 0.0f, lb = 0.0f;
-#pragma unroll
-    for (int bk = 0; bk < KB; ++bk) {
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        const float p0 = fast_exp2(__builtin_fmaf(s[bk][r], c, -mc));
-        const float p1 = fast_exp2(__builtin_fmaf(s[bk][r + 1], c, -mc));
-        const uint32_t w = DTy::pack(p0, p1);
-        pk[bk][r >> 1] = w;
-        if (r & 2) {
-          lb = DTy::sum2(w, lb);
-        } else {
-          la = DTy::sum2(w, la);
+        for (int r = 0; r < 16; r += 2) {
+          const float p0 = fast_exp2(__builtin_fmaf(s[bk][r], c, -mc));
+          const float p1 = fast_exp2(__builtin_fmaf(s[bk][r + 1], c, -mc));
+          const uint32_t w = DTy::pack(p0, p1);
+          pk[bk][r >> 1] = w;
+          l4[(r >> 1) & 3] = DTy::sum2(w, l4[(r >> 1) & 3]);
         }
       }
+      return (l4[0] + l4[1]) + (l4[2] + l4[3]);
+    };
+    // The reference point m moves only when the row max grows by more than the rescale
+    // threshold (some P above 2^kRescaleLog2), so P is first computed with the current m.
+    // P >= 0, so a lane whose sum of P stays below that bound has no such P and needs no
+    // max at all: the row max is reduced only in the rare wave where some lane's sum
+    // reaches it (every row's first step, a jump of the max), and there the rule is the
+    // exact one (max grew by more than the threshold -> rescale O and l, recompute P).
+    // A VALU cluster is bound by one wave's issue rate, so the skipped reduction is time
+    // saved.
+    float l_step = make_p(m_run * c);
+    if (__ballot(!(l_step < kRescaleBound))) {
+      float mxa = kMasked, mxb = kMasked;
+#pragma unroll
+      for (int bk = 0; bk < KB; ++bk) {
+#pragma unroll
+        for (int r = 0; r < 16; r += 4) {
+          mxa = vmax3(mxa, s[bk][r], s[bk][r + 1]);
+          mxb = vmax3(mxb, s[bk][r + 2], s[bk][r + 3]);
+        }
+      }
+      float mx;
+      {
+        float a0, a1;
+        swap32(vmax(mxa, mxb), a0, a1);
+        mx = vmax(a0, a1);
+      }
+      const bool need = (mx - m_run) * c > kRescaleLog2;
+      if (__ballot(need)) {
+        const float m_new = need ? mx : m_run;
+        const float alpha = fast_exp2((m_run - m_new) * c);
+        m_run = m_new;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) o_acc[db] *= alpha;
+        l_part *= alpha;
+        l_step = make_p(m_run * c);
+      }
     }
-    l_part += la + lb;
+    l_part += l_step;
     // Keep the P computation in this cluster: without a use here the compiler sinks it
     // past the barrier to its consumers, the P.V MFMAs of the other cluster.
 #pragma unroll
