@@ -52,8 +52,8 @@ typedef struct ta_fwd_args {
   const void* k;
   const void* v;
   void* o;
-  int64_t B, H, S, D; /* D: 64, 128, 160 or 256 (callers zero-pad other head dims);
-                         160 and 256 need tile_n = 64 */
+  int64_t B, H, S, D; /* D: 64, 128, 160 or 256 (callers zero-pad other head dims, or
+                         set d_real); 160 and 256 need tile_n = 64 */
   int64_t q_stride[4]; /* element strides for (B,H,S,D); stride[3] must be 1 */
   int64_t k_stride[4];
   int64_t v_stride[4];
@@ -67,7 +67,11 @@ typedef struct ta_fwd_args {
   int32_t device;  /* HIP device ordinal the pointers and stream belong to */
   int32_t sched;   /* workgroup -> tile order: 0 plain, 1 XCD-grouped, 2 XCD-grouped with
                       causal heavy/light complementary order */
-  int32_t reserved;
+  int32_t d_real;  /* 0, or the head-dim columns q/k/v/o actually have (a multiple of 8 below
+                      D): the kernel for D reads the missing columns as zero and does not
+                      write them, so a narrower head dim needs no padded copies (the
+                      reference pads on the host, flash_fwd.py:868-872).  Tile (128, 64)
+                      with fp32 accumulation and D <= 128 only. */
 } ta_fwd_args;
 
 /* Version of this ABI (TA_ABI_VERSION). */

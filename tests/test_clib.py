@@ -80,6 +80,13 @@ def _call(lib, a):
     (dict(k_stride=(2 * 64 * 64, 64 * 64, 64, 2)), _lib.TA_EINVAL, "last-dim stride"),
     (dict(o_stride=(2 * 64 * 64, 64 * 64, 68, 1)), _lib.TA_EINVAL, "multiple of 8"),
     (dict(S=1 << 24, k_stride=(0, 0, 128, 1), D=128), _lib.TA_EINVAL, "2^31"),
+    (dict(S=2, k_stride=(0, 0, 1 << 23, 1)), _lib.TA_EINVAL, "128 * row stride"),
+    (dict(d_real=4), _lib.TA_EINVAL, "d_real 4"),
+    (dict(d_real=72), _lib.TA_EINVAL, "d_real 72"),        # above D = 64
+    (dict(d_real=-8), _lib.TA_EINVAL, "d_real"),
+    (dict(d_real=36, D=128, tile_m=128), _lib.TA_EINVAL, "multiple of 8"),
+    (dict(d_real=96, D=128), _lib.TA_EUNSUPPORTED, "d_real needs tile (128, 64)"),  # tile 64x64
+    (dict(d_real=96, D=128, tile_m=128, accum=1), _lib.TA_EUNSUPPORTED, "d_real needs"),
 ])
 def test_argument_validation(lib, kw, status, msg):
     st = _call(lib, _args(**kw))

@@ -135,13 +135,51 @@ def test_tails_all_tiles(gpu, s, causal, dtype, d):
 
 @pytest.mark.parametrize("d", [8, 32, 48, 80, 96, 100])
 def test_head_dim_padding(gpu, d):
-    """D outside {64,128}: zero-padded to the next kernel head dim, output sliced back."""
+    """D outside {64,128}: a multiple of 8 runs in place on the default (eight-wave) kernel,
+    whose missing columns read as zero (dense output of width D); other D, and the other
+    tiles, are zero-padded on the host and the output is a sliced view."""
     q, k, v = inputs((1, 2, 200, d), "float16", 7 + d)
     for causal in (False, True):
-        say(f"pad fp16 (1,2,200,{d}) causal={causal}")
+        ref = oracle_f32(q, k, v, causal=causal)
+        say(f"pad fp16 (1,2,200,{d}) causal={causal} default tile")
         out = run_gpu(q, k, v, causal=causal)
         assert out.shape == (1, 2, 200, d)
-        check_close(as_f32(out), oracle_f32(q, k, v, causal=causal), "float16", what=f"pad D={d}")
+        assert out.is_contiguous() == (d % 8 == 0)
+        check_close(as_f32(out), ref, "float16", what=f"pad D={d}")
+        say(f"pad fp16 (1,2,200,{d}) causal={causal} tile 64x64 (host padding)")
+        host = run_gpu(q, k, v, causal=causal, tile_m=64, tile_n=64)
+        assert host.shape == (1, 2, 200, d) and not host.is_contiguous()
+        check_close(as_f32(host), ref, "float16", what=f"host pad D={d}")
+
+
+@pytest.mark.parametrize("d,dtype,causal,s", [
+    (96, "bfloat16", True, 1000), (120, "float16", False, 777), (56, "bfloat16", False, 1500),
+    (72, "float16", True, 2048), (104, "bfloat16", True, 4096),
+])
+def test_head_dim_in_kernel_padding(gpu, d, dtype, causal, s):
+    """Narrower head dims on the eight-wave kernel without host copies: ragged S, both
+    dtypes, split key ranges, [B,S,H,D]-strided views (row stride H*D, not a multiple of the
+    kernel's D), all against the oracle."""
+    import torch
+
+    from tiledattention_amd import sdpa
+
+    q, k, v = inputs((2, 3, s, d), dtype, 40 + d)
+    rows = None if s <= 2048 else sample_rows(s, 96)
+    ref = oracle_f32(q, k, v, causal=causal, rows=rows)
+    say(f"in-kernel pad {dtype} (2,3,{s},{d}) causal={causal}")
+    out = run_gpu(q, k, v, causal=causal)
+    assert out.shape == (2, 3, s, d) and out.is_contiguous()
+    check_close(as_f32(out, rows), ref, dtype, what=f"in-kernel pad D={d}")
+    say(f"in-kernel pad {dtype} (2,3,{s},{d}) causal={causal} split=2")
+    out = run_gpu(q, k, v, causal=causal, split=2)
+    check_close(as_f32(out, rows), ref, dtype, what=f"in-kernel pad D={d} split")
+    dev = torch.device("cuda:0")
+    bshd = [t.transpose(1, 2).contiguous().to(dev).transpose(1, 2) for t in (q, k, v)]
+    say(f"in-kernel pad {dtype} (2,3,{s},{d}) causal={causal} [B,S,H,D] views")
+    out = sdpa(*bshd, causal=causal)
+    torch.cuda.synchronize()
+    check_close(as_f32(out, rows), ref, dtype, what=f"in-kernel pad D={d} BSHD")
 
 
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])

@@ -87,7 +87,7 @@ class FwdArgs(ctypes.Structure):
         ("accum", ctypes.c_int32),
         ("device", ctypes.c_int32),
         ("sched", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("d_real", ctypes.c_int32),
     ]
 
 

@@ -27,6 +27,9 @@ struct FwdParams {
   int32_t split_items; // work items per (b, h)
   int32_t split_ns;    // chunks per query block (non-causal; causal derives it per block)
   int32_t split_slots; // partial slots per (b, h)
+  int32_t d_real;      // head-dim columns present in q/k/v/o (eight-wave kernel; <= D,
+                       // multiple of 8): columns d_real..D-1 read as zero, are not written
+  int32_t pad0;
 };
 
 }  // namespace ta

@@ -117,13 +117,17 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   // ---- Q fragment: B operand of S^T = K Q^T, kept for the whole key loop ------------
   // (loaded in the prologue, between the first key stage and the next stages)
   u32x4 qf[DK];
+  // Columns at or past d_real (a head dim narrower than the kernel's) are zero.
+  const int d_real = p.d_real;
   auto load_q = [&]() {
     const bool ok = !TAIL || my_q < S;
     const uint16_t* row = qp + (int64_t)(ok ? my_q : 0) * p.q_ss;
 #pragma unroll
     for (int kk = 0; kk < DK; ++kk) {
-      u32x4 v = *(const u32x4*)(row + 16 * kk + 8 * hl);
-      qf[kk] = ok ? v : u32x4{0, 0, 0, 0};
+      const int col = 16 * kk + 8 * hl;
+      const bool in = ok && col < d_real;
+      u32x4 v = *(const u32x4*)(row + (in ? col : 0));
+      qf[kk] = in ? v : u32x4{0, 0, 0, 0};
     }
   };
 
@@ -147,8 +151,14 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   const int ld_g0 = koff / RPL + wr;  // first chunk this wave fills
   const int ld_row = ld_g0 * RPL + lane / CPR;
   const int ld_pc = lane % CPR;
-  const int kvo = ld_row * k_rb + ((ld_pc ^ pp_swz_k<D>(ld_row)) << 4);
-  const int vvo = ld_row * v_rb + ((ld_pc ^ pp_swz_v<D>(ld_row)) << 4);
+  // A logical chunk at or past d_real gets an offset of 2^31 or more: every buffer resource
+  // here spans less than 2^31 bytes, so it reads zero (and the per-load row steps added
+  // below stay far from 2^32).
+  constexpr int kZeroChunk = INT32_MIN;
+  const int lck = ld_pc ^ pp_swz_k<D>(ld_row);
+  const int lcv = ld_pc ^ pp_swz_v<D>(ld_row);
+  const int kvo = 8 * lck < d_real ? ld_row * k_rb + (lck << 4) : kZeroChunk;
+  const int vvo = 8 * lcv < d_real ? ld_row * v_rb + (lcv << 4) : kZeroChunk;
   auto dma = [&](const uint16_t* gbase, int64_t row_stride, int rb, int vo, int t, char* stage) {
     const int row0 = t * TK;
     const int rows = t < t_end ? S - row0 : 0;
@@ -495,7 +505,7 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
       const uint32_t w0 = DTy::pack(o4[0], o4[1]);
       const uint32_t w1 = DTy::pack(o4[2], o4[3]);
       const int d = 32 * db + 8 * g + 4 * hl;
-      *(u32x2*)(orow + d) = u32x2{w0, w1};
+      if (d < d_real) *(u32x2*)(orow + d) = u32x2{w0, w1};
     }
   }
 }
@@ -521,7 +531,7 @@ __device__ __forceinline__ void attn_merge_body(const FwdParams& p) {
   const int row = (blockIdx.x - blk * WPB) * RPW + threadIdx.x / CH;
   const int c8 = threadIdx.x % CH;
   const int q = mi.qt * TM + row;
-  if (q >= p.S) return;
+  if (q >= p.S || 8 * c8 >= p.d_real) return;
   const int b = mi.bh / p.H;
   const int h = mi.bh - b * p.H;
   const float* lse = p.part_lse + (int64_t)mi.slot0 * TM + row;

@@ -285,6 +285,12 @@ ta_status validate_args(const ta_fwd_args* a, int64_t* n_bh_out, int64_t* n_qblk
     return fail(TA_EINVAL, "accum %d", a->accum);
   if (a->causal != 0 && a->causal != 1) return fail(TA_EINVAL, "causal %d", a->causal);
   if (a->sched < 0 || a->sched > 2) return fail(TA_EINVAL, "sched %d", a->sched);
+  if (a->d_real != 0) {
+    if (a->d_real < 8 || a->d_real > a->D || (a->d_real & 7) != 0)
+      return fail(TA_EINVAL, "d_real %d (0, or a multiple of 8 in [8, D])", a->d_real);
+    if (!(a->tile_m == kSplitRows && a->tile_n == 64 && a->accum == TA_ACC_FP32 && a->D <= 128))
+      return fail(TA_EUNSUPPORTED, "d_real needs tile (128, 64), fp32 accumulation and D <= 128");
+  }
   if (a->B < 0 || a->H < 0 || a->S < 0) return fail(TA_EINVAL, "negative shape");
   ta_status shape_st = check_shape(a->D, a->tile_m, a->tile_n);
   if (shape_st != TA_OK) return shape_st;
@@ -312,9 +318,12 @@ ta_status validate_args(const ta_fwd_args* a, int64_t* n_bh_out, int64_t* n_qblk
         return fail(TA_EINVAL, "%s: stride[%d]=%lld must be a non-negative multiple of 8", nm[i], j,
                     (long long)st[i][j]);
   }
-  // K and V are read with buffer instructions whose byte range is 32-bit.
+  // K and V are read with buffer instructions whose byte range is 32-bit: a (b, h) slice,
+  // and the 128 rows one tile step addresses, must stay below 2^31 bytes.
   if (a->S * a->k_stride[2] * 2 > 0x7fffffffLL || a->S * a->v_stride[2] * 2 > 0x7fffffffLL)
     return fail(TA_EINVAL, "k/v: S * row stride must stay below 2^31 bytes per (b, h) slice");
+  if (a->k_stride[2] * 2 * 128 >= 0x80000000LL || a->v_stride[2] * 2 * 128 >= 0x80000000LL)
+    return fail(TA_EINVAL, "k/v: 128 * row stride must stay below 2^31 bytes");
   *n_qblk_out = n_qblk;
   return TA_OK;
 }
@@ -335,6 +344,7 @@ void fill_params(const ta_fwd_args* a, int64_t n_bh, int64_t n_qblk, ta::FwdPara
   p->n_bh = static_cast<int32_t>(n_bh);
   p->scale_log2 = static_cast<float>(static_cast<double>(a->scale) * 1.4426950408889634);
   p->sched = a->sched;
+  p->d_real = a->d_real ? a->d_real : static_cast<int32_t>(a->D);
 }
 
 // Whether the split path exists for this configuration (the eight-wave kernel).
@@ -441,18 +451,26 @@ ta_status ta_split_plan(const ta_fwd_args* a, int32_t* chunk_steps) {
   int64_t n_bh = 0, n_qblk = 0;
   ta_status vst = validate_args(a, &n_bh, &n_qblk, false);
   if (vst != TA_OK || n_qblk == 0 || !split_capable(a)) return vst;
-  std::lock_guard<std::mutex> lock(g_mu);
-  DeviceGuard guard(a->device);
-  if (guard.err != hipSuccess)
-    return fail(TA_EHIP, "set device %d: %s", a->device, hipGetErrorString(guard.err));
   int ncu = 0;
-  ta_status cst = cu_count_locked(a->device, &ncu);
-  if (cst != TA_OK) return cst;
-  const auto key = std::make_tuple(a->S, n_bh, (int)a->causal, ncu);
-  auto it = g_plans.find(key);
-  if (it == g_plans.end())
-    it = g_plans.emplace(key, plan_split(a->S, n_bh, a->causal != 0, ncu)).first;
-  *chunk_steps = it->second;
+  {
+    std::lock_guard<std::mutex> lock(g_mu);
+    DeviceGuard guard(a->device);
+    if (guard.err != hipSuccess)
+      return fail(TA_EHIP, "set device %d: %s", a->device, hipGetErrorString(guard.err));
+    ta_status cst = cu_count_locked(a->device, &ncu);
+    if (cst != TA_OK) return cst;
+    auto it = g_plans.find(std::make_tuple(a->S, n_bh, (int)a->causal, ncu));
+    if (it != g_plans.end()) {
+      *chunk_steps = it->second;
+      return TA_OK;
+    }
+  }
+  // The dispatch model runs without the lock (milliseconds on a shape's first use); two
+  // threads planning the same shape compute the same value.
+  const int32_t c = plan_split(a->S, n_bh, a->causal != 0, ncu);
+  std::lock_guard<std::mutex> lock(g_mu);
+  g_plans.emplace(std::make_tuple(a->S, n_bh, (int)a->causal, ncu), c);
+  *chunk_steps = c;
   return TA_OK;
 }
 

@@ -369,19 +369,20 @@ def _raise_for_status(lib, status: int) -> None:
     raise TiledAttentionError(msg)
 
 
-def _kernel_ready(torch_mod, t, kernel_head_dim: int, pad_dim: int):
-    """Tensor in a layout the kernel reads directly: [B,H,S,kernel_D], unit last stride,
-    16-byte rows at a 16-byte aligned address (a fresh dense copy otherwise)."""
+def _kernel_ready(torch_mod, t, width: int, pad_dim: int):
+    """Tensor in a layout the kernel reads directly: [B,H,S,width] (width = the kernel's
+    head dim, or the tensor's own when the kernel pads in place), unit last stride, 16-byte
+    rows at a 16-byte aligned address (a fresh dense copy otherwise)."""
     if pad_dim > 0:
         return torch_mod.nn.functional.pad(t, (0, pad_dim)).contiguous()
-    if _strides_ok(t.stride(), t.shape[3], kernel_head_dim) and t.data_ptr() % 16 == 0:
+    if _strides_ok(t.stride(), t.shape[3], width) and t.data_ptr() % 16 == 0:
         return t
     # contiguous() returns a dense but misaligned view unchanged; a clone is a new block
     return t.clone(memory_format=torch_mod.contiguous_format)
 
 
-def _strides_ok(stride, head_dim: int, kernel_head_dim: int) -> bool:
-    return stride[3] == 1 and all(x % 8 == 0 for x in stride[:3]) and head_dim == kernel_head_dim
+def _strides_ok(stride, head_dim: int, width: int) -> bool:
+    return stride[3] == 1 and all(x % 8 == 0 for x in stride[:3]) and head_dim == width
 
 
 # Knobs this module reads, re-read on every call as in the reference.  A launch plan is
@@ -409,7 +410,7 @@ def _knob_snapshot() -> tuple:
 class _LaunchPlan:
     """Everything a launch needs that does not depend on the tensors' addresses or the scale."""
 
-    __slots__ = ("generation", "empty", "out_shape", "head_dim", "pad_dim", "kernel_head_dim",
+    __slots__ = ("generation", "empty", "out_shape", "head_dim", "pad_dim", "width",
                  "copy", "args", "kernel", "chunk", "ws_bytes", "sync_mode", "device",
                  "device_index", "dtype")
 
@@ -451,15 +452,22 @@ def _build_plan(torch_mod, lib, q, k, v, causal: bool) -> _LaunchPlan:
             )
         tile_n = _WIDE_HEAD_DIM_TILE_N
     dtype_code = _dtype_code_for_torch_dtype(q.dtype)
+    accum_code = _lib.TA_ACC_INPUT if accum_mode == "fp16" else _lib.TA_ACC_FP32
+    # A narrower head dim that is a multiple of 8 runs in place on the eight-wave kernel
+    # (ta_fwd_args.d_real: missing columns read as zero, not written); others are zero-padded
+    # on the host as the reference does (flash_fwd.py:868-872) and the output is sliced.
+    pad_in_kernel = pad_dim > 0 and head_dim % 8 == 0 and _split_capable(
+        tile_m=tile_m, tile_n=tile_n, accum_code=accum_code, kernel_head_dim=kernel_head_dim)
+    width = head_dim if pad_in_kernel else kernel_head_dim
 
     plan = _LaunchPlan()
     plan.generation = _compile_cache.generation()
     plan.device = q.device
     plan.dtype = q.dtype
     plan.head_dim = head_dim
-    plan.pad_dim = pad_dim
-    plan.kernel_head_dim = kernel_head_dim
-    plan.out_shape = (batch, heads, seq_len, kernel_head_dim)
+    plan.pad_dim = 0 if pad_in_kernel else pad_dim
+    plan.width = width
+    plan.out_shape = (batch, heads, seq_len, width)
     plan.sync_mode = sync_mode
     plan.empty = bh == 0 or seq_len == 0
     if plan.empty:
@@ -481,7 +489,6 @@ def _build_plan(torch_mod, lib, q, k, v, causal: bool) -> _LaunchPlan:
     else:
         kernel_variant = "direct"
     aligned = int(seq_len % tile_m == 0 and seq_len % tile_n == 0)
-    accum_code = _lib.TA_ACC_INPUT if accum_mode == "fp16" else _lib.TA_ACC_FP32
     device_index = q.device.index if q.device.index is not None else torch_mod.cuda.current_device()
     plan.device_index = device_index
 
@@ -502,14 +509,15 @@ def _build_plan(torch_mod, lib, q, k, v, causal: bool) -> _LaunchPlan:
     config = (dtype_code, kernel_head_dim, tile_m, tile_n, int(causal), accum_code, aligned)
     plan.kernel = get_kernel(kernel_key, lambda: _Launcher(lib, device_index, config))
 
-    # Which inputs the kernel cannot read in place (padding or strides); addresses are
+    # Which inputs the kernel cannot read in place (host padding or strides); addresses are
     # checked per call.
-    plan.copy = tuple(pad_dim > 0 or not _strides_ok(t.stride(), head_dim, kernel_head_dim)
+    plan.copy = tuple(plan.pad_dim > 0 or not _strides_ok(t.stride(), head_dim, width)
                       for t in (q, k, v))
     n_qblk = (seq_len + tile_m - 1) // tile_m
     args = _lib.FwdArgs()
     args.B, args.H, args.S, args.D = batch, heads, seq_len, kernel_head_dim
-    contiguous = (heads * seq_len * kernel_head_dim, seq_len * kernel_head_dim, kernel_head_dim, 1)
+    args.d_real = head_dim if pad_in_kernel else 0
+    contiguous = (heads * seq_len * width, seq_len * width, width, 1)
     for name, t, cp in (("q_stride", q, plan.copy[0]), ("k_stride", k, plan.copy[1]),
                         ("v_stride", v, plan.copy[2])):
         getattr(args, name)[:] = contiguous if cp else tuple(t.stride())
@@ -547,9 +555,10 @@ def run_flash_fwd(
 ):
     """Run the gfx950 SDPA forward on validated [B,H,S,D] fp16/bf16 tensors; returns o.
 
-    Follows flash_fwd.py:821-973: resolve knobs, pad the head dim if needed, allocate the
-    output, pick the kernel through the cache, launch, apply the sync mode, and return
-    ``[B,H,S,D]`` (a view sliced back to D when padded).  K is read row-major in place; no
+    Follows flash_fwd.py:821-973: resolve knobs, pad the head dim if needed (in the kernel
+    where it can, else on the host), allocate the output, pick the kernel through the cache,
+    launch, apply the sync mode, and return ``[B,H,S,D]`` (a view sliced back to D when
+    padded on the host).  K is read row-major in place; no
     transposed view or per-call copy is made unless the inputs' strides require one.  The
     resolution is cached per configuration and knob values (``_build_plan``); a call then
     allocates the output, fills the tensor addresses and scale, and launches.
@@ -565,10 +574,10 @@ def run_flash_fwd(
 
     out = torch_mod.empty(plan.out_shape, dtype=plan.dtype, device=plan.device)
     if not plan.empty:
-        kd, pad = plan.kernel_head_dim, plan.pad_dim
-        qk = _kernel_ready(torch_mod, q, kd, pad) if plan.copy[0] or q.data_ptr() % 16 else q
-        kk = _kernel_ready(torch_mod, k, kd, pad) if plan.copy[1] or k.data_ptr() % 16 else k
-        vk = _kernel_ready(torch_mod, v, kd, pad) if plan.copy[2] or v.data_ptr() % 16 else v
+        wd, pad = plan.width, plan.pad_dim
+        qk = _kernel_ready(torch_mod, q, wd, pad) if plan.copy[0] or q.data_ptr() % 16 else q
+        kk = _kernel_ready(torch_mod, k, wd, pad) if plan.copy[1] or k.data_ptr() % 16 else k
+        vk = _kernel_ready(torch_mod, v, wd, pad) if plan.copy[2] or v.data_ptr() % 16 else v
         args = _lib.FwdArgs.from_buffer_copy(plan.args)
         if qk is not q or kk is not k or vk is not v:
             for name, t in (("q_stride", qk), ("k_stride", kk), ("v_stride", vk)):
