@@ -172,12 +172,12 @@ def test_split_knob_rejects(monkeypatch, raw, capable, msg):
 
 def test_split_capability_rule():
     ok = dict(tile_m=128, tile_n=64, accum_code=_lib.TA_ACC_FP32, kernel_head_dim=128)
-    assert flash_fwd._split_capable(**ok)
-    assert flash_fwd._split_capable(**{**ok, "kernel_head_dim": 64})
-    assert not flash_fwd._split_capable(**{**ok, "kernel_head_dim": 160})
-    assert not flash_fwd._split_capable(**{**ok, "tile_m": 64})
-    assert not flash_fwd._split_capable(**{**ok, "tile_n": 128})
-    assert not flash_fwd._split_capable(**{**ok, "accum_code": _lib.TA_ACC_INPUT})
+    assert flash_fwd._eight_wave_kernel(**ok)
+    assert flash_fwd._eight_wave_kernel(**{**ok, "kernel_head_dim": 64})
+    assert not flash_fwd._eight_wave_kernel(**{**ok, "kernel_head_dim": 160})
+    assert not flash_fwd._eight_wave_kernel(**{**ok, "tile_m": 64})
+    assert not flash_fwd._eight_wave_kernel(**{**ok, "tile_n": 128})
+    assert not flash_fwd._eight_wave_kernel(**{**ok, "accum_code": _lib.TA_ACC_INPUT})
 
 
 def test_split_kernel_symbols_exist_in_code_object():

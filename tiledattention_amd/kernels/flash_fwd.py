@@ -320,9 +320,10 @@ class _Launcher:
 _SPLIT_PLANS: dict[tuple[int, int, int, int], int] = {}
 
 
-def _split_capable(*, tile_m: int, tile_n: int, accum_code: int, kernel_head_dim: int) -> bool:
-    """Split key ranges exist for the eight-wave kernel only: tile (128, 64), fp32
-    accumulation, kernel head dim <= 128."""
+def _eight_wave_kernel(*, tile_m: int, tile_n: int, accum_code: int, kernel_head_dim: int) -> bool:
+    """Whether the configuration runs the eight-wave kernel (tile (128, 64), fp32
+    accumulation, kernel head dim <= 128): the one with split key ranges and in-place
+    padding of narrower head dims."""
     return (tile_m, tile_n) == (128, 64) and accum_code == _lib.TA_ACC_FP32 and kernel_head_dim <= 128
 
 
@@ -456,7 +457,7 @@ def _build_plan(torch_mod, lib, q, k, v, causal: bool) -> _LaunchPlan:
     # A narrower head dim that is a multiple of 8 runs in place on the eight-wave kernel
     # (ta_fwd_args.d_real: missing columns read as zero, not written); others are zero-padded
     # on the host as the reference does (flash_fwd.py:868-872) and the output is sliced.
-    pad_in_kernel = pad_dim > 0 and head_dim % 8 == 0 and _split_capable(
+    pad_in_kernel = pad_dim > 0 and head_dim % 8 == 0 and _eight_wave_kernel(
         tile_m=tile_m, tile_n=tile_n, accum_code=accum_code, kernel_head_dim=kernel_head_dim)
     width = head_dim if pad_in_kernel else kernel_head_dim
 
@@ -530,7 +531,7 @@ def _build_plan(torch_mod, lib, q, k, v, causal: bool) -> _LaunchPlan:
     args.sched = _resolve_sched(n_blocks=bh * n_qblk, causal=causal, tile_m=tile_m, tile_n=tile_n,
                                 accum_code=accum_code)
 
-    capable = _split_capable(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code,
+    capable = _eight_wave_kernel(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code,
                              kernel_head_dim=kernel_head_dim)
     plan.chunk = _resolve_split(lib, args, capable=capable)
     plan.ws_bytes = 0
