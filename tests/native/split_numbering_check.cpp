@@ -114,7 +114,7 @@ int main() {
   for (int S : seqs)
     for (int n_bh : bhs)
       for (int causal = 0; causal < 2; ++causal)
-        for (int sched = 0; sched < 2; ++sched) {
+        for (int sched = 0; sched < 3; ++sched) {
           const int len = (S + 127) / 128;
           for (int c = 0; c <= len + 1; c += (c < 8 ? 1 : 1 + c / 4)) {
             check_case(S, n_bh, causal != 0, c, sched);

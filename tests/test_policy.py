@@ -226,20 +226,26 @@ def test_dtype_codes():
 
 
 # ---------------------------------------------------------------- workgroup order (this build)
-@pytest.mark.parametrize("n,causal,tiles,accum,expected", [
-    (512, True, (128, 64), "fp32", 1),   # C3 S=8192: eight-wave kernel, one per CU -> heavy first
-    (256, True, (128, 64), "fp32", 2),   # every workgroup resident
-    (512, True, (128, 64), "input", 2),  # four-wave kernel: all 512 resident (2 per CU)
-    (1024, True, (128, 64), "input", 1),
-    (256, True, (128, 128), "fp32", 2),
-    (512, True, (128, 128), "fp32", 1),
-    (512, False, (128, 64), "fp32", 1),
-    (12, True, (128, 64), "fp32", 0),    # does not split over the 8 XCDs
+@pytest.mark.parametrize("n,causal,tiles,accum,d,expected", [
+    (512, True, (128, 64), "fp32", 128, 1),   # C3 S=8192: eight-wave kernel, one per CU -> heavy first
+    (256, True, (128, 64), "fp32", 128, 2),   # every workgroup resident
+    (512, True, (128, 64), "fp32", 64, 1),    # causal eight-wave D=64: one per CU, heavy first
+    (256, True, (128, 64), "fp32", 64, 2),
+    (512, True, (128, 64), "input", 128, 2),  # four-wave kernel: all 512 resident (2 per CU)
+    (1024, True, (128, 64), "input", 128, 1),
+    (256, True, (128, 128), "fp32", 128, 2),
+    (512, True, (128, 128), "fp32", 128, 1),
+    (512, True, (128, 128), "fp32", 64, 1),   # other tiles: one per CU at any D
+    (512, False, (128, 64), "fp32", 64, 1),
+    (12, True, (128, 64), "fp32", 128, 0),    # does not split over the 8 XCDs
 ])
-def test_sched_default(n, causal, tiles, accum, expected):
+def test_sched_default(n, causal, tiles, accum, d, expected):
+    if not causal:
+        assert ff._workgroups_per_cu(tile_m=tiles[0], tile_n=tiles[1], accum_code=_lib.TA_ACC_FP32,
+                                     head_dim=d, causal=False) == (2 if tiles == (128, 64) and d <= 64 else 1)
     code = _lib.TA_ACC_FP32 if accum == "fp32" else _lib.TA_ACC_INPUT
     assert ff._resolve_sched(n_blocks=n, causal=causal, tile_m=tiles[0], tile_n=tiles[1],
-                             accum_code=code) == expected
+                             accum_code=code, head_dim=d) == expected
 
 
 def test_sched_env(monkeypatch):

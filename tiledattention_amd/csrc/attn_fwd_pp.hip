@@ -562,11 +562,18 @@ __device__ __forceinline__ void attn_merge_body(const FwdParams& p) {
 
 // Two extern "C" entries per (dtype, D, causal, tail): the whole-row kernel
 // ta_fwd_pp_<f16|bf16>_d<D>_c<0|1>_t<0|1> and the split-key-range kernel
-// ta_fwd_pp_split_<...>; 512 threads, one workgroup per CU.
+// ta_fwd_pp_split_<...>; 512 threads, one workgroup per CU (two for non-causal D = 64
+// whole rows).
+// Non-causal D = 64 whole-row kernels are built for two workgroups per CU (at most 128
+// VGPRs; LDS 2 x 64 KiB): four waves per SIMD give the VALU-heavy D = 64 softmax more waves
+// to issue from (C4 D=64 +7 %).  Causal ones stay at one per CU, where each CU takes the
+// next, lighter tile as its heavy one ends (two resident from the start measured 5 % slower
+// on B1 H8 S8192), and so do the split kernels, the residency the split planner models.
+#define TA_PP_WAVES(D, C) ((D) == 64 && (C) == 0 ? 4 : 2)
 #define TA_PP_DEFINE(DTN, DT, D, C, T)                                                    \
   extern "C" __global__ void __launch_bounds__(512)                                       \
-      __attribute__((amdgpu_waves_per_eu(2, 2))) ta_fwd_pp_##DTN##_d##D##_c##C##_t##T(     \
-          ta::FwdParams p) {                                                              \
+      __attribute__((amdgpu_waves_per_eu(TA_PP_WAVES(D, C), TA_PP_WAVES(D, C))))           \
+      ta_fwd_pp_##DTN##_d##D##_c##C##_t##T(ta::FwdParams p) {                              \
     ta::attn_fwd_pp_body<DT, D, (C != 0), (T != 0), false>(p);                            \
   }                                                                                       \
   extern "C" __global__ void __launch_bounds__(512)                                       \

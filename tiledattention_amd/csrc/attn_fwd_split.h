@@ -86,9 +86,13 @@ struct WorkItem {
   int slot;   // partial slot, or -1 when the item is the block's only chunk
 };
 
-// Whole-row grid: one item per (b, h, query block); causal blocks are ranked heaviest
-// (longest key range) first.  sched >= 1 (with 8 | total) maps block ids per XCD as
-// xcd_order describes; otherwise block ids run head by head.
+// Whole-row grid: one item per (b, h, query block).  sched >= 1 (with 8 | total) maps
+// block ids per XCD as xcd_order describes; otherwise block ids run head by head.  Causal
+// blocks are ranked heaviest (longest key range) first; with sched 2, for grids whose
+// workgroups are all resident at once (each CU then holds two, and an XCD fills one slot
+// per CU before the next), the heavier half comes first and the lighter half follows from
+// the lightest up, so the j-th and (j + nq/2)-th blocks of a head, which share a CU, add up
+// to the same work.
 TA_HD inline WorkItem whole_item(int blk, int n_bh, int nq, int sched, bool causal) {
   const int total = nq * n_bh;
   WorkItem w;
@@ -99,7 +103,12 @@ TA_HD inline WorkItem whole_item(int blk, int n_bh, int nq, int sched, bool caus
     w.bh = blk / nq;
     j = blk - w.bh * nq;
   }
-  w.qt = causal ? nq - 1 - j : j;
+  if (causal) {
+    const int half = (nq + 1) >> 1;
+    w.qt = (sched == 2 && j >= half) ? j - half : nq - 1 - j;
+  } else {
+    w.qt = j;
+  }
   w.t_beg = 0;
   w.t_end = -1;
   w.slot = -1;

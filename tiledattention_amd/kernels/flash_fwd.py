@@ -266,17 +266,21 @@ def _resolve_sync_mode() -> str:
 _CU_COUNT = 256  # MI355X
 
 
-def _workgroups_per_cu(*, tile_m: int, tile_n: int, accum_code: int) -> int:
+def _workgroups_per_cu(*, tile_m: int, tile_n: int, accum_code: int, head_dim: int = 128,
+                       causal: bool = True) -> int:
     """Workgroups of one launch resident on a CU at once: two for the four-wave 128x64
-    kernel (input-dtype accumulation), one otherwise (the eight-wave 128x64 kernel and the
-    other tile shapes fill a CU's LDS or registers)."""
+    kernel (input-dtype accumulation) and for the non-causal eight-wave kernel at kernel
+    head dim 64 (built for 128 VGPRs, 64 KiB of LDS), one otherwise (the eight-wave kernel
+    at D = 128 or causal, and the other tile shapes, fill a CU's LDS or registers)."""
     if (tile_m, tile_n) == (128, 64) and accum_code == _lib.TA_ACC_INPUT:
+        return 2
+    if (tile_m, tile_n) == (128, 64) and head_dim <= 64 and not causal:
         return 2
     return 1
 
 
 def _resolve_sched(*, n_blocks: int, causal: bool, tile_m: int, tile_n: int,
-                   accum_code: int = _lib.TA_ACC_FP32) -> int:
+                   accum_code: int = _lib.TA_ACC_FP32, head_dim: int = 128) -> int:
     """Workgroup order.  XCD grouping needs the grid to split evenly over the 8 XCDs.  Causal
     tiles go heaviest first (each CU takes the next tile as its last one ends, pairing heavy
     with light ones); when every workgroup is resident at once there is no "next", and the
@@ -285,7 +289,8 @@ def _resolve_sched(*, n_blocks: int, causal: bool, tile_m: int, tile_n: int,
     if raw == "":
         if n_blocks % 8 != 0:
             return 0
-        resident = _CU_COUNT * _workgroups_per_cu(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code)
+        resident = _CU_COUNT * _workgroups_per_cu(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code,
+                                                  head_dim=head_dim, causal=causal)
         return 2 if causal and n_blocks <= resident else 1
     if raw not in {"0", "1", "2"}:
         raise ValueError(f"Unsupported TILEDATTN_SCHED={raw!r}. Use 0, 1 or 2.")
@@ -529,7 +534,7 @@ def _build_plan(torch_mod, lib, q, k, v, causal: bool) -> _LaunchPlan:
     args.accum = accum_code
     args.device = device_index
     args.sched = _resolve_sched(n_blocks=bh * n_qblk, causal=causal, tile_m=tile_m, tile_n=tile_n,
-                                accum_code=accum_code)
+                                accum_code=accum_code, head_dim=kernel_head_dim)
 
     capable = _eight_wave_kernel(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code,
                              kernel_head_dim=kernel_head_dim)
