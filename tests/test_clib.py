@@ -94,6 +94,32 @@ def test_argument_validation(lib, kw, status, msg):
     assert msg in _lib.last_error(lib)
 
 
+def test_grid_beyond_32bit_work_items_is_rejected_before_any_device_call(lib):
+    """The dispatch packet counts work-items in 32 bits: B1 H1024 S=2^20 D128 on the
+    eight-wave kernel is 8192 * 1024 workgroups of 512 threads = 2^32 work-items."""
+    s, h, d = 1 << 20, 1024, 128
+    st = (h * s * d, s * d, d, 1)
+    a = _args(B=1, H=h, S=s, D=d, tile_m=128, tile_n=64, accum=_lib.TA_ACC_FP32,
+              q_stride=st, k_stride=st, v_stride=st, o_stride=st)
+    assert _call(lib, a) == _lib.TA_EINVAL
+    assert "2^32 work-items" in _lib.last_error(lib)
+
+
+def test_split_grid_beyond_32bit_work_items_is_rejected(lib):
+    """Non-causal B1 H512 S=2^20 D128 in 4096-step chunks: 512 heads x 8192 blocks x 2 chunks
+    = 2^23 split workgroups of 512 threads = 2^32 work-items."""
+    s, h, d = 1 << 20, 512, 128
+    st = (h * s * d, s * d, d, 1)
+    a = _args(B=1, H=h, S=s, D=d, tile_m=128, tile_n=64, accum=_lib.TA_ACC_FP32,
+              q_stride=st, k_stride=st, v_stride=st, o_stride=st)
+    need = ctypes.c_int64(0)
+    assert lib.ta_split_workspace_size(ctypes.byref(a), 4096, ctypes.byref(need)) == _lib.TA_OK
+    assert need.value > 0
+    rc = lib.ta_sdpa_fwd_split(ctypes.byref(a), 4096, ctypes.c_void_p(0x100000), need.value, None)
+    assert rc == _lib.TA_EINVAL
+    assert "split kernel grid" in _lib.last_error(lib)
+
+
 def test_null_args_pointer(lib):
     assert lib.ta_sdpa_fwd(None, None) == _lib.TA_EINVAL
     assert "NULL" in _lib.last_error(lib)

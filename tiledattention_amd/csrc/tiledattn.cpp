@@ -175,6 +175,29 @@ ta_status get_function_locked(int device, const KernelId& id, hipFunction_t* out
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// The dispatch packet counts work-items in 32 bits: grid * block must fit.
+ta_status check_grid(int64_t blocks, unsigned block, const char* what) {
+  if (blocks * static_cast<int64_t>(block) > 0xffffffffLL)
+    return fail(TA_EINVAL, "%s grid of %lld workgroups x %u threads exceeds 2^32 work-items", what,
+                (long long)blocks, block);
+  return TA_OK;
+}
+
+// Caller holds g_mu.  Unloads every module; the launch paths resolve and launch under the
+// same lock, so no launch can use a function of a module unloaded here.
+ta_status cache_reset_locked() {
+  ta_status st = TA_OK;
+  for (auto& kv : g_modules) {
+    DeviceGuard guard(std::get<0>(kv.first));
+    hipError_t e = hipModuleUnload(kv.second);
+    if (e != hipSuccess && st == TA_OK)
+      st = fail(TA_EHIP, "hipModuleUnload: %s", hipGetErrorString(e));
+  }
+  g_modules.clear();
+  g_funcs.clear();
+  return st;
+}
+
 // ---- split key ranges ------------------------------------------------------------------
 // The eight-wave kernel (128 query rows, steps of 128 keys) can cut each query block's key
 // range into chunks of C steps counted back from its last step; every chunk is one
@@ -373,16 +396,7 @@ const char* ta_status_string(int32_t status) {
 
 ta_status ta_cache_reset(void) {
   std::lock_guard<std::mutex> lock(g_mu);
-  ta_status st = TA_OK;
-  for (auto& kv : g_modules) {
-    DeviceGuard guard(std::get<0>(kv.first));
-    hipError_t e = hipModuleUnload(kv.second);
-    if (e != hipSuccess && st == TA_OK)
-      st = fail(TA_EHIP, "hipModuleUnload: %s", hipGetErrorString(e));
-  }
-  g_modules.clear();
-  g_funcs.clear();
-  return st;
+  return cache_reset_locked();
 }
 
 int32_t ta_cache_size(void) {
@@ -392,8 +406,8 @@ int32_t ta_cache_size(void) {
 
 ta_status ta_set_code_object_dir(const char* dir) {
   if (dir == nullptr) return fail(TA_EINVAL, "code object dir is NULL");
-  ta_status st = ta_cache_reset();
   std::lock_guard<std::mutex> lock(g_mu);
+  ta_status st = cache_reset_locked();
   g_dir = dir;
   return st;
 }
@@ -421,22 +435,20 @@ ta_status ta_sdpa_fwd(const ta_fwd_args* a, void* stream) {
   const bool aligned = (a->S % a->tile_m == 0) && (a->S % a->tile_n == 0);
   const KernelId id =
       kernel_id(a->dtype, (int)a->D, a->tile_m, a->tile_n, a->causal, !aligned, a->accum);
-  hipFunction_t fn = nullptr;
-  {
-    std::lock_guard<std::mutex> lock(g_mu);
-    DeviceGuard guard(a->device);
-    if (guard.err != hipSuccess)
-      return fail(TA_EHIP, "set device %d: %s", a->device, hipGetErrorString(guard.err));
-    ta_status s = get_function_locked(a->device, id, &fn);
-    if (s != TA_OK) return s;
-  }
-
+  ta_status gst = check_grid(n_bh * n_qblk, id.block, "kernel");
+  if (gst != TA_OK) return gst;
   ta::FwdParams p;
   fill_params(a, n_bh, n_qblk, &p);
 
+  // Resolve and launch under the cache lock (a concurrent ta_cache_reset cannot unload the
+  // module in between); the launch only enqueues.
+  std::lock_guard<std::mutex> lock(g_mu);
   DeviceGuard guard(a->device);
   if (guard.err != hipSuccess)
     return fail(TA_EHIP, "set device %d: %s", a->device, hipGetErrorString(guard.err));
+  hipFunction_t fn = nullptr;
+  ta_status s = get_function_locked(a->device, id, &fn);
+  if (s != TA_OK) return s;
   void* params[] = {&p};
   const unsigned grid = static_cast<unsigned>(n_bh * n_qblk);
   hipError_t e = hipModuleLaunchKernel(fn, grid, 1, 1, id.block, 1, 1, 0,
@@ -514,6 +526,11 @@ ta_status ta_sdpa_fwd_split(const ta_fwd_args* a, int32_t chunk_steps, void* wor
   if (n_bh * l.items > 0x7fffffffLL || n_bh * l.slots * kSplitRows > 0x7fffffffLL ||
       n_bh * l.merge * kSplitRows > 0x7fffffffLL)
     return fail(TA_EINVAL, "split grid too large");
+  // merge: one thread per (row, 16-byte output chunk), 256 threads a workgroup
+  const int64_t merge_wgs = n_bh * l.merge * (kSplitRows / (256 / (a->D / 8)));
+  ta_status gst = check_grid(n_bh * l.items, 512u, "split kernel");
+  if (gst == TA_OK) gst = check_grid(merge_wgs, 256u, "merge kernel");
+  if (gst != TA_OK) return gst;
 
   const bool aligned = (a->S % a->tile_m == 0) && (a->S % a->tile_n == 0);
   const char* dt = a->dtype == TA_BF16 ? "bf16" : "f16";
@@ -523,17 +540,6 @@ ta_status ta_sdpa_fwd_split(const ta_fwd_args* a, int32_t chunk_steps, void* wor
   const KernelId sid{"attn_fwd_pp.hsaco", name, 512u};
   snprintf(name, sizeof(name), "ta_fwd_merge_%s_d%d_c%d", dt, (int)a->D, a->causal ? 1 : 0);
   const KernelId mid{"attn_fwd_pp.hsaco", name, 256u};
-  hipFunction_t sfn = nullptr, mfn = nullptr;
-  {
-    std::lock_guard<std::mutex> lock(g_mu);
-    DeviceGuard guard(a->device);
-    if (guard.err != hipSuccess)
-      return fail(TA_EHIP, "set device %d: %s", a->device, hipGetErrorString(guard.err));
-    ta_status s = get_function_locked(a->device, sid, &sfn);
-    if (s == TA_OK) s = get_function_locked(a->device, mid, &mfn);
-    if (s != TA_OK) return s;
-  }
-
   ta::FwdParams p;
   fill_params(a, n_bh, n_qblk, &p);
   const int64_t rows = n_bh * l.slots * kSplitRows;
@@ -545,16 +551,20 @@ ta_status ta_sdpa_fwd_split(const ta_fwd_args* a, int32_t chunk_steps, void* wor
   p.split_ns = static_cast<int32_t>(l.ns);
   p.split_slots = static_cast<int32_t>(l.slots);
 
+  // Resolve and launch under the cache lock, as ta_sdpa_fwd does.
+  std::lock_guard<std::mutex> lock(g_mu);
   DeviceGuard guard(a->device);
   if (guard.err != hipSuccess)
     return fail(TA_EHIP, "set device %d: %s", a->device, hipGetErrorString(guard.err));
+  hipFunction_t sfn = nullptr, mfn = nullptr;
+  ta_status s = get_function_locked(a->device, sid, &sfn);
+  if (s == TA_OK) s = get_function_locked(a->device, mid, &mfn);
+  if (s != TA_OK) return s;
   void* params[] = {&p};
   hipStream_t hs = static_cast<hipStream_t>(stream);
   hipError_t e = hipModuleLaunchKernel(sfn, static_cast<unsigned>(n_bh * l.items), 1, 1, 512, 1,
                                        1, 0, hs, params, nullptr);
   if (e != hipSuccess) return fail(TA_EHIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
-  // merge: one thread per (row, 16-byte output chunk), 256 threads a workgroup
-  const int64_t merge_wgs = n_bh * l.merge * (kSplitRows / (256 / (a->D / 8)));
   e = hipModuleLaunchKernel(mfn, static_cast<unsigned>(merge_wgs), 1, 1, 256, 1, 1, 0, hs, params,
                             nullptr);
   if (e != hipSuccess) return fail(TA_EHIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
