@@ -17,7 +17,10 @@
  *   - Calls are asynchronous with respect to the host (work is enqueued on `stream`).
  *   - Every entry point returns a ta_status; on a non-OK status ta_last_error() returns a
  *     message for the calling thread.  No C++ exception crosses the boundary.
- *   - Thread-safe: the kernel cache is guarded by a mutex.
+ *   - Thread-safe: the kernel cache is guarded by a mutex, and a launch resolves its kernel
+ *     and enqueues it under that mutex, so ta_cache_reset / ta_set_code_object_dir never
+ *     unload a module a concurrent launch is using (launches from several threads
+ *     serialize for the few microseconds of the enqueue).
  */
 #ifndef TILEDATTN_H_
 #define TILEDATTN_H_
