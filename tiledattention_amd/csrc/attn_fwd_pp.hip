@@ -67,6 +67,9 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   constexpr int NLD = STAGE / 1024 / 8;  // loads per wave per tensor per step (own half)
   static_assert(STAGE % (8 * 1024) == 0, "stage must split over the eight waves");
   static_assert(TM == kPPRows && TK == kPPKeys, "grid numbering assumes 128 x 128 steps");
+  // Raised MFMA-cluster priority only in the kernels built for two workgroups per CU (the
+  // non-causal D = 64 whole-row ones, TA_PP_WAVES below).
+  constexpr bool kPrioMfma = !SPLIT && D == 64 && !CAUSAL;
   using DTy = DType<DT>;
 
   // One array per (tensor, stage): the stage of every access is a compile-time constant
@@ -401,18 +404,20 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
     softmax(t);
     wait_dma();  // this group's halves of K_{t+1} and V_t (issued one MFMA cluster ago)
     barrier();
-    // MFMA cluster at raised priority, so that the softmax wave on the same SIMD does not
-    // delay its issue: S of step t + 1 (past the last step it reads a stale or zero stage
-    // and is never used) and P.V of step t, one straight-line block whose LDS reads run
-    // AHEAD MFMAs in front of their consumers, with this wave's loads of K_{t+2} and
-    // V_{t+1} spread over it.
-    __builtin_amdgcn_s_setprio(1);
+    // MFMA cluster: S of step t + 1 (past the last step it reads a stale or zero stage and
+    // is never used) and P.V of step t, one straight-line block whose LDS reads run AHEAD
+    // MFMAs in front of their consumers, with this wave's loads of K_{t+2} and V_{t+1}
+    // spread over it.  Both clusters run at the same priority (the softmax cluster is the
+    // longer one, and giving the MFMA cluster priority cost 1-4 %), except in the kernels
+    // that share a CU between two workgroups, where raising it keeps the two workgroups'
+    // MFMA clusters from delaying each other (2.5 % there).
+    if constexpr (kPrioMfma) __builtin_amdgcn_s_setprio(1);
     qk(k_nxt);
     pv(v_cur);
     dma(kp, p.k_ss, k_rb, kvo, t + 2, k_cur);
     dma(vp, p.v_ss, v_rb, vvo, t + 1, v_nxt);
     mfma_cluster_order(2 * NLD);
-    __builtin_amdgcn_s_setprio(0);
+    if constexpr (kPrioMfma) __builtin_amdgcn_s_setprio(0);
     barrier();
   };
   if (grp == 0) {
