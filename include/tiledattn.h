@@ -74,7 +74,7 @@ typedef struct ta_fwd_args {
                       D): the kernel for D reads the missing columns as zero and does not
                       write them, so a narrower head dim needs no padded copies (the
                       reference pads on the host, flash_fwd.py:868-872).  Tile (128, 64)
-                      with fp32 accumulation and D <= 128 only. */
+                      with fp32 accumulation and D <= 160 only. */
 } ta_fwd_args;
 
 /* Version of this ABI (TA_ABI_VERSION). */

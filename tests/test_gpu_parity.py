@@ -196,6 +196,35 @@ def test_wide_head_dims(gpu, dtype, d, tiles):
         check_close(as_f32(out), oracle_f32(q, k, v, causal=causal), dtype, what=f"D={d}")
 
 
+@pytest.mark.parametrize("d,dtype,causal,s", [
+    (160, "bfloat16", True, 2048), (160, "float16", False, 1000), (152, "bfloat16", False, 777),
+    (136, "float16", True, 3000),
+])
+def test_eight_wave_d160(gpu, d, dtype, causal, s):
+    """Kernel head dim 160 on the eight-wave kernel (default tile (128, 64)): stages split
+    into a 128-column part and a 32-column tail part; head dims 129-159 run in place with
+    the missing tail columns read as zero.  Ragged S, both dtypes, [B,S,H,D] views."""
+    import torch
+
+    from tiledattention_amd import _lib, sdpa
+
+    assert _lib.kernel_symbol(dtype=_lib.TA_BF16, head_dim=160, tile_m=128, tile_n=64,
+                              causal=causal, tail=False, accum=_lib.TA_ACC_FP32)[1].startswith("ta_fwd_pp_")
+    q, k, v = inputs((2, 3, s, d), dtype, 160 + d + s)
+    rows = None if s <= 2048 else sample_rows(s, 96)
+    ref = oracle_f32(q, k, v, causal=causal, rows=rows)
+    say(f"eight-wave D={d} {dtype} (2,3,{s},{d}) causal={causal}")
+    out = run_gpu(q, k, v, causal=causal)
+    assert out.shape == (2, 3, s, d) and out.is_contiguous()
+    check_close(as_f32(out, rows), ref, dtype, what=f"eight-wave D={d}")
+    dev = torch.device("cuda:0")
+    bshd = [t.transpose(1, 2).contiguous().to(dev).transpose(1, 2) for t in (q, k, v)]
+    say(f"eight-wave D={d} {dtype} (2,3,{s},{d}) causal={causal} [B,S,H,D] views")
+    out = sdpa(*bshd, causal=causal)
+    torch.cuda.synchronize()
+    check_close(as_f32(out, rows), ref, dtype, what=f"eight-wave D={d} BSHD")
+
+
 @pytest.mark.parametrize("d", [144, 200])
 def test_wide_head_dim_padding(gpu, d):
     """D in (128, 256] outside {160, 256}: padded to the next wide kernel."""

@@ -172,12 +172,19 @@ def test_split_knob_rejects(monkeypatch, raw, capable, msg):
 
 def test_split_capability_rule():
     ok = dict(tile_m=128, tile_n=64, accum_code=_lib.TA_ACC_FP32, kernel_head_dim=128)
-    assert flash_fwd._eight_wave_kernel(**ok)
-    assert flash_fwd._eight_wave_kernel(**{**ok, "kernel_head_dim": 64})
-    assert not flash_fwd._eight_wave_kernel(**{**ok, "kernel_head_dim": 160})
-    assert not flash_fwd._eight_wave_kernel(**{**ok, "tile_m": 64})
-    assert not flash_fwd._eight_wave_kernel(**{**ok, "tile_n": 128})
-    assert not flash_fwd._eight_wave_kernel(**{**ok, "accum_code": _lib.TA_ACC_INPUT})
+    for rule in (flash_fwd._eight_wave_kernel, flash_fwd._split_capable):
+        assert rule(**ok)
+        assert rule(**{**ok, "kernel_head_dim": 64})
+        assert not rule(**{**ok, "kernel_head_dim": 256})
+        assert not rule(**{**ok, "tile_m": 64})
+        assert not rule(**{**ok, "tile_n": 128})
+        assert not rule(**{**ok, "accum_code": _lib.TA_ACC_INPUT})
+    # D = 160 runs the eight-wave kernel on whole rows only.
+    assert flash_fwd._eight_wave_kernel(**{**ok, "kernel_head_dim": 160})
+    assert not flash_fwd._split_capable(**{**ok, "kernel_head_dim": 160})
+    with pytest.raises(ValueError, match="D <= 128"):
+        _lib.kernel_symbol(dtype=_lib.TA_BF16, head_dim=160, tile_m=128, tile_n=64, causal=True,
+                           tail=False, accum=_lib.TA_ACC_FP32, split=True)
 
 
 def test_split_kernel_symbols_exist_in_code_object():

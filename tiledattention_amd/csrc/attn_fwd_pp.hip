@@ -58,14 +58,26 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   constexpr int TM = 128;            // query rows per workgroup
   constexpr int TK = 128;            // keys per workgroup step (64 per wave group)
   constexpr int KB = 2;              // 32-key blocks per wave per step
+  // A stage holds 128 key rows: the first DA = min(D, 128) columns of each row in a main
+  // part (rows of 2 DA bytes), the rest (D = 160: 32 columns) in a tail part of 64-byte
+  // rows behind it, so both parts have power-of-two rows.
+  constexpr int DA = D > 128 ? 128 : D;
+  constexpr int DT2 = D - DA;        // tail columns
+  static_assert(DT2 == 0 || DT2 == 32, "head dims 64, 128 and 160");
   constexpr int DK = D / 16;         // k-steps of the QK^T product
+  constexpr int DKA = DA / 16;       // ... whose K operand is in the main part
   constexpr int DB = D / 32;         // 32-wide d blocks of O
-  constexpr int CPR = D / 8;         // 16-byte chunks per row
-  constexpr int RB = 2 * D;          // bytes per LDS row
-  constexpr int STAGE = TK * RB;     // bytes of one K or V stage
-  constexpr int RPL = 1024 / RB;     // rows one wave instruction fills
-  constexpr int NLD = STAGE / 1024 / 8;  // loads per wave per tensor per step (own half)
-  static_assert(STAGE % (8 * 1024) == 0, "stage must split over the eight waves");
+  constexpr int DBA = DA / 32;       // ... whose V operand is in the main part
+  constexpr int CPR = DA / 8;        // 16-byte chunks per main-part row
+  constexpr int RB = 2 * DA;         // bytes per main-part row
+  constexpr int RBT = 2 * DT2;       // bytes per tail row
+  constexpr int STAGE_A = TK * RB;   // bytes of a stage's main part
+  constexpr int STAGE = TK * (RB + RBT);  // bytes of one K or V stage
+  constexpr int RPL = 1024 / RB;     // main-part rows one wave instruction fills
+  constexpr int NLD = STAGE_A / 1024 / 8;  // main-part loads per wave per tensor per step
+  constexpr int NLDT = DT2 ? 1 : 0;  // tail loads (a group's 64 tail rows are 4 KiB)
+  constexpr int NLDS = NLD + NLDT;   // loads per wave per tensor per step (own half)
+  static_assert(STAGE_A % (8 * 1024) == 0, "stage must split over the eight waves");
   static_assert(TM == kPPRows && TK == kPPKeys, "grid numbering assumes 128 x 128 steps");
   // Raised MFMA-cluster priority only in the kernels built for two workgroups per CU (the
   // non-causal D = 64 whole-row ones, TA_PP_WAVES below).
@@ -158,11 +170,22 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   // here spans less than 2^31 bytes, so it reads zero (and the per-load row steps added
   // below stay far from 2^32).
   constexpr int kZeroChunk = INT32_MIN;
-  const int lck = ld_pc ^ pp_swz_k<D>(ld_row);
-  const int lcv = ld_pc ^ pp_swz_v<D>(ld_row);
+  const int lck = ld_pc ^ pp_swz_k<DA>(ld_row);
+  const int lcv = ld_pc ^ pp_swz_v<DA>(ld_row);
   const int kvo = 8 * lck < d_real ? ld_row * k_rb + (lck << 4) : kZeroChunk;
   const int vvo = 8 * lcv < d_real ? ld_row * v_rb + (lcv << 4) : kZeroChunk;
-  auto dma = [&](const uint16_t* gbase, int64_t row_stride, int rb, int vo, int t, char* stage) {
+  // Tail part: wave (grp, wr) fills the group's tail rows koff + 16 wr .. + 15, lane l
+  // writing physical chunk l % 4 of row l / 4 of them.  K's tail chunks are swizzled with
+  // (row >> 2) & 3 (a b128 read pass covers 16 consecutive rows at one chunk, rows 256
+  // bytes apart repeat every 4); V's tail needs none (a transposed read pass covers 4 rows
+  // x 64 bytes).  For these rows (row >> 2) & 3 = (l >> 4) & 3.
+  const int tl_row = koff + 16 * wr + (lane >> 2);
+  const int tl_lck = (lane & 3) ^ ((lane >> 4) & 3);
+  const int tl_lcv = lane & 3;
+  const int tkvo = DA + 8 * tl_lck < d_real ? tl_row * k_rb + 2 * DA + (tl_lck << 4) : kZeroChunk;
+  const int tvvo = DA + 8 * tl_lcv < d_real ? tl_row * v_rb + 2 * DA + (tl_lcv << 4) : kZeroChunk;
+  auto dma = [&](const uint16_t* gbase, int64_t row_stride, int rb, int vo, int tvo, int t,
+                 char* stage) {
     const int row0 = t * TK;
     const int rows = t < t_end ? S - row0 : 0;
     const __amdgpu_buffer_rsrc_t r = row_rsrc(gbase + (int64_t)row0 * row_stride, rows, rb);
@@ -171,6 +194,11 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           r, (__attribute__((address_space(3))) void*)(stage + (ld_g0 + 4 * i) * 1024), 16,
           vo + i * 4 * RPL * rb, 0, 0, 0);
+    }
+    if constexpr (NLDT != 0) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          r, (__attribute__((address_space(3))) void*)(stage + STAGE_A + koff * RBT + wr * 1024),
+          16, tvo, 0, 0, 0);
     }
   };
   // Wait for this wave's direct-to-LDS loads (vmcnt = 0; expcnt and lgkmcnt left at their
@@ -181,8 +209,12 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   // K: lane reads row koff + 32 bk + l32 at logical chunk 2 kk + hl; with m = swz_k(l32)
   // that is byte (koff + l32) * RB + (32 * (m >> 1) + 16 * (hl ^ (m & 1))) ^ (32 kk), plus
   // 32 * bk * RB.
-  const int mk = pp_swz_k<D>(l32);
+  const int mk = pp_swz_k<DA>(l32);
   const int k_rd = (koff + l32) * RB + 32 * (mk >> 1) + 16 * (hl ^ (mk & 1));
+  // K tail (k-steps DKA, DKA + 1): logical chunk 2 (kk - DKA) + hl of tail row
+  // koff + 32 bk + l32, physical chunk logical ^ ((l32 >> 2) & 3): byte
+  // kt_rd ^ (32 (kk - DKA)) of the tail part, plus 32 * bk * RBT.
+  const int kt_rd = (koff + l32) * RBT + 16 * (hl ^ ((l32 >> 2) & 3));
   // V^T via the transposed read: lane l of 16-lane group G addresses row 4 hl + r,
   // r = (l % 16) / 4, of a 16-key chunk and d = 32 db + 16 (G % 2) + 4 (l % 4); the hardware
   // hands lane l column 32 db + 16 (G % 2) + l % 16 of those 4 rows.  swz_v depends only on
@@ -190,7 +222,9 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   const int tr_r = (lane & 15) >> 2;
   const int tr_d = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
   const int v_rd = (koff + 4 * hl + tr_r) * RB +
-                   16 * ((tr_d >> 3) ^ pp_swz_v<D>(4 * hl + tr_r)) + 2 * (tr_d & 7);
+                   16 * ((tr_d >> 3) ^ pp_swz_v<DA>(4 * hl + tr_r)) + 2 * (tr_d & 7);
+  // V tail (d block DBA): the same rows and columns tr_d of the unswizzled 64-byte tail rows.
+  const int vt_rd = (koff + 4 * hl + tr_r) * RBT + 2 * tr_d;
 
   // ---- running state (lane = query l32 of this wave) ----------------------------------
   float m_run = kNegLarge;
@@ -218,7 +252,9 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
     for (int kk = 0; kk < DK; ++kk) {
 #pragma unroll
       for (int bk = 0; bk < KB; ++bk) {
-        const u32x4 a = *(const u32x4*)(kst + bk * 32 * RB + (k_rd ^ (32 * kk)));
+        const char* ap = kk < DKA ? kst + bk * 32 * RB + (k_rd ^ (32 * kk))
+                                  : kst + STAGE_A + bk * 32 * RBT + (kt_rd ^ (32 * (kk - DKA)));
+        const u32x4 a = *(const u32x4*)ap;
         s[bk] = DTy::mfma(a, qf[kk], kk == 0 ? f32x16{} : s[bk]);
       }
     }
@@ -235,9 +271,11 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
                              pk[bk][4 * kc + 3]};
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-          const char* a0p = vst + (v_rd ^ (64 * db)) + (32 * bk + 16 * kc) * RB;
+          const int rbd = db < DBA ? RB : RBT;  // row bytes of the part holding d block db
+          const char* a0p = db < DBA ? vst + (v_rd ^ (64 * db)) + (32 * bk + 16 * kc) * RB
+                                     : vst + STAGE_A + vt_rd + (32 * bk + 16 * kc) * RBT;
           s16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)a0p);
-          s16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a0p + 8 * RB));
+          s16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a0p + 8 * rbd));
           u32x2 w0 = __builtin_bit_cast(u32x2, r0);
           u32x2 w1 = __builtin_bit_cast(u32x2, r1);
           const u32x4 a = {w0[0], w0[1], w1[0], w1[1]};
@@ -378,17 +416,17 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   // Both groups run the same sequence, group 1 one phase later.
   //
   // Prologue: every wave issues its share of K_0, its Q fragment, and its group's halves of
-  // K_1 and V_0, then waits until at most the last 2 NLD loads (K_1 and V_0) are in flight:
+  // K_1 and V_0, then waits until at most the last 2 NLDS loads (K_1 and V_0) are in flight:
   // K_0 and Q have landed, and the latencies of all four overlap.  The Q fragment is
   // complete before the loop on every path, so the waitcnt insertion carries no pending
   // load into it.  K_1 and V_0 are waited for at the end of the group's first softmax
   // cluster, like the loads of every MFMA cluster.
-  static_assert(2 * NLD < 16, "vmcnt field");
-  dma(kp, p.k_ss, k_rb, kvo, t_beg, lds_k0);
+  static_assert(2 * NLDS < 16, "vmcnt field");
+  dma(kp, p.k_ss, k_rb, kvo, tkvo, t_beg, lds_k0);
   load_q();
-  dma(kp, p.k_ss, k_rb, kvo, t_beg + 1, lds_k1);
-  dma(vp, p.v_ss, v_rb, vvo, t_beg, lds_v0);
-  __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * NLD));
+  dma(kp, p.k_ss, k_rb, kvo, tkvo, t_beg + 1, lds_k1);
+  dma(vp, p.v_ss, v_rb, vvo, tvvo, t_beg, lds_v0);
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * NLDS));
   barrier();
   // S_0.
   auto first = [&]() { qk(lds_k0); };
@@ -414,9 +452,9 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
     if constexpr (kPrioMfma) __builtin_amdgcn_s_setprio(1);
     qk(k_nxt);
     pv(v_cur);
-    dma(kp, p.k_ss, k_rb, kvo, t + 2, k_cur);
-    dma(vp, p.v_ss, v_rb, vvo, t + 1, v_nxt);
-    mfma_cluster_order(2 * NLD);
+    dma(kp, p.k_ss, k_rb, kvo, tkvo, t + 2, k_cur);
+    dma(vp, p.v_ss, v_rb, vvo, tvvo, t + 1, v_nxt);
+    mfma_cluster_order(2 * NLDS);
     if constexpr (kPrioMfma) __builtin_amdgcn_s_setprio(0);
     barrier();
   };
@@ -602,7 +640,21 @@ __device__ __forceinline__ void attn_merge_body(const FwdParams& p) {
   TA_MERGE_DEFINE(DTN, DT, D, 0)    \
   TA_MERGE_DEFINE(DTN, DT, D, 1)
 
+// D = 160: whole-row kernels only (160 KiB of LDS: four stages of 128 rows x 320 bytes).
+#define TA_PP_DEFINE_WHOLE(DTN, DT, D, C, T)                                              \
+  extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) \
+      ta_fwd_pp_##DTN##_d##D##_c##C##_t##T(ta::FwdParams p) {                              \
+    ta::attn_fwd_pp_body<DT, D, (C != 0), (T != 0), false>(p);                            \
+  }
+#define TA_PP_DEFINE_WHOLE_CT(DTN, DT, D) \
+  TA_PP_DEFINE_WHOLE(DTN, DT, D, 0, 0)    \
+  TA_PP_DEFINE_WHOLE(DTN, DT, D, 0, 1)    \
+  TA_PP_DEFINE_WHOLE(DTN, DT, D, 1, 0)    \
+  TA_PP_DEFINE_WHOLE(DTN, DT, D, 1, 1)
+
 TA_PP_DEFINE_CT(f16, 0, 64)
 TA_PP_DEFINE_CT(f16, 0, 128)
+TA_PP_DEFINE_WHOLE_CT(f16, 0, 160)
 TA_PP_DEFINE_CT(bf16, 1, 64)
 TA_PP_DEFINE_CT(bf16, 1, 128)
+TA_PP_DEFINE_WHOLE_CT(bf16, 1, 160)

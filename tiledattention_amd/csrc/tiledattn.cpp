@@ -92,9 +92,9 @@ struct KernelId {
 KernelId kernel_id(int dtype, int d, int tm, int tn, int causal, int tail, int accum) {
   const char* dt = dtype == TA_BF16 ? "bf16" : "f16";
   char buf[96];
-  if (tm == 128 && tn == 64 && accum == TA_ACC_FP32 && d <= 128) {
+  if (tm == 128 && tn == 64 && accum == TA_ACC_FP32 && d <= 160) {
     // Eight waves: two per SIMD sharing the rows of a 32-row block, splitting every
-    // 128-key step between them (attn_fwd_pp.hip).
+    // 128-key step between them (attn_fwd_pp.hip; D = 64, 128 and 160).
     snprintf(buf, sizeof(buf), "ta_fwd_pp_%s_d%d_c%d_t%d", dt, d, causal ? 1 : 0, tail ? 1 : 0);
     return {"attn_fwd_pp.hsaco", buf, 512u};
   }
@@ -311,8 +311,8 @@ ta_status validate_args(const ta_fwd_args* a, int64_t* n_bh_out, int64_t* n_qblk
   if (a->d_real != 0) {
     if (a->d_real < 8 || a->d_real > a->D || (a->d_real & 7) != 0)
       return fail(TA_EINVAL, "d_real %d (0, or a multiple of 8 in [8, D])", a->d_real);
-    if (!(a->tile_m == kSplitRows && a->tile_n == 64 && a->accum == TA_ACC_FP32 && a->D <= 128))
-      return fail(TA_EUNSUPPORTED, "d_real needs tile (128, 64), fp32 accumulation and D <= 128");
+    if (!(a->tile_m == kSplitRows && a->tile_n == 64 && a->accum == TA_ACC_FP32 && a->D <= 160))
+      return fail(TA_EUNSUPPORTED, "d_real needs tile (128, 64), fp32 accumulation and D <= 160");
   }
   if (a->B < 0 || a->H < 0 || a->S < 0) return fail(TA_EINVAL, "negative shape");
   ta_status shape_st = check_shape(a->D, a->tile_m, a->tile_n);
@@ -370,7 +370,8 @@ void fill_params(const ta_fwd_args* a, int64_t n_bh, int64_t n_qblk, ta::FwdPara
   p->d_real = a->d_real ? a->d_real : static_cast<int32_t>(a->D);
 }
 
-// Whether the split path exists for this configuration (the eight-wave kernel).
+// Whether the split path exists for this configuration (the eight-wave kernel, D <= 128:
+// at D = 160 its stages fill the LDS and its merge kernel's rows do not tile 256 threads).
 bool split_capable(const ta_fwd_args* a) {
   return a->tile_m == kSplitRows && a->tile_n == 64 && a->accum == TA_ACC_FP32 && a->D <= 128;
 }
