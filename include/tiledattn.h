@@ -102,7 +102,7 @@ ta_status ta_sdpa_fwd(const ta_fwd_args* args, void* stream);
  * longest rows finish.  The split path cuts every 128-row query block's keys into chunks of
  * `chunk_steps` steps of 128 keys, runs one workgroup per chunk, and merges the chunks of a
  * block (log-sum-exp weights) in a second kernel on the same stream.  It exists for tile
- * (128, 64) with fp32 accumulation and D <= 128; the result matches ta_sdpa_fwd within
+ * (128, 64) with fp32 accumulation and D <= 160; the result matches ta_sdpa_fwd within
  * fp32 rounding of the merge. */
 
 /* Chunk length (key steps) this library would use for `args` on its device: 0 when the

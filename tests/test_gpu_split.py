@@ -28,6 +28,9 @@ pytestmark = pytest.mark.gpu
     ((1, 4, 2304, 128), "float16", True, (5,)),
     ((1, 1, 129, 128), "bfloat16", True, (1,)),
     ((1, 1, 129, 64), "float16", False, (1,)),
+    ((1, 4, 1300, 160), "bfloat16", True, (1, 3)),
+    ((2, 2, 900, 160), "float16", False, (2,)),
+    ((1, 3, 1000, 144), "bfloat16", True, (2,)),   # in-kernel padding to 160
 ])
 def test_forced_chunks_match_oracle(gpu, shape, dtype, causal, chunks):
     q, k, v = inputs(shape, dtype, 300 + shape[2])
@@ -40,7 +43,7 @@ def test_forced_chunks_match_oracle(gpu, shape, dtype, causal, chunks):
         check_close(as_f32(out), ref, dtype, what=f"split chunk={chunk}")
 
 
-@pytest.mark.parametrize("shape", [(1, 8, 2048, 128), (1, 1, 8192, 128), (1, 2, 4096, 128)])
+@pytest.mark.parametrize("shape", [(1, 8, 2048, 128), (1, 1, 8192, 128), (1, 2, 4096, 128), (1, 8, 2048, 160)])
 def test_split_and_whole_rows_agree(gpu, shape):
     """bf16 causal, seed 1234, forced 8-step chunks (C3's shape) and the automatic plan
     (which splits the B*H = 1 and 2 shapes): both paths meet the oracle's tolerance and
@@ -143,7 +146,8 @@ def test_cabi_split_with_caller_workspace(gpu):
     dev = torch.device("cuda:0")
     ws = torch.full((64 << 20,), 0x7f, dtype=torch.uint8, device=dev)  # NaN-ish bytes
     stream = torch.cuda.current_stream(dev).cuda_stream
-    for shape, causal, chunk in (((1, 4, 1536, 128), 1, 2), ((1, 2, 700, 64), 0, 1)):
+    for shape, causal, chunk in (((1, 4, 1536, 128), 1, 2), ((1, 2, 700, 64), 0, 1),
+                                 ((1, 2, 700, 160), 1, 2)):
         q, k, v = inputs(shape, "bfloat16", 11 + shape[2])
         qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
         o = torch.empty_like(qd)

@@ -69,7 +69,7 @@ def _slots(S: int, causal: bool, chunk: int) -> int:
 @pytest.mark.parametrize("S", [129, 1000, 1024, 2048, 4096, 5000])
 @pytest.mark.parametrize("causal", [0, 1])
 @pytest.mark.parametrize("chunk", [1, 2, 3, 7, 16])
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [64, 128, 160])
 def test_workspace_size_is_one_fp32_partial_per_chunk_of_a_split_block(lib, S, causal, chunk, D):
     a = _args(S=S, B=2, H=3, D=D, causal=causal)
     out = ctypes.c_int64(-1)
@@ -87,7 +87,7 @@ def test_workspace_size_edge_cases(lib):
     # a chunk as long as the longest row splits nothing
     assert lib.ta_split_workspace_size(ctypes.byref(_args(S=4096)), 32, ctypes.byref(out)) == _lib.TA_OK
     assert out.value == 0
-    for kw in (dict(tile_m=64), dict(tile_n=128), dict(accum=_lib.TA_ACC_INPUT), dict(D=160)):
+    for kw in (dict(tile_m=64), dict(tile_n=128), dict(accum=_lib.TA_ACC_INPUT), dict(D=256)):
         st = lib.ta_split_workspace_size(ctypes.byref(_args(S=4096, **kw)), 4, ctypes.byref(out))
         assert st == _lib.TA_EUNSUPPORTED, kw
         assert "split key ranges" in _lib.last_error(lib)
@@ -172,25 +172,23 @@ def test_split_knob_rejects(monkeypatch, raw, capable, msg):
 
 def test_split_capability_rule():
     ok = dict(tile_m=128, tile_n=64, accum_code=_lib.TA_ACC_FP32, kernel_head_dim=128)
-    for rule in (flash_fwd._eight_wave_kernel, flash_fwd._split_capable):
-        assert rule(**ok)
-        assert rule(**{**ok, "kernel_head_dim": 64})
-        assert not rule(**{**ok, "kernel_head_dim": 256})
-        assert not rule(**{**ok, "tile_m": 64})
-        assert not rule(**{**ok, "tile_n": 128})
-        assert not rule(**{**ok, "accum_code": _lib.TA_ACC_INPUT})
-    # D = 160 runs the eight-wave kernel on whole rows only.
-    assert flash_fwd._eight_wave_kernel(**{**ok, "kernel_head_dim": 160})
-    assert not flash_fwd._split_capable(**{**ok, "kernel_head_dim": 160})
-    with pytest.raises(ValueError, match="D <= 128"):
-        _lib.kernel_symbol(dtype=_lib.TA_BF16, head_dim=160, tile_m=128, tile_n=64, causal=True,
+    rule = flash_fwd._eight_wave_kernel
+    assert rule(**ok)
+    assert rule(**{**ok, "kernel_head_dim": 64})
+    assert rule(**{**ok, "kernel_head_dim": 160})
+    assert not rule(**{**ok, "kernel_head_dim": 256})
+    assert not rule(**{**ok, "tile_m": 64})
+    assert not rule(**{**ok, "tile_n": 128})
+    assert not rule(**{**ok, "accum_code": _lib.TA_ACC_INPUT})
+    with pytest.raises(ValueError, match="D <= 160"):
+        _lib.kernel_symbol(dtype=_lib.TA_BF16, head_dim=256, tile_m=128, tile_n=64, causal=True,
                            tail=False, accum=_lib.TA_ACC_FP32, split=True)
 
 
 def test_split_kernel_symbols_exist_in_code_object():
     data = (_lib.lib_dir() / "attn_fwd_pp.hsaco").read_bytes()
     for dtype, dt in ((_lib.TA_FP16, "f16"), (_lib.TA_BF16, "bf16")):
-        for d in (64, 128):
+        for d in (64, 128, 160):
             for causal in (0, 1):
                 for tail in (0, 1):
                     f, sym = _lib.kernel_symbol(dtype=dtype, head_dim=d, tile_m=128, tile_n=64,

@@ -39,12 +39,10 @@ def kernel_symbol(*, dtype: int, head_dim: int, tile_m: int, tile_n: int, causal
     dt = "bf16" if dtype == TA_BF16 else "f16"
     c, t = int(bool(causal)), int(bool(tail))
     if (tile_m, tile_n) == (128, 64) and accum == TA_ACC_FP32 and head_dim <= 160:
-        if split and head_dim > 128:
-            raise ValueError("split key ranges exist for tile (128, 64), fp32 accumulation, D <= 128")
         kind = "pp_split" if split else "pp"
         return "attn_fwd_pp.hsaco", f"ta_fwd_{kind}_{dt}_d{head_dim}_c{c}_t{t}"
     if split:
-        raise ValueError("split key ranges exist for tile (128, 64), fp32 accumulation, D <= 128")
+        raise ValueError("split key ranges exist for tile (128, 64), fp32 accumulation, D <= 160")
     return (f"attn_fwd_m{tile_m}_n{tile_n}.hsaco",
             f"ta_fwd_{dt}_d{head_dim}_m{tile_m}_n{tile_n}_c{c}_t{t}_a{int(accum != TA_ACC_FP32)}")
 

@@ -557,17 +557,17 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
 // stream): per row, with L_i the chunks' log-sum-exps, O = sum_i 2^(L_i - max L) O_i /
 // sum_i 2^(L_i - max L), the same rescale the online softmax applies between key tiles,
 // here folded into one pass over the chunks (running max, weights rescaled when it grows).
-// One thread per (row, 16-byte output chunk): a workgroup of 256 threads covers 256 / (D/8)
-// rows, so a split block takes 128 / (256 / (D/8)) workgroups; the partial reads of the
-// chunks are independent and contiguous across the D/8 threads of a row, and a row is
-// written by those threads as one contiguous run.
+// One thread per (row, 16-byte output chunk): a workgroup covers merge_rows_per_wg(D) rows
+// (merge_threads(D) threads), so a split block takes 128 / merge_rows_per_wg(D)
+// workgroups; the partial reads of the chunks are independent and contiguous across the
+// D/8 threads of a row, and a row is written by those threads as one contiguous run.
 template <int DT, int D, bool CAUSAL>
 __device__ __forceinline__ void attn_merge_body(const FwdParams& p) {
   constexpr int TM = kPPRows;
   constexpr int CH = D / 8;        // 16-byte output chunks per row
-  constexpr int RPW = 256 / CH;    // rows per workgroup
-  constexpr int WPB = TM / RPW;    // workgroups per split block
-  static_assert(256 % CH == 0 && TM % RPW == 0, "workgroups must cover whole rows");
+  constexpr int RPW = merge_rows_per_wg(D);  // rows per workgroup
+  constexpr int WPB = TM / RPW;              // workgroups per split block
+  static_assert(merge_threads(D) <= 256 && TM % RPW == 0, "workgroups must cover whole rows");
   using DTy = DType<DT>;
   const int blk = blockIdx.x / WPB;
   const MergeItem mi = merge_item(blk, p.n_qblk, CAUSAL, p.split_c, p.split_ns, p.split_slots);
@@ -625,7 +625,8 @@ __device__ __forceinline__ void attn_merge_body(const FwdParams& p) {
     ta::attn_fwd_pp_body<DT, D, (C != 0), (T != 0), true>(p);                             \
   }
 
-// Merge kernels of the split path: ta_fwd_merge_<f16|bf16>_d<D>_c<0|1>, 256 threads.
+// Merge kernels of the split path: ta_fwd_merge_<f16|bf16>_d<D>_c<0|1>, merge_threads(D)
+// threads.
 #define TA_MERGE_DEFINE(DTN, DT, D, C)                                                     \
   extern "C" __global__ void __launch_bounds__(256) ta_fwd_merge_##DTN##_d##D##_c##C(      \
       ta::FwdParams p) {                                                                  \
@@ -640,21 +641,9 @@ __device__ __forceinline__ void attn_merge_body(const FwdParams& p) {
   TA_MERGE_DEFINE(DTN, DT, D, 0)    \
   TA_MERGE_DEFINE(DTN, DT, D, 1)
 
-// D = 160: whole-row kernels only (160 KiB of LDS: four stages of 128 rows x 320 bytes).
-#define TA_PP_DEFINE_WHOLE(DTN, DT, D, C, T)                                              \
-  extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) \
-      ta_fwd_pp_##DTN##_d##D##_c##C##_t##T(ta::FwdParams p) {                              \
-    ta::attn_fwd_pp_body<DT, D, (C != 0), (T != 0), false>(p);                            \
-  }
-#define TA_PP_DEFINE_WHOLE_CT(DTN, DT, D) \
-  TA_PP_DEFINE_WHOLE(DTN, DT, D, 0, 0)    \
-  TA_PP_DEFINE_WHOLE(DTN, DT, D, 0, 1)    \
-  TA_PP_DEFINE_WHOLE(DTN, DT, D, 1, 0)    \
-  TA_PP_DEFINE_WHOLE(DTN, DT, D, 1, 1)
-
 TA_PP_DEFINE_CT(f16, 0, 64)
 TA_PP_DEFINE_CT(f16, 0, 128)
-TA_PP_DEFINE_WHOLE_CT(f16, 0, 160)
+TA_PP_DEFINE_CT(f16, 0, 160)
 TA_PP_DEFINE_CT(bf16, 1, 64)
 TA_PP_DEFINE_CT(bf16, 1, 128)
-TA_PP_DEFINE_WHOLE_CT(bf16, 1, 160)
+TA_PP_DEFINE_CT(bf16, 1, 160)

@@ -17,6 +17,14 @@ namespace ta {
 constexpr int kPPRows = 128;  // query rows per block
 constexpr int kPPKeys = 128;  // keys per step
 
+// Merge kernel workgroup: one thread per (row, 16-byte output chunk), the largest power of
+// two of rows whose D / 8 threads each fit 256 (32 rows at D = 64, 16 at D = 128, 8 at
+// D = 160 with 160 threads), so a workgroup covers whole rows and a block whole workgroups.
+constexpr int merge_rows_per_wg(int d) {
+  return d / 8 <= 8 ? 32 : d / 8 <= 16 ? 16 : 8;
+}
+constexpr int merge_threads(int d) { return merge_rows_per_wg(d) * (d / 8); }
+
 // Split key ranges with chunks of C steps: a query block with `len` key steps is cut
 // into ns = ceil(len / C) chunks counted back from its last step (chunk 0 takes the
 // remainder), one work item each.  Causal block qt has qt + 1 steps, so blocks

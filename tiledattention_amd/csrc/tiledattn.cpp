@@ -370,10 +370,9 @@ void fill_params(const ta_fwd_args* a, int64_t n_bh, int64_t n_qblk, ta::FwdPara
   p->d_real = a->d_real ? a->d_real : static_cast<int32_t>(a->D);
 }
 
-// Whether the split path exists for this configuration (the eight-wave kernel, D <= 128:
-// at D = 160 its stages fill the LDS and its merge kernel's rows do not tile 256 threads).
+// Whether the split path exists for this configuration (the eight-wave kernel).
 bool split_capable(const ta_fwd_args* a) {
-  return a->tile_m == kSplitRows && a->tile_n == 64 && a->accum == TA_ACC_FP32 && a->D <= 128;
+  return a->tile_m == kSplitRows && a->tile_n == 64 && a->accum == TA_ACC_FP32 && a->D <= 160;
 }
 
 }  // namespace
@@ -501,7 +500,7 @@ ta_status ta_split_workspace_size(const ta_fwd_args* a, int32_t chunk_steps, int
   ta_status vst = validate_args(a, &n_bh, &n_qblk, false);
   if (vst != TA_OK || n_qblk == 0 || chunk_steps == 0) return vst;
   if (!split_capable(a))
-    return fail(TA_EUNSUPPORTED, "split key ranges need tile (128, 64), fp32 accumulation, D <= 128");
+    return fail(TA_EUNSUPPORTED, "split key ranges need tile (128, 64), fp32 accumulation, D <= 160");
   SplitLayout l;
   if (split_layout(a->S, a->causal != 0, chunk_steps, &l)) *bytes = split_ws_bytes(n_bh, a->D, l);
   return TA_OK;
@@ -517,7 +516,7 @@ ta_status ta_sdpa_fwd_split(const ta_fwd_args* a, int32_t chunk_steps, void* wor
   if (chunk_steps == 0 || !split_layout(a->S, a->causal != 0, chunk_steps, &l))
     return ta_sdpa_fwd(a, stream);
   if (!split_capable(a))
-    return fail(TA_EUNSUPPORTED, "split key ranges need tile (128, 64), fp32 accumulation, D <= 128");
+    return fail(TA_EUNSUPPORTED, "split key ranges need tile (128, 64), fp32 accumulation, D <= 160");
   const int64_t need = split_ws_bytes(n_bh, a->D, l);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(TA_EINVAL, "workspace of %lld bytes needed, %lld given", (long long)need,
@@ -527,10 +526,12 @@ ta_status ta_sdpa_fwd_split(const ta_fwd_args* a, int32_t chunk_steps, void* wor
   if (n_bh * l.items > 0x7fffffffLL || n_bh * l.slots * kSplitRows > 0x7fffffffLL ||
       n_bh * l.merge * kSplitRows > 0x7fffffffLL)
     return fail(TA_EINVAL, "split grid too large");
-  // merge: one thread per (row, 16-byte output chunk), 256 threads a workgroup
-  const int64_t merge_wgs = n_bh * l.merge * (kSplitRows / (256 / (a->D / 8)));
+  // merge: one thread per (row, 16-byte output chunk), merge_rows_per_wg(D) rows a workgroup
+  const int d8 = static_cast<int>(a->D);
+  const unsigned merge_block = static_cast<unsigned>(ta::merge_threads(d8));
+  const int64_t merge_wgs = n_bh * l.merge * (kSplitRows / ta::merge_rows_per_wg(d8));
   ta_status gst = check_grid(n_bh * l.items, 512u, "split kernel");
-  if (gst == TA_OK) gst = check_grid(merge_wgs, 256u, "merge kernel");
+  if (gst == TA_OK) gst = check_grid(merge_wgs, merge_block, "merge kernel");
   if (gst != TA_OK) return gst;
 
   const bool aligned = (a->S % a->tile_m == 0) && (a->S % a->tile_n == 0);
@@ -566,7 +567,7 @@ ta_status ta_sdpa_fwd_split(const ta_fwd_args* a, int32_t chunk_steps, void* wor
   hipError_t e = hipModuleLaunchKernel(sfn, static_cast<unsigned>(n_bh * l.items), 1, 1, 512, 1,
                                        1, 0, hs, params, nullptr);
   if (e != hipSuccess) return fail(TA_EHIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
-  e = hipModuleLaunchKernel(mfn, static_cast<unsigned>(merge_wgs), 1, 1, 256, 1, 1, 0, hs, params,
+  e = hipModuleLaunchKernel(mfn, static_cast<unsigned>(merge_wgs), 1, 1, merge_block, 1, 1, 0, hs, params,
                             nullptr);
   if (e != hipSuccess) return fail(TA_EHIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
   return TA_OK;

@@ -327,15 +327,10 @@ _SPLIT_PLANS: dict[tuple[int, int, int, int], int] = {}
 
 def _eight_wave_kernel(*, tile_m: int, tile_n: int, accum_code: int, kernel_head_dim: int) -> bool:
     """Whether the configuration runs the eight-wave kernel (tile (128, 64), fp32
-    accumulation, kernel head dim 64, 128 or 160): the one with in-place padding of
-    narrower head dims."""
+    accumulation, kernel head dim 64, 128 or 160): the one with split key ranges and
+    in-place padding of narrower head dims."""
     return (tile_m, tile_n) == (128, 64) and accum_code == _lib.TA_ACC_FP32 and kernel_head_dim <= 160
 
-
-def _split_capable(*, tile_m: int, tile_n: int, accum_code: int, kernel_head_dim: int) -> bool:
-    """Whether split key ranges exist: the eight-wave kernel at kernel head dim <= 128."""
-    return kernel_head_dim <= 128 and _eight_wave_kernel(
-        tile_m=tile_m, tile_n=tile_n, accum_code=accum_code, kernel_head_dim=kernel_head_dim)
 
 
 def _resolve_split(lib, args: _lib.FwdArgs, *, capable: bool) -> int:
@@ -361,7 +356,7 @@ def _resolve_split(lib, args: _lib.FwdArgs, *, capable: bool) -> int:
         raise ValueError(f"TILEDATTN_SPLIT must be >= 0, got {chunk}.")
     if chunk and not capable:
         raise ValueError(
-            "TILEDATTN_SPLIT needs tile (128, 64), fp32 accumulation and a head dim of at most 128."
+            "TILEDATTN_SPLIT needs tile (128, 64), fp32 accumulation and a head dim of at most 160."
         )
     return chunk
 
@@ -542,8 +537,8 @@ def _build_plan(torch_mod, lib, q, k, v, causal: bool) -> _LaunchPlan:
     args.sched = _resolve_sched(n_blocks=bh * n_qblk, causal=causal, tile_m=tile_m, tile_n=tile_n,
                                 accum_code=accum_code, head_dim=kernel_head_dim)
 
-    capable = _split_capable(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code,
-                             kernel_head_dim=kernel_head_dim)
+    capable = _eight_wave_kernel(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code,
+                                 kernel_head_dim=kernel_head_dim)
     plan.chunk = _resolve_split(lib, args, capable=capable)
     plan.ws_bytes = 0
     if plan.chunk:
