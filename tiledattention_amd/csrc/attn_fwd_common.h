@@ -55,6 +55,13 @@ struct DType<0> {  // float16
     const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, u), one, acc, false);
   }
+  // lo(u) + hi(u): the same dot2 with an inline-constant zero accumulator (VOP3P form; the
+  // compiler would materialise the zero with a v_mov for the accumulating form).
+  __device__ static inline float sum2_head(uint32_t u) {
+    float x;
+    asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(x) : "v"(u), "s"(0x3c003c00u));
+    return x;
+  }
 };
 
 template <>
@@ -75,6 +82,12 @@ struct DType<1> {  // bfloat16
   __device__ static inline float sum2(uint32_t u, float acc) {
     const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, u), one, acc, false);
+  }
+  // lo(u) + hi(u) (VOP3P dot2 with an inline-constant zero accumulator, as for fp16).
+  __device__ static inline float sum2_head(uint32_t u) {
+    float x;
+    asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(x) : "v"(u), "s"(0x3f803f80u));
+    return x;
   }
 };
 

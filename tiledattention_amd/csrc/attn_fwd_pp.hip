@@ -306,9 +306,10 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
       }
     }
     // P = 2^(s c - m c) packed into pk, and the sum of the rounded P: four independent
-    // partial sums so the dot2 chain is short.
+    // partial sums so the dot2 chain is short, each started without a zeroed accumulator
+    // (four VALU ops fewer in this cluster; 0.3-2 % per call measured).
     auto make_p = [&](float mc) {
-      float l4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      float l4[4];
 #pragma unroll
       for (int bk = 0; bk < KB; ++bk) {
 #pragma unroll
@@ -317,7 +318,8 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
           const float p1 = fast_exp2(__builtin_fmaf(s[bk][r + 1], c, -mc));
           const uint32_t w = DTy::pack(p0, p1);
           pk[bk][r >> 1] = w;
-          l4[(r >> 1) & 3] = DTy::sum2(w, l4[(r >> 1) & 3]);
+          const int j = (r >> 1) & 3;
+          l4[j] = bk == 0 && r < 8 ? DTy::sum2_head(w) : DTy::sum2(w, l4[j]);
         }
       }
       return (l4[0] + l4[1]) + (l4[2] + l4[3]);
