@@ -73,8 +73,8 @@ typedef struct ta_fwd_args {
   int32_t d_real;  /* 0, or the head-dim columns q/k/v/o actually have (a multiple of 8 below
                       D): the kernel for D reads the missing columns as zero and does not
                       write them, so a narrower head dim needs no padded copies (the
-                      reference pads on the host, flash_fwd.py:868-872).  Tile (128, 64)
-                      with fp32 accumulation and D <= 160 only. */
+                      reference pads on the host, flash_fwd.py:868-872).  Tiles (128, 64)
+                      and (128, 128) with fp32 accumulation and D <= 160 only. */
 } ta_fwd_args;
 
 /* Version of this ABI (TA_ABI_VERSION). */
@@ -101,8 +101,8 @@ ta_status ta_sdpa_fwd(const ta_fwd_args* args, void* stream);
  * lengths differ by S / 128 key steps, that grid leaves compute units idle while the
  * longest rows finish.  The split path cuts every 128-row query block's keys into chunks of
  * `chunk_steps` steps of 128 keys, runs one workgroup per chunk, and merges the chunks of a
- * block (log-sum-exp weights) in a second kernel on the same stream.  It exists for tile
- * (128, 64) with fp32 accumulation and D <= 160; the result matches ta_sdpa_fwd within
+ * block (log-sum-exp weights) in a second kernel on the same stream.  It exists for tiles
+ * (128, 64) and (128, 128) with fp32 accumulation and D <= 160; the result matches ta_sdpa_fwd within
  * fp32 rounding of the merge. */
 
 /* Chunk length (key steps) this library would use for `args` on its device: 0 when the
@@ -113,7 +113,7 @@ ta_status ta_sdpa_fwd(const ta_fwd_args* args, void* stream);
 ta_status ta_split_plan(const ta_fwd_args* args, int32_t* chunk_steps);
 
 /* The model behind ta_split_plan for a device with `compute_units` CUs, without touching
- * a device: chunk length for a (128, 64)-tile fp32-accumulation forward of sequence length
+ * a device: chunk length for a 128-row-tile fp32-accumulation forward of sequence length
  * S over n_bh (b, h) slices, 0 for no split or invalid sizes. */
 int32_t ta_split_plan_model(int64_t S, int64_t n_bh, int32_t causal, int32_t compute_units);
 

@@ -87,7 +87,8 @@ def test_workspace_size_edge_cases(lib):
     # a chunk as long as the longest row splits nothing
     assert lib.ta_split_workspace_size(ctypes.byref(_args(S=4096)), 32, ctypes.byref(out)) == _lib.TA_OK
     assert out.value == 0
-    for kw in (dict(tile_m=64), dict(tile_n=128), dict(accum=_lib.TA_ACC_INPUT), dict(D=256)):
+    for kw in (dict(tile_m=64), dict(tile_m=64, tile_n=128), dict(accum=_lib.TA_ACC_INPUT),
+               dict(tile_n=128, accum=_lib.TA_ACC_INPUT), dict(D=256)):
         st = lib.ta_split_workspace_size(ctypes.byref(_args(S=4096, **kw)), 4, ctypes.byref(out))
         assert st == _lib.TA_EUNSUPPORTED, kw
         assert "split key ranges" in _lib.last_error(lib)
@@ -178,7 +179,7 @@ def test_split_capability_rule():
     assert rule(**{**ok, "kernel_head_dim": 160})
     assert not rule(**{**ok, "kernel_head_dim": 256})
     assert not rule(**{**ok, "tile_m": 64})
-    assert not rule(**{**ok, "tile_n": 128})
+    assert rule(**{**ok, "tile_n": 128})  # the eight-wave step is 128 keys
     assert not rule(**{**ok, "accum_code": _lib.TA_ACC_INPUT})
     with pytest.raises(ValueError, match="D <= 160"):
         _lib.kernel_symbol(dtype=_lib.TA_BF16, head_dim=256, tile_m=128, tile_n=64, causal=True,

@@ -38,11 +38,12 @@ def kernel_symbol(*, dtype: int, head_dim: int, tile_m: int, tile_n: int, causal
     names the split-key-range kernel (its merge kernel is ta_fwd_merge_<dt>_d<D>_c<c>)."""
     dt = "bf16" if dtype == TA_BF16 else "f16"
     c, t = int(bool(causal)), int(bool(tail))
-    if (tile_m, tile_n) == (128, 64) and accum == TA_ACC_FP32 and head_dim <= 160:
+    if tile_m == 128 and tile_n in (64, 128) and accum == TA_ACC_FP32 and head_dim <= 160:
         kind = "pp_split" if split else "pp"
         return "attn_fwd_pp.hsaco", f"ta_fwd_{kind}_{dt}_d{head_dim}_c{c}_t{t}"
     if split:
-        raise ValueError("split key ranges exist for tile (128, 64), fp32 accumulation, D <= 160")
+        raise ValueError("split key ranges exist for tiles (128, 64) and (128, 128), fp32 "
+                         "accumulation, D <= 160")
     return (f"attn_fwd_m{tile_m}_n{tile_n}.hsaco",
             f"ta_fwd_{dt}_d{head_dim}_m{tile_m}_n{tile_n}_c{c}_t{t}_a{int(accum != TA_ACC_FP32)}")
 

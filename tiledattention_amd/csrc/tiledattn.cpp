@@ -5,7 +5,7 @@
 // kernel cache (src/tiledattention/kernels/compile_cache.py:10-37):
 //   * kernels are precompiled into gfx950 code objects: attn_fwd_m<TM>_n<TN>.hsaco per tile
 //     shape, and attn_fwd_pp.hsaco with the eight-wave kernels that serve the (128, 64)
-//     shape with fp32 accumulation; one module per (device, file) is loaded on first use
+//     and (128, 128) shapes with fp32 accumulation; one module per (device, file) is loaded on first use
 //     and kept, and resolved hipFunction_t handles are cached per (device, kernel name);
 //   * the cache is guarded by a mutex (the reference's dict is unguarded);
 //   * launches go to the caller's stream under a device guard, like the reference's torch op
@@ -89,12 +89,20 @@ struct KernelId {
   unsigned block;
 };
 
+// The eight-wave kernel (attn_fwd_pp.hip) serves 128-row tiles with fp32 accumulation at
+// D = 64, 128 and 160: its workgroup step is 128 rows x 128 keys, 64 keys per wave group,
+// so it stands for both TILE_N = 64 and TILE_N = 128 (the latter only up to D = 128,
+// check_shape).
+bool eight_wave(int64_t tm, int64_t tn, int64_t accum, int64_t d) {
+  return tm == 128 && (tn == 64 || tn == 128) && accum == TA_ACC_FP32 && d <= 160;
+}
+
 KernelId kernel_id(int dtype, int d, int tm, int tn, int causal, int tail, int accum) {
   const char* dt = dtype == TA_BF16 ? "bf16" : "f16";
   char buf[96];
-  if (tm == 128 && tn == 64 && accum == TA_ACC_FP32 && d <= 160) {
+  if (eight_wave(tm, tn, accum, d)) {
     // Eight waves: two per SIMD sharing the rows of a 32-row block, splitting every
-    // 128-key step between them (attn_fwd_pp.hip; D = 64, 128 and 160).
+    // 128-key step between them.
     snprintf(buf, sizeof(buf), "ta_fwd_pp_%s_d%d_c%d_t%d", dt, d, causal ? 1 : 0, tail ? 1 : 0);
     return {"attn_fwd_pp.hsaco", buf, 512u};
   }
@@ -311,8 +319,9 @@ ta_status validate_args(const ta_fwd_args* a, int64_t* n_bh_out, int64_t* n_qblk
   if (a->d_real != 0) {
     if (a->d_real < 8 || a->d_real > a->D || (a->d_real & 7) != 0)
       return fail(TA_EINVAL, "d_real %d (0, or a multiple of 8 in [8, D])", a->d_real);
-    if (!(a->tile_m == kSplitRows && a->tile_n == 64 && a->accum == TA_ACC_FP32 && a->D <= 160))
-      return fail(TA_EUNSUPPORTED, "d_real needs tile (128, 64), fp32 accumulation and D <= 160");
+    if (!eight_wave(a->tile_m, a->tile_n, a->accum, a->D))
+      return fail(TA_EUNSUPPORTED,
+                  "d_real needs tile (128, 64) or (128, 128), fp32 accumulation and D <= 160");
   }
   if (a->B < 0 || a->H < 0 || a->S < 0) return fail(TA_EINVAL, "negative shape");
   ta_status shape_st = check_shape(a->D, a->tile_m, a->tile_n);
@@ -372,7 +381,7 @@ void fill_params(const ta_fwd_args* a, int64_t n_bh, int64_t n_qblk, ta::FwdPara
 
 // Whether the split path exists for this configuration (the eight-wave kernel).
 bool split_capable(const ta_fwd_args* a) {
-  return a->tile_m == kSplitRows && a->tile_n == 64 && a->accum == TA_ACC_FP32 && a->D <= 160;
+  return eight_wave(a->tile_m, a->tile_n, a->accum, a->D);
 }
 
 }  // namespace
@@ -500,7 +509,7 @@ ta_status ta_split_workspace_size(const ta_fwd_args* a, int32_t chunk_steps, int
   ta_status vst = validate_args(a, &n_bh, &n_qblk, false);
   if (vst != TA_OK || n_qblk == 0 || chunk_steps == 0) return vst;
   if (!split_capable(a))
-    return fail(TA_EUNSUPPORTED, "split key ranges need tile (128, 64), fp32 accumulation, D <= 160");
+    return fail(TA_EUNSUPPORTED, "split key ranges need tile (128, 64) or (128, 128), fp32 accumulation, D <= 160");
   SplitLayout l;
   if (split_layout(a->S, a->causal != 0, chunk_steps, &l)) *bytes = split_ws_bytes(n_bh, a->D, l);
   return TA_OK;
@@ -516,7 +525,7 @@ ta_status ta_sdpa_fwd_split(const ta_fwd_args* a, int32_t chunk_steps, void* wor
   if (chunk_steps == 0 || !split_layout(a->S, a->causal != 0, chunk_steps, &l))
     return ta_sdpa_fwd(a, stream);
   if (!split_capable(a))
-    return fail(TA_EUNSUPPORTED, "split key ranges need tile (128, 64), fp32 accumulation, D <= 160");
+    return fail(TA_EUNSUPPORTED, "split key ranges need tile (128, 64) or (128, 128), fp32 accumulation, D <= 160");
   const int64_t need = split_ws_bytes(n_bh, a->D, l);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(TA_EINVAL, "workspace of %lld bytes needed, %lld given", (long long)need,

@@ -35,9 +35,9 @@ Environment knobs are re-read on every call, as in the reference:
 ``TILEDATTN_SPLIT`` (this build only)
     Split key ranges (``ta_sdpa_fwd_split``): ``auto`` (default) asks the library's
     dispatch model (``ta_split_plan``), ``0``/``off`` never splits, a positive integer
-    forces chunks of that many 128-key steps.  Splitting exists for tile (128, 64) with
-    fp32 accumulation and kernel head dims up to 128; forcing it elsewhere raises
-    ``ValueError``.
+    forces chunks of that many 128-key steps.  Splitting exists for tiles (128, 64) and
+    (128, 128) with fp32 accumulation and kernel head dims up to 160; forcing it elsewhere
+    raises ``ValueError``.
 """
 
 from __future__ import annotations
@@ -274,7 +274,8 @@ def _workgroups_per_cu(*, tile_m: int, tile_n: int, accum_code: int, head_dim: i
     at D = 128 or causal, and the other tile shapes, fill a CU's LDS or registers)."""
     if (tile_m, tile_n) == (128, 64) and accum_code == _lib.TA_ACC_INPUT:
         return 2
-    if (tile_m, tile_n) == (128, 64) and head_dim <= 64 and not causal:
+    if _eight_wave_kernel(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code,
+                          kernel_head_dim=head_dim) and head_dim <= 64 and not causal:
         return 2
     return 1
 
@@ -326,10 +327,12 @@ _SPLIT_PLANS: dict[tuple[int, int, int, int], int] = {}
 
 
 def _eight_wave_kernel(*, tile_m: int, tile_n: int, accum_code: int, kernel_head_dim: int) -> bool:
-    """Whether the configuration runs the eight-wave kernel (tile (128, 64), fp32
-    accumulation, kernel head dim 64, 128 or 160): the one with split key ranges and
-    in-place padding of narrower head dims."""
-    return (tile_m, tile_n) == (128, 64) and accum_code == _lib.TA_ACC_FP32 and kernel_head_dim <= 160
+    """Whether the configuration runs the eight-wave kernel (tile (128, 64) or (128, 128),
+    fp32 accumulation, kernel head dim 64, 128 or 160): the one with split key ranges and
+    in-place padding of narrower head dims.  Its workgroup step is 128 rows x 128 keys, 64
+    keys per wave group, so it serves both 128-row tiles."""
+    return (tile_m == 128 and tile_n in (64, 128) and accum_code == _lib.TA_ACC_FP32
+            and kernel_head_dim <= 160)
 
 
 
@@ -356,7 +359,8 @@ def _resolve_split(lib, args: _lib.FwdArgs, *, capable: bool) -> int:
         raise ValueError(f"TILEDATTN_SPLIT must be >= 0, got {chunk}.")
     if chunk and not capable:
         raise ValueError(
-            "TILEDATTN_SPLIT needs tile (128, 64), fp32 accumulation and a head dim of at most 160."
+            "TILEDATTN_SPLIT needs tile (128, 64) or (128, 128), fp32 accumulation and a head dim "
+            "of at most 160."
         )
     return chunk
 
