@@ -35,7 +35,7 @@ if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
 PEAK_TFLOPS = 2516.6  # dense fp16/bf16 MFMA, MI355X: 256 CU * 4096 FLOP/clk * 2.4 GHz
-REFERENCE_GB10_C3_S8192 = 60.87  # BASELINE.md 1.1 (benchmark_results.csv:548), TFLOP/s
+REFERENCE_GB10_C3_S8192 = 60.87  # benchmark-gb10/results/benchmark_results.csv:548, TFLOP/s
 
 
 def _args():
