@@ -513,12 +513,13 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   float la, lb;
   swap32(l_part * a0 + l1 * a1, la, lb);
   const float l_tot = la + lb;
-  // Whole-row kernels at D = 128 stage O through this wave's merge region, so that each
-  // store instruction writes whole rows (16 bytes a lane) instead of 8 bytes in each of 32
-  // rows; every lane takes part in that exchange, rows past S included.  It shortens the
-  // time to the last store (B1 H8 causal: S = 1024 -7 %, S = 2048 -4 %, S = 8192 -0.7 %); at
-  // D = 64 it measured 3-10 % slower and is not used.
-  constexpr bool kStageOut = !SPLIT && D == 128;
+  // Whole-row kernels at D = 128, and causal ones at D = 64, stage O through this wave's
+  // merge region, so that each store instruction writes whole rows (16 bytes a lane)
+  // instead of 8 bytes in each of 32 rows; every lane takes part in that exchange, rows
+  // past S included.  It shortens the time to the last store (B1 H8 causal, D = 128:
+  // S = 1024 -7 %, S = 8192 -0.7 %; D = 64: S = 2048 -6.6 %, S = 8192 -1 %); the non-causal
+  // D = 64 kernels, two workgroups per CU, measured 3-10 % slower with it.
+  constexpr bool kStageOut = !SPLIT && (D == 128 || (D == 64 && CAUSAL));
   if (!kStageOut && TAIL && my_q >= S) return;
   const float inv = 1.0f / l_tot;
   const float w0s = a0 * inv, w1s = a1 * inv;
