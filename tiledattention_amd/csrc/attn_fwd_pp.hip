@@ -513,13 +513,14 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   float la, lb;
   swap32(l_part * a0 + l1 * a1, la, lb);
   const float l_tot = la + lb;
-  // Whole-row kernels at D = 128, and causal ones at D = 64, stage O through this wave's
-  // merge region, so that each store instruction writes whole rows (16 bytes a lane)
+  // Whole-row kernels at D = 128 and 160, and causal ones at D = 64, stage O through this
+  // wave's merge region, so that each store instruction writes whole rows (16 bytes a lane)
   // instead of 8 bytes in each of 32 rows; every lane takes part in that exchange, rows
   // past S included.  It shortens the time to the last store (B1 H8 causal, D = 128:
-  // S = 1024 -7 %, S = 8192 -0.7 %; D = 64: S = 2048 -6.6 %, S = 8192 -1 %); the non-causal
-  // D = 64 kernels, two workgroups per CU, measured 3-10 % slower with it.
-  constexpr bool kStageOut = !SPLIT && (D == 128 || (D == 64 && CAUSAL));
+  // S = 1024 -7 %, S = 8192 -0.7 %; D = 64: S = 2048 -6.6 %, S = 8192 -1 %; D = 160: -0.7 to
+  // -2.8 %); the non-causal D = 64 kernels, two workgroups per CU, measured 3-10 % slower
+  // with it.
+  constexpr bool kStageOut = !SPLIT && (D == 128 || D == 160 || (D == 64 && CAUSAL));
   if (!kStageOut && TAIL && my_q >= S) return;
   const float inv = 1.0f / l_tot;
   const float w0s = a0 * inv, w1s = a1 * inv;
@@ -543,7 +544,41 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
     if (hl == 0) p.part_lse[(int64_t)slot * TM + (my_q - q0)] = m * c + fast_log2(l_tot);
     return;
   }
-  if constexpr (kStageOut) {
+  if constexpr (kStageOut && D == 160) {
+    // 20 chunks a row: rows padded to 336 bytes instead of swizzled, so the 8-byte writes of
+    // one instruction (one chunk, 32 rows) are free of bank conflicts; the 16-byte reads run
+    // over the tile's 640 chunks in row-major order (a 2-way conflict where a read pass
+    // crosses a row pad).
+    char* ob = (char*)xo;
+    constexpr int RBL = 2 * D + 16;  // LDS bytes per staged row
+    constexpr int CPO = D / 8;       // 16-byte chunks per output row
+    static_assert(32 * CPO % 64 == 0 && 32 * RBL <= STAGE / 2, "staged tile in the region");
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float o4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * g + e;
+          o4[e] = o_acc[db][r] * w0s + x1[db][r] * w1s;
+        }
+        *(u32x2*)(ob + l32 * RBL + 16 * (4 * db + g) + 8 * hl) =
+            u32x2{DTy::pack(o4[0], o4[1]), DTy::pack(o4[2], o4[3])};
+      }
+    }
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < 32 * CPO / 64; ++i) {
+      const int idx = 64 * i + lane;
+      const int row = idx / CPO;
+      const int ch = idx - row * CPO;
+      const u32x4 v = *(const u32x4*)(ob + row * RBL + 16 * ch);
+      const int q = wq0 + row;
+      if ((!TAIL || q < S) && 8 * ch < d_real) *(u32x4*)(op + (int64_t)q * p.o_ss + 8 * ch) = v;
+    }
+    return;
+  } else if constexpr (kStageOut) {
     // 32 rows x 2D bytes in the wave's own merge region (its group-1 values are in
     // registers by now), 16-byte chunks swizzled per row as the K stages are (chunk ^
     // swz_k(row)): the 8-byte writes of one instruction (one chunk, 32 rows) and the
