@@ -546,9 +546,9 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   }
   if constexpr (kStageOut && D == 160) {
     // 20 chunks a row: rows padded to 336 bytes instead of swizzled, so the 8-byte writes of
-    // one instruction (one chunk, 32 rows) are free of bank conflicts; the 16-byte reads run
-    // over the tile's 640 chunks in row-major order (a 2-way conflict where a read pass
-    // crosses a row pad).
+    // one instruction (one chunk, 32 rows) conflict only 2-way (rows 16 apart share banks);
+    // the 16-byte reads run over the tile's 640 chunks in row-major order (a 2-way conflict
+    // where a read pass crosses a row pad).
     char* ob = (char*)xo;
     constexpr int RBL = 2 * D + 16;  // LDS bytes per staged row
     constexpr int CPO = D / 8;       // 16-byte chunks per output row
@@ -581,8 +581,9 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   } else if constexpr (kStageOut) {
     // 32 rows x 2D bytes in the wave's own merge region (its group-1 values are in
     // registers by now), 16-byte chunks swizzled per row as the K stages are (chunk ^
-    // swz_k(row)): the 8-byte writes of one instruction (one chunk, 32 rows) and the
-    // 16-byte row-major reads are both conflict-free.
+    // swz_k(row)): the 16-byte row-major reads are conflict-free and the 8-byte writes of
+    // one instruction (one chunk, 32 rows) conflict 2-way (rows 16 apart share banks;
+    // 64 cycles a wave).
     char* ob = (char*)xo;
     constexpr int RBO = 2 * D;
     constexpr int CPO = D / 8;      // 16-byte chunks per output row
