@@ -57,7 +57,10 @@ typedef struct ta_fwd_args {
   void* o;
   int64_t B, H, S, D; /* D: 64, 128, 160 or 256 (callers zero-pad other head dims, or
                          set d_real); 160 and 256 need tile_n = 64 */
-  int64_t q_stride[4]; /* element strides for (B,H,S,D); stride[3] must be 1 */
+  int64_t q_stride[4]; /* element strides for (B,H,S,D); stride[3] must be 1, the others
+                          multiples of 8; S * stride[2] * 2 bytes below 2^31 for k and v
+                          (and for q on tiles (128, 64) / (128, 128) with fp32
+                          accumulation), which are read with 32-bit buffer offsets */
   int64_t k_stride[4];
   int64_t v_stride[4];
   int64_t o_stride[4];

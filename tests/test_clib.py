@@ -81,6 +81,9 @@ def _call(lib, a):
     (dict(o_stride=(2 * 64 * 64, 64 * 64, 68, 1)), _lib.TA_EINVAL, "multiple of 8"),
     (dict(S=1 << 24, k_stride=(0, 0, 128, 1), D=128), _lib.TA_EINVAL, "2^31"),
     (dict(S=2, k_stride=(0, 0, 1 << 23, 1)), _lib.TA_EINVAL, "128 * row stride"),
+    # Q's range limit applies where Q is staged with buffer loads (the eight-wave kernel)
+    (dict(S=1 << 20, q_stride=(0, 0, 1024, 1), D=128, tile_m=128), _lib.TA_EINVAL, "q: S * row stride"),
+    (dict(S=2, q_stride=(0, 0, 1 << 23, 1), D=128, tile_m=128), _lib.TA_EINVAL, "q: S * row stride"),
     (dict(d_real=4), _lib.TA_EINVAL, "d_real 4"),
     (dict(d_real=72), _lib.TA_EINVAL, "d_real 72"),        # above D = 64
     (dict(d_real=-8), _lib.TA_EINVAL, "d_real"),

@@ -356,6 +356,10 @@ ta_status validate_args(const ta_fwd_args* a, int64_t* n_bh_out, int64_t* n_qblk
     return fail(TA_EINVAL, "k/v: S * row stride must stay below 2^31 bytes per (b, h) slice");
   if (a->k_stride[2] * 2 * 128 >= 0x80000000LL || a->v_stride[2] * 2 * 128 >= 0x80000000LL)
     return fail(TA_EINVAL, "k/v: 128 * row stride must stay below 2^31 bytes");
+  // The eight-wave kernel stages Q the same way (one buffer resource per query block).
+  if (eight_wave(a->tile_m, a->tile_n, a->accum, a->D) &&
+      (a->S * a->q_stride[2] * 2 > 0x7fffffffLL || a->q_stride[2] * 2 * 128 >= 0x80000000LL))
+    return fail(TA_EINVAL, "q: S * row stride must stay below 2^31 bytes per (b, h) slice");
   *n_qblk_out = n_qblk;
   return TA_OK;
 }
