@@ -17,9 +17,9 @@
 //   the transposed V reads use the same permutation, so no lane shuffle is needed.  Each
 //   lane again holds one query, so the per-query rescale by alpha and the final 1/l are
 //   lane-local.
-// * K/V tiles go HBM -> VGPR -> LDS through two LDS stages: tile t+1 is fetched (buffer
-//   loads, range-checked so rows past S read as zero) while tile t is consumed; one
-//   barrier per tile.  LDS rows are padded (K: 2D+16 bytes, V: 2D+64 bytes) so the b128 K
+// * K/V tiles go HBM -> VGPR -> LDS through two LDS stages (one for the 64 x 128 tile):
+//   tile t+1 is fetched (buffer loads, range-checked so rows past S read as zero) while
+//   tile t is consumed; one barrier per tile (two with one stage).  LDS rows are padded (K: 2D+16 bytes, V: 2D+64 bytes) so the b128 K
 //   reads and the b64 transposed V reads are free of bank conflicts on the 64-bank LDS.
 // * exp is v_exp_f32 (2^x) with scale*log2(e) folded into one FMA per score.
 // * Causal: tiles above the diagonal are never loaded by a wave that does not need them,
@@ -43,6 +43,18 @@
 #endif
 #ifndef TA_TILE_N
 #define TA_TILE_N 64
+#endif
+
+// LDS stages of K/V tiles: two (the next tile is stored while the current one is read,
+// one barrier per tile), except for the 64 x 128 tile, whose two stages (151 KiB at D = 128)
+// would leave one two-wave workgroup per CU; with one stage two workgroups fit, at the cost
+// of a second barrier per tile (C4 D = 128 bf16: 308 -> 573 TFLOP/s).
+#ifndef TA_STAGES
+#if TA_TILE_M == 64 && TA_TILE_N == 128
+#define TA_STAGES 1
+#else
+#define TA_STAGES 2
+#endif
 #endif
 
 namespace ta {
@@ -80,7 +92,8 @@ __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
   constexpr int STAGE = K_BYTES + TN * L::VS;
   using DTy = DType<DT>;
 
-  __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+  constexpr int NST = TA_STAGES;
+  __shared__ __attribute__((aligned(16))) char smem[NST * STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -366,7 +379,7 @@ __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
     if (has_next) load_tile(kt + 1);
 
     const int k0 = kt * TN;
-    const char* st = smem + (kt & 1) * STAGE;
+    const char* st = smem + (NST == 2 ? (kt & 1) * STAGE : 0);
     // Fully visible: every key of the tile is <= the wave's first query (causal) and < S.
     const bool full = (!CAUSAL || k0 + TN - 1 <= wq0) && (!TAIL || k0 + TN <= S);
     if (full) {
@@ -375,8 +388,18 @@ __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
       tile(st, k0, std::false_type{});
     }
 
-    if (has_next) store_tile((kt + 1) & 1);
-    __syncthreads();
+    if constexpr (NST == 2) {
+      if (has_next) store_tile((kt + 1) & 1);
+      __syncthreads();
+    } else {
+      // One stage: the next tile (in registers since the top of this iteration) replaces
+      // the current one once every wave is done reading it.
+      __syncthreads();
+      if (has_next) {
+        store_tile(0);
+        __syncthreads();
+      }
+    }
   }
 
   // ---- epilogue: O = acc / l, written back as [q][d] ------------------------------------
