@@ -17,7 +17,7 @@
 //   the transposed V reads use the same permutation, so no lane shuffle is needed.  Each
 //   lane again holds one query, so the per-query rescale by alpha and the final 1/l are
 //   lane-local.
-// * K/V tiles go HBM -> VGPR -> LDS through two LDS stages (one for the 64 x 128 tile):
+// * K/V tiles go HBM -> VGPR -> LDS through two LDS stages (one for the 64-row tiles):
 //   tile t+1 is fetched (buffer loads, range-checked so rows past S read as zero) while
 //   tile t is consumed; one barrier per tile (two with one stage).  LDS rows are padded (K: 2D+16 bytes, V: 2D+64 bytes) so the b128 K
 //   reads and the b64 transposed V reads are free of bank conflicts on the 64-bank LDS.
@@ -46,11 +46,13 @@
 #endif
 
 // LDS stages of K/V tiles: two (the next tile is stored while the current one is read,
-// one barrier per tile), except for the 64 x 128 tile, whose two stages (151 KiB at D = 128)
-// would leave one two-wave workgroup per CU; with one stage two workgroups fit, at the cost
-// of a second barrier per tile (C4 D = 128 bf16: 308 -> 573 TFLOP/s).
+// one barrier per tile), except for the 64-row tiles, whose two-wave workgroups are too
+// small to fill a CU at two stages (64 x 128: 151 KiB at D = 128, one workgroup per CU;
+// 64 x 64: 76 KiB, two): with one stage, at the cost of a second barrier per tile, two
+// (64 x 128) or four (64 x 64, with two waves per SIMD below) share a CU.  C4 D = 128 bf16:
+// 64 x 128 308 -> 573 TFLOP/s, 64 x 64 584 -> 836; 64 x 64 at D = 256 105 -> 211.
 #ifndef TA_STAGES
-#if TA_TILE_M == 64 && TA_TILE_N == 128
+#if TA_TILE_M == 64
 #define TA_STAGES 1
 #else
 #define TA_STAGES 2
@@ -430,11 +432,11 @@ __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
 
 }  // namespace ta
 
-// Waves per SIMD the register allocation is sized for: two when two workgroups fit a CU
-// by LDS (TM = 128, TN = 64: 8 waves per CU), so one wave's MFMAs overlap the other's
-// softmax; one otherwise, and always one for head dims above 128 (whose O, Q and staging
-// registers need the whole register file, and whose tiles fill most of the LDS).
-#if TA_TILE_M == 128 && TA_TILE_N == 64
+// Waves per SIMD the register allocation is sized for: two when enough workgroups fit a
+// CU by LDS for 8 waves (TM = 128, TN = 64: two workgroups; 64 x 64 with one stage: four),
+// so one wave's MFMAs overlap another's softmax; one otherwise, and always one for head
+// dims above 128 (whose O, Q and staging registers need the whole register file).
+#if (TA_TILE_M == 128 && TA_TILE_N == 64) || (TA_TILE_M == 64 && TA_TILE_N == 64)
 #define TA_WAVES_PER_SIMD 2
 #else
 #define TA_WAVES_PER_SIMD 1

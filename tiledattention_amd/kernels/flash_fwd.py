@@ -269,7 +269,8 @@ _CU_COUNT = 256  # MI355X
 def _workgroups_per_cu(*, tile_m: int, tile_n: int, accum_code: int, head_dim: int = 128,
                        causal: bool = True) -> int:
     """Workgroups of one launch resident on a CU at once: two for the four-wave 128x64
-    kernel (input-dtype accumulation), for the four-wave 64x128 kernel (one LDS stage) and
+    kernel (input-dtype accumulation), for the four-wave 64x128 kernel (one LDS stage; four
+    for 64x64 up to D = 128, two above) and
     for the non-causal eight-wave kernel at kernel head dim 64 (built for 128 VGPRs, 64 KiB
     of LDS), one otherwise (the eight-wave kernel at D = 128 or causal, and the other tile
     shapes, fill a CU's LDS or registers)."""
@@ -277,6 +278,8 @@ def _workgroups_per_cu(*, tile_m: int, tile_n: int, accum_code: int, head_dim: i
         return 2
     if (tile_m, tile_n) == (64, 128) and head_dim <= 128:
         return 2  # one LDS stage (76 KiB at D = 128), one wave per SIMD
+    if (tile_m, tile_n) == (64, 64):
+        return 4 if head_dim <= 128 else 2  # one LDS stage; two waves per SIMD up to D = 128
     if _eight_wave_kernel(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code,
                           kernel_head_dim=head_dim) and head_dim <= 64 and not causal:
         return 2
