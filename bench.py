@@ -14,9 +14,16 @@ The JSON line also carries:
   rocprofv3 counters (profiles/), or null when not measured in this run;
 * ``cpu_baseline``: the reference's eager attention restated on the host CPU
   (oracle/eager.py, run_study.py:304-335) on a bounded sample of the same workload;
-* ``sweep``: the C3 sequence sweep S in {512..8192}, kernel TFLOP/s and share of peak.
+* ``sweep``: the C3 sequence sweep S in {512..8192} (bf16), as before;
+* ``blocks``: every other BASELINE.json configuration, each timed the same way (TFLOP/s,
+  share of peak, algorithmic HBM GB/s, mean and p95 per call): C2, the C3 sweep in fp16, the
+  C4 tile x accumulation sweep (fp16/bf16, D 64/128), C5 and its outlier variant C5b.
 
-Usage: ``python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]``.
+Inputs are generated on the CPU from a seeded ``torch.Generator`` (q, k, v drawn in that
+order, as run_study.py:526-529 does) and copied to the GPU before any timing.
+
+Usage: ``python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+[--no-sweep] [--no-blocks]``.
 """
 
 from __future__ import annotations
@@ -36,6 +43,7 @@ if str(ROOT) not in sys.path:
 
 PEAK_TFLOPS = 2516.6  # dense fp16/bf16 MFMA, MI355X: 256 CU * 4096 FLOP/clk * 2.4 GHz
 REFERENCE_GB10_C3_S8192 = 60.87  # benchmark-gb10/results/benchmark_results.csv:548, TFLOP/s
+C4_TILES = ((64, 64), (64, 128), (128, 64), (128, 128))
 
 
 def _args():
@@ -46,6 +54,8 @@ def _args():
     ap.add_argument("--seq", type=int, default=8192, help="sequence length of the headline workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-blocks", action="store_true", help="skip the other BASELINE configurations")
+    ap.add_argument("--only-block", default="", help="run only blocks whose name starts with this")
     ap.add_argument("--traffic-json", default=str(ROOT / "profiles" / "traffic.json"),
                     help="HBM bytes per launch measured by rocprofv3 (optional)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
@@ -58,6 +68,49 @@ def _args():
 def _log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
+
+# ---------------------------------------------------------------- workload definitions
+
+def make_inputs(shape, dtype: str, seed: int, *, scale_inputs: float = 1.0, outlier_frac: float = 0.0,
+                outlier_gain: float = 20.0, outlier_seed: int | None = None):
+    """Seeded q, k, v (CPU tensors of ``dtype``): ``randn`` in fp32 from
+    ``torch.Generator('cpu').manual_seed(seed)`` in the order q, k, v (run_study.py:526-529),
+    times ``scale_inputs``; ``outlier_frac`` > 0 multiplies that fraction of k's entries,
+    chosen uniformly with ``outlier_seed``, by ``outlier_gain`` (BASELINE config C5b)."""
+    import torch
+
+    tdt = {"float16": torch.float16, "bfloat16": torch.bfloat16}[dtype]
+    g = torch.Generator(device="cpu").manual_seed(int(seed))
+    q = torch.randn(shape, generator=g, dtype=torch.float32) * scale_inputs
+    k = torch.randn(shape, generator=g, dtype=torch.float32) * scale_inputs
+    v = torch.randn(shape, generator=g, dtype=torch.float32) * scale_inputs
+    if outlier_frac > 0.0:
+        g2 = torch.Generator(device="cpu").manual_seed(int(outlier_seed if outlier_seed is not None else seed + 1))
+        idx = torch.randperm(k.numel(), generator=g2)[: int(round(k.numel() * outlier_frac))]
+        flat = k.reshape(-1)
+        flat[idx] = flat[idx] * outlier_gain
+    return q.to(tdt), k.to(tdt), v.to(tdt)
+
+
+def flops_of(b: int, h: int, s: int, d: int, causal: bool) -> float:
+    """Work of one forward as BASELINE.json counts it: 4*B*H*S^2*D, halved when causal."""
+    f = 4.0 * b * h * s * s * d
+    return f / 2.0 if causal else f
+
+
+def alg_bytes(b: int, h: int, s: int, d: int) -> float:
+    """Algorithmic HBM bytes: q, k, v read and o written once, 2 bytes an element
+    (run_study.py:146)."""
+    return 4.0 * b * h * s * d * 2
+
+
+def p95(values) -> float:
+    """95th percentile as run_study.py:30-45 takes it (quantiles n=20, index 18)."""
+    vals = list(values)
+    return vals[0] if len(vals) == 1 else statistics.quantiles(vals, n=20)[18]
+
+
+# ---------------------------------------------------------------- timing
 
 def time_kernel(fn, *, steps: int, warmup: int):
     """Warm up, then time ``steps`` back-to-back calls: wall clock around the region
@@ -101,14 +154,135 @@ def time_calls(fn, *, steps: int, warmup: int):
     return [a.elapsed_time(b) for a, b in ev]
 
 
+def measure(fn, *, flops: float, nbytes: float, hot_s: float = 0.2, regions: int = 5, per_region: int = 10,
+            calls: int = 50) -> dict:
+    """Kernel time of ``fn``: ``hot_s`` seconds of the same work first (the clocks drop under
+    light load and take tens of milliseconds of sustained work to come back), then the
+    median over ``regions`` regions of ``per_region`` back-to-back launches; p95 over
+    ``calls`` individually timed calls."""
+    import torch
+
+    t_end = time.perf_counter() + hot_s
+    while time.perf_counter() < t_end:
+        for _ in range(per_region):
+            fn()
+        torch.cuda.synchronize()
+    mean_ms = statistics.median(time_kernel(fn, steps=per_region, warmup=0)[1] for _ in range(regions))
+    per = time_calls(fn, steps=calls, warmup=0)
+    tf = flops / (mean_ms * 1e-3) / 1e12
+    return {
+        "tflops": round(tf, 2),
+        "frac_peak": round(tf / PEAK_TFLOPS, 4),
+        "mean_ms": round(mean_ms, 5),
+        "p95_ms": round(p95(per), 5),
+        "hbm_gbps_alg": round(nbytes / (mean_ms * 1e-3) / 1e9, 1),
+    }
+
+
+class _Env:
+    """Set TILEDATTN_* knobs for a block, restoring the previous values after it."""
+
+    def __init__(self, **env):
+        self.env = {"TILEDATTN_" + k.upper(): v for k, v in env.items()}
+        self.old = {}
+
+    def __enter__(self):
+        for k, v in self.env.items():
+            self.old[k] = os.environ.get(k)
+            os.environ[k] = str(v)
+
+    def __exit__(self, *exc):
+        for k, v in self.old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+def run_blocks(dev, only: str = "") -> dict:
+    """Every BASELINE.json configuration beside the headline, timed like the sweep."""
+    import torch
+
+    from tiledattention import sdpa
+
+    blocks: dict = {}
+
+    def want(name):
+        return name.startswith(only) if only else True
+
+    def one(name, shape, dtype, causal, seed, env=None, **input_kw):
+        b, h, s, d = shape
+        q, k, v = (t.to(dev) for t in make_inputs(shape, dtype, seed, **input_kw))
+        with _Env(**(env or {})):
+            fn = lambda: sdpa(q, k, v, causal=causal)  # noqa: E731
+            rec = measure(fn, flops=flops_of(b, h, s, d, causal), nbytes=alg_bytes(b, h, s, d))
+        rec.update({"B": b, "H": h, "S": s, "D": d, "dtype": dtype, "causal": causal, "seed": seed})
+        if env:
+            rec["knobs"] = {("TILEDATTN_" + k.upper()): v for k, v in env.items()}
+        _log(f"block {name}: {rec['tflops']} TFLOP/s ({rec['frac_peak']:.1%}), "
+             f"{rec['hbm_gbps_alg']} GB/s alg, p95 {rec['p95_ms']} ms")
+        del q, k, v
+        torch.cuda.empty_cache()
+        return rec
+
+    if want("C2"):
+        # C2: B1 H8 S1024 D64 fp16 non-causal, tile 64x64, fp32 accumulation (aligned fast path)
+        blocks["C2"] = one("C2", (1, 8, 1024, 64), "float16", False, 2026,
+                           env={"tile_m": 64, "tile_n": 64, "accum_mode": "fp32"})
+    if want("C3_fp16"):
+        blocks["C3_fp16"] = {str(s): one(f"C3_fp16 S={s}", (1, 8, s, 128), "float16", True, 1234)
+                             for s in (512, 1024, 2048, 4096, 8192)}
+    if want("C4"):
+        # C4: B4 H16 S4096 non-causal, inputs N(0,1)*0.5 seed 2026; every tile, both
+        # accumulation modes; plus the default configuration (no knobs).
+        c4 = {}
+        for dtype in ("float16", "bfloat16"):
+            for d in (64, 128):
+                shape = (4, 16, 4096, d)
+                q, k, v = (t.to(dev) for t in make_inputs(shape, dtype, 2026, scale_inputs=0.5))
+                for tiles in (None,) + C4_TILES:
+                    for acc in (("fp32",) if tiles is None else ("fp32", "fp16")):
+                        key = f"{'fp16' if dtype == 'float16' else 'bf16'}_d{d}_" + (
+                            "default" if tiles is None else f"{tiles[0]}x{tiles[1]}_{acc}")
+                        env = {} if tiles is None else {"tile_m": tiles[0], "tile_n": tiles[1],
+                                                         "accum_mode": acc}
+                        with _Env(**env):
+                            fn = lambda: sdpa(q, k, v, causal=False)  # noqa: E731
+                            rec = measure(fn, flops=flops_of(*shape, False), nbytes=alg_bytes(*shape),
+                                          hot_s=0.1, regions=3, per_region=10, calls=20)
+                        rec.update({"knobs": {("TILEDATTN_" + k_.upper()): v_ for k_, v_ in env.items()}})
+                        c4[key] = rec
+                        _log(f"block C4 {key}: {rec['tflops']} TFLOP/s ({rec['frac_peak']:.1%})")
+                del q, k, v
+                torch.cuda.empty_cache()
+        blocks["C4"] = c4
+    if want("C5"):
+        blocks["C5"] = one("C5", (1, 8, 16384, 128), "float16", True, 1234)
+        blocks["C5b"] = one("C5b", (1, 8, 16384, 128), "float16", True, 1234,
+                            outlier_frac=0.01, outlier_gain=20.0, outlier_seed=1235)
+    return blocks
+
+
+def _cpu_model() -> str:
+    """The host CPU's model string (``model name`` in /proc/cpuinfo)."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
 def cpu_baseline(shape, dtype: str, seed: int, causal: bool, budget_s: float):
-    """Time the eager restatement on host cores over whole (b, h) slices of the workload."""
+    """Time the eager restatement on host cores over whole (b, h) slices of the workload,
+    with every core this process may run on."""
     import torch
 
     from oracle import eager
     from oracle import oracle as O
 
-    threads = min(os.cpu_count() or 1, 16)
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
     torch.set_num_threads(threads)
     q, k, v = O.make_inputs(shape, dtype, seed)
     b_, h_, s, d = shape
@@ -138,7 +312,7 @@ def cpu_baseline(shape, dtype: str, seed: int, causal: bool, budget_s: float):
                    f"{per_head * 1e3:.1f} ms/head; same FLOP count as the GPU line"),
         "ms_per_head_median": per_head * 1e3,
         "ms_per_head_p95": O.p95([t * 1e3 for t in times]),
-        "cpu_model": platform.processor() or platform.machine(),
+        "cpu_model": _cpu_model(),
         "os_cpu_count": os.cpu_count(),
     }
 
@@ -152,17 +326,16 @@ def main() -> int:
 
     import torch
 
-    from oracle import oracle as O
-    from tiledattention_amd import _lib, sdpa
-    from tiledattention_amd.kernels import flash_fwd
+    from tiledattention import _lib, sdpa
+    from tiledattention.kernels import flash_fwd
 
     dev = torch.device("cuda:0")
     b, h, s, d = 1, 8, args.seq, 128
     dtype, causal, seed = "bfloat16", True, 1234
     _log(f"workload C3 B={b} H={h} S={s} D={d} {dtype} causal seed={seed}")
-    q, k, v = (t.to(dev) for t in O.make_inputs((b, h, s, d), dtype, seed))
-    flops = O.attention_forward_flops(b=b, h=h, s=s, d=d, causal=causal)
-    nbytes = O.approximate_bytes(b=b, h=h, s=s, d=d, bytes_per_elem=2)
+    q, k, v = (t.to(dev) for t in make_inputs((b, h, s, d), dtype, seed))
+    flops = flops_of(b, h, s, d, causal)
+    nbytes = alg_bytes(b, h, s, d)
 
     def step():
         return sdpa(q, k, v, causal=causal)
@@ -198,29 +371,13 @@ def main() -> int:
     sweep = {}
     if not args.no_sweep:
         for ss in (512, 1024, 2048, 4096, 8192):
-            qs, ks, vs = (t.to(dev) for t in O.make_inputs((1, 8, ss, 128), dtype, seed))
-            f = O.attention_forward_flops(b=1, h=8, s=ss, d=128, causal=True)
+            qs, ks, vs = (t.to(dev) for t in make_inputs((1, 8, ss, 128), dtype, seed))
             fn_s = lambda: sdpa(qs, ks, vs, causal=True)  # noqa: E731
-            # The clocks drop under the light load of the smaller sizes and take tens of
-            # milliseconds of sustained work to come back: 0.2 s of this size first, then the
-            # median over five regions of ten back-to-back launches.
-            t_end = time.perf_counter() + 0.2
-            while time.perf_counter() < t_end:
-                for _ in range(10):
-                    fn_s()
-                torch.cuda.synchronize()
-            mean_s = statistics.median(time_kernel(fn_s, steps=10, warmup=0)[1] for _ in range(5))
-            per_s = time_calls(fn_s, steps=50, warmup=0)
-            sweep[str(ss)] = {
-                "tflops": round(f / (mean_s * 1e-3) / 1e12, 2),
-                "frac_peak": round(f / (mean_s * 1e-3) / 1e12 / PEAK_TFLOPS, 4),
-                "mean_ms": round(mean_s, 5),
-                "p95_ms": round(O.p95(per_s), 5),
-                "hbm_gbps_alg": round(O.approximate_bytes(b=1, h=8, s=ss, d=128, bytes_per_elem=2)
-                                      / (mean_s * 1e-3) / 1e9, 1),
-            }
+            sweep[str(ss)] = measure(fn_s, flops=flops_of(1, 8, ss, 128, True), nbytes=alg_bytes(1, 8, ss, 128))
             _log(f"sweep S={ss}: {sweep[str(ss)]}")
             del qs, ks, vs
+
+    blocks = {} if args.no_blocks else run_blocks(dev, args.only_block)
 
     line = {
         "metric": "SDPA fwd TFLOP/s vs seq len (fp16/bf16, D=64/128) + % of MI355X MFMA peak",
@@ -253,6 +410,7 @@ def main() -> int:
             "alg_bytes": nbytes,
         },
         "sweep": sweep,
+        "blocks": blocks,
     }
 
     if args.copy_probe_mib > 0:

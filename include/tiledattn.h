@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define TA_ABI_VERSION 1
+#define TA_ABI_VERSION 2
 
 typedef enum ta_status {
   TA_OK = 0,
@@ -58,7 +58,9 @@ typedef struct ta_fwd_args {
   int64_t B, H, S, D; /* D: 64, 128, 160 or 256 (callers zero-pad other head dims, or
                          set d_real); 160 and 256 need tile_n = 64 */
   int64_t q_stride[4]; /* element strides for (B,H,S,D); stride[3] must be 1, the others
-                          multiples of 8; S * stride[2] * 2 bytes below 2^31 for k and v
+                          non-negative multiples of 8; the row stride stride[2] at least
+                          the row width (D, or d_real when set: rows must not overlap)
+                          and below 2^23; S * stride[2] * 2 bytes below 2^31 for k and v
                           (and for q on tiles (128, 64) / (128, 128) with fp32
                           accumulation), which are read with 32-bit buffer offsets */
   int64_t k_stride[4];
@@ -78,6 +80,11 @@ typedef struct ta_fwd_args {
                       write them, so a narrower head dim needs no padded copies (the
                       reference pads on the host, flash_fwd.py:868-872).  Tiles (128, 64)
                       and (128, 128) with fp32 accumulation and D <= 160 only. */
+  int32_t aligned; /* 1: the kernel variant without tail masking runs when S is a multiple
+                      of tile_m and tile_n (the reference's aligned fast path,
+                      flash_fwd.py:199-238, 880-921); 0: the tail-masked variant always
+                      runs (TILEDATTN_DISABLE_ALIGNED_FASTPATH).  Both give the same
+                      result on such S; zero-initialised arguments get the masked one. */
 } ta_fwd_args;
 
 /* Version of this ABI (TA_ABI_VERSION). */
@@ -94,9 +101,9 @@ ta_status ta_set_code_object_dir(const char* dir);
 ta_status ta_prepare(int32_t device, int32_t dtype, int32_t head_dim, int32_t tile_m,
                      int32_t tile_n, int32_t causal, int32_t accum, int32_t aligned);
 
-/* Enqueue one SDPA forward on `stream`.  Picks the unmasked-tail kernel when S is a
- * multiple of both tiles.  Zero-size problems (B*H == 0 or S == 0) return TA_OK with no
- * launch. */
+/* Enqueue one SDPA forward on `stream`.  Picks the unmasked-tail kernel when
+ * args->aligned is 1 and S is a multiple of both tiles.  Zero-size problems (B*H == 0 or
+ * S == 0) return TA_OK with no launch. */
 ta_status ta_sdpa_fwd(const ta_fwd_args* args, void* stream);
 
 /* Split key ranges: no counterpart in the reference, whose grid is one program per

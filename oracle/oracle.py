@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
 ``cpu_baseline`` leg may import this module, and only as the checker or the timed CPU
-baseline; the operator in ``tiledattention_amd`` never imports it and has no CPU fallback.
+baseline; the operator in ``tiledattention`` never imports it and has no CPU fallback.
 
 Contents:
 

@@ -2,7 +2,7 @@
 
 Markers: ``gpu`` - needs a gfx950 GPU and the built native library; the CPU suite runs with
 ``-m "not gpu"``.  The repository root is put on ``sys.path`` so ``oracle`` (test
-infrastructure) and ``tiledattention_amd`` import from the checkout.
+infrastructure) and ``tiledattention`` import from the checkout.
 """
 
 from __future__ import annotations
@@ -55,7 +55,7 @@ def gpu():
     """Skip unless a GPU is visible; on a GPU box the kernels must be built (fail loudly)."""
     if not gpu_available():
         pytest.skip("no GPU visible")
-    from tiledattention_amd import _runtime
+    from tiledattention import _runtime
 
     _runtime._reset_runtime_cache_for_tests()
     _runtime.require_supported_runtime()

@@ -56,7 +56,7 @@ def inputs(shape, dtype, seed, **kw):
 def run_gpu(q, k, v, *, causal, scale=None, **env):
     import torch
 
-    from tiledattention_amd import sdpa
+    from tiledattention import sdpa
 
     dev = torch.device("cuda:0")
     qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)

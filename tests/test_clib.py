@@ -10,7 +10,7 @@ from pathlib import Path
 
 import pytest
 
-from tiledattention_amd import _lib
+from tiledattention import _lib
 
 ROOT = Path(__file__).resolve().parents[1]
 HEADER = ROOT / "include" / "tiledattn.h"
@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_status_names(lib):
-    assert lib.ta_abi_version() == _lib.ABI_VERSION == 1
+    assert lib.ta_abi_version() == _lib.ABI_VERSION == 2
     names = [lib.ta_status_string(i).decode() for i in range(5)]
     assert names == ["TA_OK", "TA_EINVAL", "TA_EUNSUPPORTED", "TA_ENOKERNEL", "TA_EHIP"]
     assert lib.ta_status_string(99).decode() == "TA_UNKNOWN"
@@ -58,6 +58,10 @@ def _args(**kw) -> _lib.FwdArgs:
         else:
             setattr(a, key, val)
     return a
+
+
+# element strides of dense D = 128 rows (batch and head strides 0: a broadcast slice is valid)
+_D128 = {n: (0, 0, 128, 1) for n in ("q_stride", "k_stride", "v_stride", "o_stride")}
 
 
 def _call(lib, a):
@@ -79,11 +83,22 @@ def _call(lib, a):
     (dict(v=0x10008), _lib.TA_EINVAL, "16-byte aligned"),
     (dict(k_stride=(2 * 64 * 64, 64 * 64, 64, 2)), _lib.TA_EINVAL, "last-dim stride"),
     (dict(o_stride=(2 * 64 * 64, 64 * 64, 68, 1)), _lib.TA_EINVAL, "multiple of 8"),
-    (dict(S=1 << 24, k_stride=(0, 0, 128, 1), D=128), _lib.TA_EINVAL, "2^31"),
-    (dict(S=2, k_stride=(0, 0, 1 << 23, 1)), _lib.TA_EINVAL, "128 * row stride"),
+    (dict(S=1 << 24, D=128, **_D128), _lib.TA_EINVAL, "2^31"),
+    (dict(S=2, k_stride=(0, 0, 1 << 23, 1)), _lib.TA_EINVAL, "k: row stride 8388608 must stay below 2^23"),
+    # a stride large enough that S * stride would overflow int64 is rejected by its bound first
+    (dict(S=1 << 30, v_stride=(0, 0, 1 << 60, 1)), _lib.TA_EINVAL, "v: row stride"),
     # Q's range limit applies where Q is staged with buffer loads (the eight-wave kernel)
-    (dict(S=1 << 20, q_stride=(0, 0, 1024, 1), D=128, tile_m=128), _lib.TA_EINVAL, "q: S * row stride"),
-    (dict(S=2, q_stride=(0, 0, 1 << 23, 1), D=128, tile_m=128), _lib.TA_EINVAL, "q: S * row stride"),
+    (dict(S=1 << 20, D=128, tile_m=128, **{**_D128, "q_stride": (0, 0, 1024, 1)}), _lib.TA_EINVAL,
+     "q: S * row stride"),
+    (dict(S=2, q_stride=(0, 0, 1 << 23, 1), D=128, tile_m=128), _lib.TA_EINVAL, "q: row stride"),
+    # rows that overlap: a zero row stride (k expanded along S) or one below the row width
+    (dict(k_stride=(0, 0, 0, 1)), _lib.TA_EINVAL, "k: row stride 0 is below the row width 64"),
+    (dict(v_stride=(0, 0, 56, 1)), _lib.TA_EINVAL, "v: row stride 56 is below the row width 64"),
+    (dict(D=128, **{**_D128, "o_stride": (0, 0, 120, 1)}), _lib.TA_EINVAL,
+     "o: row stride 120"),
+    (dict(d_real=96, D=128, tile_m=128, **{**_D128, "k_stride": (0, 0, 88, 1)}), _lib.TA_EINVAL,
+     "below the row width 96"),
+    (dict(aligned=2), _lib.TA_EINVAL, "aligned 2"),
     (dict(d_real=4), _lib.TA_EINVAL, "d_real 4"),
     (dict(d_real=72), _lib.TA_EINVAL, "d_real 72"),        # above D = 64
     (dict(d_real=-8), _lib.TA_EINVAL, "d_real"),

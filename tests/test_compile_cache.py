@@ -5,7 +5,7 @@ from __future__ import annotations
 
 import threading
 
-from tiledattention_amd.kernels import compile_cache as cc
+from tiledattention.kernels import compile_cache as cc
 
 
 def test_get_kernel_hit_miss_and_reset():

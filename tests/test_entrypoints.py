@@ -23,3 +23,28 @@ def test_graft_entry_exposes_build_and_smoke():
     sys.path.insert(0, str(ROOT))
     mod = importlib.import_module("__graft_entry__")
     assert callable(mod.build) and callable(mod.smoke)
+
+
+def test_bench_workload_inputs_and_counts_match_the_oracle_helpers():
+    """bench.py generates its inputs and counts work on its own (the product and the bench
+    never import the oracle outside the CPU-baseline leg); both must equal what the parity
+    tests feed the oracle, so every timed configuration is one the tests check."""
+    import torch
+
+    sys.path.insert(0, str(ROOT))
+    import bench
+    from oracle import oracle as O
+
+    for kw in ({}, {"scale_inputs": 0.5}, {"outlier_frac": 0.01, "outlier_gain": 20.0, "outlier_seed": 1235}):
+        for dtype in ("float16", "bfloat16"):
+            a = bench.make_inputs((1, 2, 64, 64), dtype, 1234, **kw)
+            b = O.make_inputs((1, 2, 64, 64), dtype, 1234, **kw)
+            for x, y in zip(a, b):
+                assert x.dtype == y.dtype and torch.equal(x, y)
+    for causal in (False, True):
+        assert bench.flops_of(1, 8, 8192, 128, causal) == O.attention_forward_flops(b=1, h=8, s=8192, d=128,
+                                                                                    causal=causal)
+    assert bench.alg_bytes(1, 8, 8192, 128) == O.approximate_bytes(b=1, h=8, s=8192, d=128, bytes_per_elem=2)
+    vals = [0.1 * i for i in range(1, 60)]
+    assert bench.p95(vals) == O.p95(vals)
+    assert bench.flops_of(1, 8, 8192, 128, True) == 137438953472.0  # 2*B*H*S^2*D

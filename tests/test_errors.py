@@ -10,8 +10,8 @@ from __future__ import annotations
 import pytest
 
 from tests.fakes import make_torch_module
-from tiledattention_amd._errors import DependencyError, UnsupportedPlatformError
-from tiledattention_amd._runtime import _reset_runtime_cache_for_tests, require_supported_runtime
+from tiledattention._errors import DependencyError, UnsupportedPlatformError
+from tiledattention._runtime import _reset_runtime_cache_for_tests, require_supported_runtime
 
 
 def _raise_dependency_error(message: str) -> None:
@@ -19,7 +19,7 @@ def _raise_dependency_error(message: str) -> None:
 
 
 def test_runtime_raises_on_gpu_unavailable(monkeypatch: pytest.MonkeyPatch) -> None:
-    import tiledattention_amd._runtime as runtime
+    import tiledattention._runtime as runtime
 
     monkeypatch.setattr(runtime, "_get_torch_module", lambda: make_torch_module(cuda_available=False))
     _reset_runtime_cache_for_tests()
@@ -28,7 +28,7 @@ def test_runtime_raises_on_gpu_unavailable(monkeypatch: pytest.MonkeyPatch) -> N
 
 
 def test_runtime_raises_on_non_rocm_torch(monkeypatch: pytest.MonkeyPatch) -> None:
-    import tiledattention_amd._runtime as runtime
+    import tiledattention._runtime as runtime
 
     monkeypatch.setattr(runtime, "_get_torch_module",
                         lambda: make_torch_module(cuda_available=True, hip=None))
@@ -38,7 +38,7 @@ def test_runtime_raises_on_non_rocm_torch(monkeypatch: pytest.MonkeyPatch) -> No
 
 
 def test_runtime_raises_on_non_gfx950_gpu(monkeypatch: pytest.MonkeyPatch) -> None:
-    import tiledattention_amd._runtime as runtime
+    import tiledattention._runtime as runtime
 
     monkeypatch.setattr(runtime, "_get_torch_module",
                         lambda: make_torch_module(cuda_available=True, arch="gfx942:sramecc+:xnack-"))
@@ -48,7 +48,7 @@ def test_runtime_raises_on_non_gfx950_gpu(monkeypatch: pytest.MonkeyPatch) -> No
 
 
 def test_runtime_raises_on_missing_native_library(monkeypatch: pytest.MonkeyPatch) -> None:
-    import tiledattention_amd._runtime as runtime
+    import tiledattention._runtime as runtime
 
     monkeypatch.setattr(runtime, "_get_torch_module", lambda: make_torch_module(cuda_available=True))
     monkeypatch.setattr(runtime, "_get_native_library",
@@ -60,7 +60,7 @@ def test_runtime_raises_on_missing_native_library(monkeypatch: pytest.MonkeyPatc
 
 def test_missing_library_file_is_a_dependency_error(monkeypatch: pytest.MonkeyPatch, tmp_path) -> None:
     # The real loader, pointed at an empty directory: fails loudly, no fallback.
-    from tiledattention_amd import _lib
+    from tiledattention import _lib
 
     monkeypatch.setenv("TILEDATTN_LIB_DIR", str(tmp_path))
     monkeypatch.setattr(_lib, "_lib", None)
@@ -69,7 +69,7 @@ def test_missing_library_file_is_a_dependency_error(monkeypatch: pytest.MonkeyPa
 
 
 def test_missing_code_object_is_a_dependency_error(monkeypatch: pytest.MonkeyPatch, tmp_path) -> None:
-    from tiledattention_amd import _lib
+    from tiledattention import _lib
 
     real = _lib.library_path()
     if not real.exists():
@@ -82,7 +82,7 @@ def test_missing_code_object_is_a_dependency_error(monkeypatch: pytest.MonkeyPat
 
 
 def test_gate_passes_with_fakes_and_is_cached(monkeypatch: pytest.MonkeyPatch) -> None:
-    import tiledattention_amd._runtime as runtime
+    import tiledattention._runtime as runtime
 
     calls = []
     monkeypatch.setattr(runtime, "_get_torch_module", lambda: make_torch_module(cuda_available=True))

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 from tests.parity_util import check_close, inputs, oracle_f32, say
-from tiledattention_amd import _lib
+from tiledattention import _lib
 
 pytestmark = pytest.mark.gpu
 

@@ -162,7 +162,7 @@ def test_head_dim_in_kernel_padding(gpu, d, dtype, causal, s):
     kernel's D), all against the oracle."""
     import torch
 
-    from tiledattention_amd import sdpa
+    from tiledattention import sdpa
 
     q, k, v = inputs((2, 3, s, d), dtype, 40 + d)
     rows = None if s <= 2048 else sample_rows(s, 96)
@@ -206,7 +206,7 @@ def test_eight_wave_d160(gpu, d, dtype, causal, s):
     the missing tail columns read as zero.  Ragged S, both dtypes, [B,S,H,D] views."""
     import torch
 
-    from tiledattention_amd import _lib, sdpa
+    from tiledattention import _lib, sdpa
 
     assert _lib.kernel_symbol(dtype=_lib.TA_BF16, head_dim=160, tile_m=128, tile_n=64,
                               causal=causal, tail=False, accum=_lib.TA_ACC_FP32)[1].startswith("ta_fwd_pp_")
@@ -309,7 +309,7 @@ def test_strided_inputs_match_contiguous(gpu):
 def test_non_default_stream_and_sync_modes(gpu):
     import torch
 
-    from tiledattention_amd import sdpa
+    from tiledattention import sdpa
     from tests.parity_util import knobs
 
     q, k, v = (t.cuda() for t in inputs((1, 2, 512, 64), "bfloat16", 9))
@@ -326,7 +326,7 @@ def test_non_default_stream_and_sync_modes(gpu):
 def test_zero_size_inputs(gpu):
     import torch
 
-    from tiledattention_amd import sdpa
+    from tiledattention import sdpa
 
     say("zero-size inputs")
     for shape in [(0, 2, 16, 64), (1, 0, 16, 64), (1, 2, 0, 64)]:
@@ -338,7 +338,7 @@ def test_zero_size_inputs(gpu):
 def test_invalid_knobs_raise_before_launch(gpu):
     import torch
 
-    from tiledattention_amd import sdpa
+    from tiledattention import sdpa
     from tests.parity_util import knobs
 
     q = torch.zeros((1, 1, 64, 64), dtype=torch.float16, device="cuda")

@@ -63,7 +63,7 @@ _CASES = [_draw(r) for r in [random.Random(_SEED)] for _ in range(_N)]
 def test_randomized_parity(gpu, case):
     import torch
 
-    from tiledattention_amd import sdpa
+    from tiledattention import sdpa
 
     c = case
     q, k, v = inputs((c["b"], c["h"], c["s"], c["d"]), c["dtype"], c["seed"], scale_inputs=c["mag"])

@@ -48,7 +48,7 @@ def test_split_and_whole_rows_agree(gpu, shape):
     """bf16 causal, seed 1234, forced 8-step chunks (C3's shape) and the automatic plan
     (which splits the B*H = 1 and 2 shapes): both paths meet the oracle's tolerance and
     differ from each other only by the rounding of the merge."""
-    from tiledattention_amd.kernels import flash_fwd
+    from tiledattention.kernels import flash_fwd
 
     s, n_bh = shape[2], shape[1]
     q, k, v = inputs(shape, "bfloat16", 1234)
@@ -87,7 +87,7 @@ def test_strided_inputs_and_scale(gpu):
     """[B,S,H,D]-strided views (no copy: unit last stride, 16-byte rows) and an explicit scale."""
     import torch
 
-    from tiledattention_amd import sdpa
+    from tiledattention import sdpa
 
     q, k, v = inputs((2, 4, 640, 64), "bfloat16", 77)
     ref = oracle_f32(q, k, v, causal=True, scale=0.3)
@@ -106,7 +106,7 @@ def test_cabi_chunk_zero_is_the_whole_row_launch(gpu):
     outputs are bit-identical."""
     import torch
 
-    from tiledattention_amd import _lib
+    from tiledattention import _lib
 
     lib = _lib.load()
     q, k, v = inputs((1, 2, 512, 128), "float16", 5)
@@ -140,7 +140,7 @@ def test_cabi_split_with_caller_workspace(gpu):
     different shapes in a row on one stream; the workspace starts as garbage."""
     import torch
 
-    from tiledattention_amd import _lib
+    from tiledattention import _lib
 
     lib = _lib.load()
     dev = torch.device("cuda:0")

@@ -9,7 +9,7 @@ import math
 import pytest
 
 from tests.parity_util import say
-from tiledattention_amd import study
+from tiledattention import study
 
 pytestmark = pytest.mark.gpu
 

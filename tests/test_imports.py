@@ -4,8 +4,8 @@ from __future__ import annotations
 
 
 def test_import_tiledattention() -> None:
-    import tiledattention_amd
+    import tiledattention
 
-    assert isinstance(tiledattention_amd.__version__, str)
-    assert tiledattention_amd.__version__
-    assert hasattr(tiledattention_amd, "sdpa")
+    assert isinstance(tiledattention.__version__, str)
+    assert tiledattention.__version__
+    assert hasattr(tiledattention, "sdpa")

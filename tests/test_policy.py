@@ -9,9 +9,9 @@ from __future__ import annotations
 
 import pytest
 
-from tiledattention_amd._errors import DTypeNotSupportedError, InvalidShapeError
-from tiledattention_amd import _lib
-from tiledattention_amd.kernels import flash_fwd as ff
+from tiledattention._errors import DTypeNotSupportedError, InvalidShapeError
+from tiledattention import _lib
+from tiledattention.kernels import flash_fwd as ff
 
 
 # ---------------------------------------------------------------- flash_fwd.py:47-65
@@ -67,16 +67,6 @@ def test_gfx950_tile_set(tm, tn, ok):
             ff._check_tile_supported(tm, tn)
 
 
-# ---------------------------------------------------------------- flash_fwd.py:241-259
-@pytest.mark.parametrize("s,d,causal,expected", [
-    (2048, 128, False, (64, 128)), (8192, 128, False, (64, 128)),
-    (2047, 128, False, (64, 64)), (2048, 128, True, (64, 64)),
-    (4096, 64, False, (64, 64)), (4096, 96, False, (64, 64)), (64, 64, True, (64, 64)),
-])
-def test_reference_default_tile_table(s, d, causal, expected):
-    assert ff._default_tile_config_for_shape(seq_len=s, head_dim=d, causal=causal) == expected
-
-
 # ---------------------------------------------------------------- flash_fwd.py:87-99
 def test_kernel_options_defaults_and_parse(monkeypatch):
     assert ff._resolve_kernel_options() == (3, None, None)
@@ -90,15 +80,6 @@ def test_kernel_options_defaults_and_parse(monkeypatch):
 
 
 # ---------------------------------------------------------------- flash_fwd.py:102-146
-@pytest.mark.parametrize("s,d,causal,expected", [
-    (1024, 64, False, "fp16"), (4096, 64, False, "fp16"), (1023, 64, False, "fp32"),
-    (1024, 64, True, "fp32"), (1024, 128, False, "fp32"), (8192, 128, False, "fp32"),
-    (1024, 32, False, "fp32"),
-])
-def test_default_accum_mode_table(s, d, causal, expected):
-    assert ff._default_accum_mode_for_shape(seq_len=s, head_dim=d, causal=causal) == expected
-
-
 @pytest.mark.parametrize("raw,expected", [
     (None, "fp32"), ("", "fp32"), ("auto", "fp32"), (" AUTO ", "fp32"),
     ("fp32", "fp32"), (" FP32", "fp32"), ("fp16", "fp16"), ("Fp16 ", "fp16"),
@@ -108,9 +89,9 @@ def test_resolve_accum_mode(monkeypatch, raw, expected):
         monkeypatch.delenv("TILEDATTN_ACCUM_MODE", raising=False)
     else:
         monkeypatch.setenv("TILEDATTN_ACCUM_MODE", raw)
-    # a shape where the reference's auto rule picks the input dtype (non-causal, D=64,
-    # S>=1024); on gfx950 auto resolves to fp32 (faster and more accurate here)
-    assert ff._default_accum_mode_for_shape(seq_len=2048, head_dim=64, causal=False) == "fp16"
+    # a shape where the reference's auto rule (flash_fwd.py:102-120: non-causal, D = 64,
+    # S >= 1024) picks the input dtype; on gfx950 auto resolves to fp32 (faster and more
+    # accurate here)
     assert ff._resolve_accum_mode(seq_len=2048, head_dim=64, causal=False) == expected
 
 
@@ -127,14 +108,6 @@ def test_resolve_accum_mode_rejects(monkeypatch, raw):
 
 
 # ---------------------------------------------------------------- flash_fwd.py:149-163
-@pytest.mark.parametrize("d,expected", [
-    (64, (64, 0)), (128, (128, 0)), (32, (32, 0)), (96, (128, 32)), (160, (256, 96)),
-    (48, (64, 16)), (100, (128, 28)), (1, (1, 0)), (65, (128, 63)),
-])
-def test_reference_head_dim_padding_rule(d, expected):
-    assert ff._resolve_kernel_head_dim(d) == expected
-
-
 @pytest.mark.parametrize("d,expected", [
     (1, (64, 63)), (32, (64, 32)), (64, (64, 0)), (65, (128, 63)), (96, (128, 32)), (128, (128, 0)),
     (129, (160, 31)), (160, (160, 0)), (161, (256, 95)), (192, (256, 64)), (256, (256, 0)),
@@ -170,32 +143,46 @@ def test_resolve_chunk_plan_rejects(monkeypatch):
 
 
 # ---------------------------------------------------------------- flash_fwd.py:199-238
-_FP = dict(pad_dim=0, chunk_plan=None, tile_m=64, tile_n=64)
-
-
-@pytest.mark.parametrize("kw,expected", [
-    (dict(seq_len=1024, head_dim=64, causal=False), True),
-    (dict(seq_len=1023, head_dim=64, causal=False), False),      # below the D=64 threshold
-    (dict(seq_len=1024, head_dim=128, causal=False), False),     # D=128 needs S >= 2048
-    (dict(seq_len=2048, head_dim=128, causal=False), True),
-    (dict(seq_len=2048, head_dim=128, causal=True), False),      # never for causal
-    (dict(seq_len=1088, head_dim=64, causal=False, tile_n=128), False),  # 1088 % 128 != 0
-    (dict(seq_len=1152, head_dim=64, causal=False, tile_m=128), True),   # 1152 = 9*128
-    (dict(seq_len=4096, head_dim=96, causal=False), False),      # D not in {64, 128}
-    (dict(seq_len=4096, head_dim=64, causal=False, pad_dim=8), False),
-    (dict(seq_len=4096, head_dim=64, causal=False, chunk_plan=((0, 64),)), False),
+@pytest.mark.parametrize("s,tm,tn,expected", [
+    (1024, 64, 64, True), (1024, 128, 64, True), (1024, 128, 128, True), (1088, 64, 128, False),
+    (1152, 128, 64, True), (100, 64, 64, False), (64, 128, 64, False), (8192, 128, 64, True),
 ])
-def test_aligned_fastpath_predicate(kw, expected):
-    args = {**_FP, **kw}
-    assert ff._should_use_aligned_noncausal_fastpath(**args) is expected
+def test_unmasked_tail_kernel_predicate(s, tm, tn, expected):
+    assert ff._use_unmasked_tail_kernel(seq_len=s, tile_m=tm, tile_n=tn) is expected
 
 
 @pytest.mark.parametrize("raw,expected", [("", True), ("0", True), ("false", True), ("False", True),
-                                          ("1", False), ("true", False), ("FALSE", False), ("yes", False)])
+                                          (" 0 ", True), ("1", False), ("true", False),
+                                          ("FALSE", False), ("yes", False)])
 def test_aligned_fastpath_disable_env(monkeypatch, raw, expected):
+    # the reference's parse (flash_fwd.py:225-226): only "", "0", "false", "False" keep it on
     monkeypatch.setenv("TILEDATTN_DISABLE_ALIGNED_FASTPATH", raw)
-    args = {**_FP, **dict(seq_len=1024, head_dim=64, causal=False)}
-    assert ff._should_use_aligned_noncausal_fastpath(**args) is expected
+    assert ff._use_unmasked_tail_kernel(seq_len=1024, tile_m=64, tile_n=64) is expected
+
+
+_D = 128
+
+
+@pytest.mark.parametrize("shape,stride,width,ok", [
+    ((1, 2, 64, _D), (2 * 64 * _D, 64 * _D, _D, 1), _D, True),      # dense
+    ((1, 2, 64, _D), (64 * 4 * _D, _D, 4 * _D, 1), _D, True),       # [B,S,H,D] transposed
+    ((1, 2, 64, _D), (0, 0, _D, 1), _D, True),                      # broadcast (b, h)
+    ((1, 2, 64, _D), (0, 64 * _D, 0, 1), _D, False),                # expanded along S
+    ((1, 2, 1, _D), (0, _D, 0, 1), _D, False),                      # S = 1, zero row stride
+    ((1, 2, 64, _D), (0, 0, 120, 1), _D, False),                    # overlapping rows
+    ((1, 2, 64, 96), (0, 0, 96, 1), 96, True),                      # in-kernel padded width
+    ((1, 2, 64, 96), (0, 0, 96, 1), _D, False),                     # needs a host pad
+    ((1, 2, 64, _D), (0, 0, 132, 1), _D, False),                    # 16-byte rows
+    ((1, 2, 64, _D), (0, 0, _D, 2), _D, False),                     # last stride
+    ((1, 1, 2, _D), (0, 0, 1 << 23, 1), _D, False),                 # 128 rows >= 2^31 bytes
+    ((1, 1, (1 << 16) - 1, _D), (0, 0, 1 << 14, 1), _D, True),      # slice = 2^31 - 2^15 bytes
+    ((1, 1, 1 << 16, _D), (0, 0, 1 << 14, 1), _D, False),           # slice = 2^31 bytes
+])
+def test_strides_kernel_ready(shape, stride, width, ok):
+    """Which views the kernels read in place; the rest are copied to dense tensors (the C ABI
+    rejects them with TA_EINVAL, tests/test_clib.py)."""
+    assert ff._strides_ok(stride, shape, width) is ok
+
 
 
 # ---------------------------------------------------------------- flash_fwd.py:805-818

@@ -7,23 +7,23 @@ from types import ModuleType
 import pytest
 
 from tests.fakes import FakeTensor, make_torch_module
-from tiledattention_amd._errors import (
+from tiledattention._errors import (
     DTypeNotSupportedError,
     InvalidShapeError,
     UnsupportedPlatformError,
 )
-from tiledattention_amd._runtime import _reset_runtime_cache_for_tests
-from tiledattention_amd.sdpa import sdpa
+from tiledattention._runtime import _reset_runtime_cache_for_tests
+from tiledattention.sdpa import sdpa
 
 
 def _patch_runtime_dependency_modules(monkeypatch: pytest.MonkeyPatch) -> None:
-    import tiledattention_amd._runtime as runtime
+    import tiledattention._runtime as runtime
 
     monkeypatch.setattr(runtime, "_get_native_library", lambda: ModuleType("libtiledattn"))
 
 
 def _gpu_torch(monkeypatch):
-    import tiledattention_amd._runtime as runtime
+    import tiledattention._runtime as runtime
 
     torch_mod = make_torch_module(cuda_available=True)
     monkeypatch.setattr(runtime, "_get_torch_module", lambda: torch_mod)
@@ -32,7 +32,7 @@ def _gpu_torch(monkeypatch):
 
 
 def test_sdpa_prefers_runtime_error_on_cpu_path(monkeypatch: pytest.MonkeyPatch) -> None:
-    import tiledattention_amd._runtime as runtime
+    import tiledattention._runtime as runtime
 
     monkeypatch.setattr(runtime, "_get_torch_module", lambda: make_torch_module(cuda_available=False))
     _reset_runtime_cache_for_tests()
@@ -57,7 +57,7 @@ def test_sdpa_validates_dtype(monkeypatch: pytest.MonkeyPatch) -> None:
 
 
 def test_sdpa_valid_input_reaches_kernel_stub(monkeypatch: pytest.MonkeyPatch) -> None:
-    import tiledattention_amd.sdpa as sdpa_mod
+    import tiledattention.sdpa as sdpa_mod
 
     torch_mod = _gpu_torch(monkeypatch)
     seen = {}
@@ -77,7 +77,7 @@ def test_sdpa_valid_input_reaches_kernel_stub(monkeypatch: pytest.MonkeyPatch) -
 
 @pytest.mark.parametrize("causal", [1, "yes", None])
 def test_causal_must_be_bool_before_runtime_gate(monkeypatch, causal) -> None:
-    import tiledattention_amd._runtime as runtime
+    import tiledattention._runtime as runtime
 
     monkeypatch.setattr(runtime, "_get_torch_module", lambda: make_torch_module(cuda_available=False))
     _reset_runtime_cache_for_tests()
@@ -87,7 +87,7 @@ def test_causal_must_be_bool_before_runtime_gate(monkeypatch, causal) -> None:
 
 @pytest.mark.parametrize("scale", [0, -1.0, "0.5", complex(1, 0)])
 def test_scale_must_be_positive_real(monkeypatch, scale) -> None:
-    import tiledattention_amd._runtime as runtime
+    import tiledattention._runtime as runtime
 
     monkeypatch.setattr(runtime, "_get_torch_module", lambda: make_torch_module(cuda_available=False))
     _reset_runtime_cache_for_tests()
@@ -96,7 +96,7 @@ def test_scale_must_be_positive_real(monkeypatch, scale) -> None:
 
 
 def test_scale_true_passes_as_one(monkeypatch) -> None:
-    import tiledattention_amd.sdpa as sdpa_mod
+    import tiledattention.sdpa as sdpa_mod
 
     torch_mod = _gpu_torch(monkeypatch)
     got = []
@@ -108,7 +108,7 @@ def test_scale_true_passes_as_one(monkeypatch) -> None:
 
 
 def test_zero_head_dim_default_scale_raises(monkeypatch) -> None:
-    import tiledattention_amd.sdpa as sdpa_mod
+    import tiledattention.sdpa as sdpa_mod
 
     torch_mod = _gpu_torch(monkeypatch)
     monkeypatch.setattr(sdpa_mod, "run_flash_fwd", lambda *a, **kw: "ok")

@@ -13,8 +13,8 @@ from pathlib import Path
 
 import pytest
 
-from tiledattention_amd import _lib
-from tiledattention_amd.kernels import flash_fwd
+from tiledattention import _lib
+from tiledattention.kernels import flash_fwd
 
 ROOT = Path(__file__).resolve().parents[1]
 MI355X_CUS = 256
@@ -219,7 +219,7 @@ def test_knob_snapshot_follows_the_environment(monkeypatch):
         monkeypatch.delenv(name)
         assert flash_fwd._knob_snapshot() == base
     # every TILEDATTN_* knob the host path reads is part of the key
-    src = (ROOT / "tiledattention_amd" / "kernels" / "flash_fwd.py").read_text()
+    src = (ROOT / "tiledattention" / "kernels" / "flash_fwd.py").read_text()
     import re
 
     read = set(re.findall(r'"(TILEDATTN_[A-Z_]+)"', src))

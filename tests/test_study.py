@@ -8,7 +8,7 @@ import math
 
 import pytest
 
-from tiledattention_amd import study
+from tiledattention import study
 
 
 def test_bench_schema_is_the_reference_column_order():

@@ -7,8 +7,8 @@ import pytest
 
 torch = pytest.importorskip("torch")
 
-from tiledattention_amd import torch_op  # noqa: E402  (registers the operator)
-from tiledattention_amd._errors import DTypeNotSupportedError, InvalidShapeError  # noqa: E402
+from tiledattention import torch_op  # noqa: E402  (registers the operator)
+from tiledattention._errors import DTypeNotSupportedError, InvalidShapeError  # noqa: E402
 
 
 def _fake_mode():
@@ -21,7 +21,7 @@ def test_operator_is_registered():
     assert torch_op.OP_NAME == "tiledattention::sdpa_fwd"
     op = torch.ops.tiledattention.sdpa_fwd.default
     names = [a.name for a in op._schema.arguments]
-    assert names == ["q", "k", "v", "causal", "scale"]
+    assert names == ["q", "k", "v", "causal", "scale", "tile_m", "tile_n", "accum"]
     assert str(op._schema.returns[0].type) == "Tensor"
 
 
@@ -57,3 +57,21 @@ def test_graph_capture_keeps_the_operator():
         g = make_fx(fn, tracing_mode="real")(q, q, q)
     targets = [str(n.target) for n in g.graph.nodes if n.op == "call_function"]
     assert targets[0].startswith("tiledattention.sdpa_fwd")
+
+
+@pytest.mark.parametrize("tm,tn,acc,msg", [
+    (64, 0, -1, "both be 0"), (0, 128, -1, "both be 0"), (32, 64, -1, "Unsupported tile"),
+    (128, 256, -1, "Unsupported tile"), (0, 0, 2, "accum must be"), (64, 64, -2, "accum must be"),
+])
+def test_fake_checks_the_tile_and_accum_arguments(tm, tn, acc, msg):
+    with _fake_mode():
+        q = torch.empty((1, 2, 8, 64), dtype=torch.float16, device="cuda")
+        with pytest.raises(ValueError, match=msg):
+            torch.ops.tiledattention.sdpa_fwd(q, q, q, False, None, tm, tn, acc)
+
+
+def test_overrides_map_to_run_flash_fwd_keywords():
+    assert torch_op._overrides(0, 0, -1) == {}
+    assert torch_op._overrides(64, 128, -1) == {"tile": (64, 128)}
+    assert torch_op._overrides(0, 0, 1) == {"accum": "fp16"}
+    assert torch_op._overrides(128, 64, 0) == {"tile": (128, 64), "accum": "fp32"}

@@ -1,21 +1,23 @@
-"""ctypes binding of the C ABI in ``include/tiledattn.h`` (``lib/libtiledattn.so``).
+"""ctypes binding of the C ABI in ``include/tiledattn.h`` (``libtiledattn.so``).
 
 The library and the gfx950 code objects it loads are built in-tree by
-``tiledattention_amd/csrc/build.py`` into ``tiledattention_amd/lib/``.  ``TILEDATTN_LIB_DIR``
-overrides where both are looked up.  Nothing here falls back to another implementation:
-if the library is missing, ``load()`` raises ``DependencyError``.
+``tiledattention_amd/csrc/build.py`` into ``tiledattention_amd/lib/`` (the native package
+beside this one; located without importing it).  ``TILEDATTN_LIB_DIR`` overrides where both
+are looked up.  Nothing here falls back to another implementation: if the library is
+missing, ``load()`` raises ``DependencyError``.
 """
 
 from __future__ import annotations
 
 import ctypes
+import importlib.util
 import os
 from pathlib import Path
 from threading import Lock
 
 from ._errors import DependencyError
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 TA_OK = 0
 TA_EINVAL = 1
@@ -89,6 +91,7 @@ class FwdArgs(ctypes.Structure):
         ("device", ctypes.c_int32),
         ("sched", ctypes.c_int32),
         ("d_real", ctypes.c_int32),
+        ("aligned", ctypes.c_int32),
     ]
 
 
@@ -97,10 +100,18 @@ _lib: ctypes.CDLL | None = None
 
 
 def lib_dir() -> Path:
+    """Directory of ``libtiledattn.so`` and the code objects: ``TILEDATTN_LIB_DIR``, else
+    ``lib/`` of the ``tiledattention_amd`` package (found by its import spec, which does not
+    execute it)."""
     env = os.getenv("TILEDATTN_LIB_DIR", "").strip()
     if env:
         return Path(env)
-    return Path(__file__).resolve().parent / "lib"
+    spec = importlib.util.find_spec("tiledattention_amd")
+    if spec is None or not spec.submodule_search_locations:
+        raise DependencyError(
+            "The native package tiledattention_amd (kernels and C-ABI library) is not installed."
+        )
+    return Path(list(spec.submodule_search_locations)[0]) / "lib"
 
 
 def library_path() -> Path:

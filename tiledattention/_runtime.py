@@ -44,7 +44,7 @@ def _get_torch_module() -> ModuleType:
         return _cached_torch
     except ModuleNotFoundError as exc:
         raise DependencyError(
-            "PyTorch is required for tiledattention_amd. Install a ROCm-enabled torch build first."
+            "PyTorch is required for tiledattention. Install a ROCm-enabled torch build first."
         ) from exc
 
 
@@ -91,14 +91,14 @@ def require_supported_runtime() -> None:
 
         if not bool(torch_mod.cuda.is_available()):
             raise UnsupportedPlatformError(
-                "tiledattention_amd requires a ROCm (HIP) GPU of the MI355X class (gfx950). "
+                "tiledattention requires a ROCm (HIP) GPU of the MI355X class (gfx950). "
                 "torch.cuda.is_available() is False."
             )
 
         hip_version = getattr(getattr(torch_mod, "version", None), "hip", None)
         if not hip_version:
             raise UnsupportedPlatformError(
-                "tiledattention_amd requires PyTorch built for ROCm (torch.version.hip is not set)."
+                "tiledattention requires PyTorch built for ROCm (torch.version.hip is not set)."
             )
 
         arch = _query_device_arch(torch_mod)

@@ -8,7 +8,7 @@ from importlib.metadata import PackageNotFoundError, version
 def _resolve_version() -> str:
     """Installed distribution version, or ``"0.0.0"`` for an in-tree checkout."""
     try:
-        return version("tiledattention_amd")
+        return version("tiledattention")
     except PackageNotFoundError:
         return "0.0.0"
 

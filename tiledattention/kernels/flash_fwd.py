@@ -22,13 +22,20 @@ Environment knobs are re-read on every call, as in the reference:
     ``async`` (default) | ``post`` | ``strict`` (flash_fwd.py:805-818).  Validated before
     the launch here (the reference validates after launching).
 ``TILEDATTN_DISABLE_ALIGNED_FASTPATH``
-    As flash_fwd.py:225-226.
+    Parsed as flash_fwd.py:225-226 (anything but unset, "", "0", "false", "False"
+    disables).  The fast path is the kernel variant without tail masking
+    (``ta_fwd_args.aligned``): it runs when S is a multiple of both tile sizes, causal or
+    not, unless this knob is set, which forces the tail-masked variant.  The reference's
+    other conditions (non-causal, S >= 1024 / 2048, D in {64, 128}, flash_fwd.py:199-238)
+    exist because its aligned kernel has no causal mask and was tuned on GB10; both
+    variants compute the same result.
 ``TILEDATTN_KERNEL_OPT_LEVEL`` / ``_OCCUPANCY`` / ``_NUM_CTAS``
     Parsed as in flash_fwd.py:87-99 (``ValueError`` on non-integers) and kept in the cache
     key; the code objects are precompiled at -O3, so they do not change the kernel.
 ``TILEDATTN_CHUNKED_HEAD_DIMS``
     Parsed as in flash_fwd.py:166-196.  A chunked plan computes the same attention as the
-    unchunked one, so here it runs the zero-padded kernel (96 -> 128); 160 is rejected.
+    unchunked one, so here it runs the kernel that serves the head dim unchunked (96 on the
+    D = 128 kernel with in-kernel padding, 160 on the native D = 160 kernel).
 ``TILEDATTN_SCHED`` (this build only)
     Workgroup-to-tile order: ``0`` plain, ``1`` XCD-grouped, ``2`` XCD-grouped with causal
     heavy/light complementary order; default: see ``_resolve_sched``.
@@ -53,13 +60,6 @@ from .compile_cache import get_kernel
 
 _DEFAULT_TM = 64
 _DEFAULT_TN = 64
-_NEG_LARGE = -1.0e30
-_DIRECT_HEAD_DIMS = frozenset({64, 128})
-_ALIGNED_FASTPATH_HEAD_DIMS = frozenset({64, 128})
-_ALIGNED_FASTPATH_MIN_SEQ_BY_HEAD_DIM = {
-    64: 1024,
-    128: 2048,
-}
 _CHUNKED_HEAD_DIM_PARTS = {
     96: (64, 32),
     160: (128, 32),
@@ -121,15 +121,6 @@ def _resolve_kernel_options() -> tuple[int, int | None, int | None]:
     return opt_level, occupancy, num_ctas
 
 
-def _default_accum_mode_for_shape(*, seq_len: int, head_dim: int, causal: bool) -> str:
-    """The reference's auto accumulation policy (flash_fwd.py:102-120): input dtype iff
-    non-causal, D == 64, S >= 1024.  A speed heuristic for its kernels, kept for API
-    compatibility; ``auto`` resolves with ``_default_accum_mode_for_shape_gfx950``."""
-    if (not causal) and head_dim == 64 and seq_len >= 1024:
-        return "fp16"
-    return "fp32"
-
-
 def _default_accum_mode_for_shape_gfx950(*, seq_len: int, head_dim: int, causal: bool) -> str:
     """``auto`` on gfx950: fp32 for every shape.  Input-dtype accumulation runs the four-wave
     kernels and rounds O after every key tile; fp32 runs the eight-wave kernel at the
@@ -153,14 +144,6 @@ def _resolve_accum_mode(*, seq_len: int, head_dim: int, causal: bool) -> str:
             f"Unsupported TILEDATTN_ACCUM_MODE={mode!r}. Use one of: auto, fp32, fp16."
         )
     return mode
-
-
-def _resolve_kernel_head_dim(head_dim: int) -> tuple[int, int]:
-    """The reference's padding rule (flash_fwd.py:149-163): D in {64,128} as is, else next power of two."""
-    if head_dim in _DIRECT_HEAD_DIMS:
-        return head_dim, 0
-    kernel_head_dim = 1 << (head_dim - 1).bit_length()
-    return kernel_head_dim, kernel_head_dim - head_dim
 
 
 def _resolve_kernel_head_dim_gfx950(head_dim: int) -> tuple[int, int]:
@@ -206,40 +189,22 @@ def _resolve_chunk_plan(head_dim: int) -> tuple[tuple[int, int], ...] | None:
     return tuple(plan)
 
 
-def _should_use_aligned_noncausal_fastpath(
-    *,
-    seq_len: int,
-    head_dim: int,
-    causal: bool,
-    pad_dim: int,
-    chunk_plan: tuple[tuple[int, int], ...] | None,
-    tile_m: int,
-    tile_n: int,
-) -> bool:
-    """The reference's unmasked-variant predicate (flash_fwd.py:199-238)."""
-    if os.getenv("TILEDATTN_DISABLE_ALIGNED_FASTPATH", "").strip() not in {"", "0", "false", "False"}:
-        return False
-    if causal:
-        return False
-    if chunk_plan is not None:
-        return False
-    if pad_dim != 0:
-        return False
-    if head_dim not in _ALIGNED_FASTPATH_HEAD_DIMS:
-        return False
-    min_seq = _ALIGNED_FASTPATH_MIN_SEQ_BY_HEAD_DIM.get(head_dim, 2048)
-    if seq_len < min_seq:
-        return False
-    return (seq_len % tile_m == 0) and (seq_len % tile_n == 0)
+def _aligned_fastpath_disabled() -> bool:
+    """``TILEDATTN_DISABLE_ALIGNED_FASTPATH`` as flash_fwd.py:225-226 reads it: any value
+    other than unset, "", "0", "false" or "False" disables the fast path."""
+    return os.getenv("TILEDATTN_DISABLE_ALIGNED_FASTPATH", "").strip() not in {"", "0", "false", "False"}
 
 
-def _default_tile_config_for_shape(*, seq_len: int, head_dim: int, causal: bool) -> tuple[int, int]:
-    """The reference's GB10-tuned default (flash_fwd.py:241-259), kept for API compatibility."""
-    tile_m = _DEFAULT_TM
-    tile_n = _DEFAULT_TN
-    if (not causal) and head_dim == 128 and seq_len >= 2048:
-        tile_n = 128
-    return tile_m, tile_n
+def _use_unmasked_tail_kernel(*, seq_len: int, tile_m: int, tile_n: int) -> bool:
+    """The aligned fast path on gfx950: the kernel variant without tail masking, taken when
+    every tile is whole (S a multiple of both tile sizes) unless the knob disables it.  The
+    reference's predicate (flash_fwd.py:199-238) also requires non-causal, D in {64, 128},
+    S >= 1024 (D = 64) / 2048 (D = 128) and no padding or chunk plan: its unmasked kernel has
+    no causal mask and the thresholds are its GB10 tuning.  Here causal masking is separate
+    from tail masking, and the two variants give the same result on such S."""
+    if _aligned_fastpath_disabled():
+        return False
+    return seq_len % tile_m == 0 and seq_len % tile_n == 0
 
 
 def _default_tile_config_for_shape_gfx950(*, seq_len: int, head_dim: int, causal: bool) -> tuple[int, int]:
@@ -392,14 +357,30 @@ def _kernel_ready(torch_mod, t, width: int, pad_dim: int):
     rows at a 16-byte aligned address (a fresh dense copy otherwise)."""
     if pad_dim > 0:
         return torch_mod.nn.functional.pad(t, (0, pad_dim)).contiguous()
-    if _strides_ok(t.stride(), t.shape[3], width) and t.data_ptr() % 16 == 0:
+    if _strides_ok(t.stride(), t.shape, width) and t.data_ptr() % 16 == 0:
         return t
     # contiguous() returns a dense but misaligned view unchanged; a clone is a new block
     return t.clone(memory_format=torch_mod.contiguous_format)
 
 
-def _strides_ok(stride, head_dim: int, width: int) -> bool:
-    return stride[3] == 1 and all(x % 8 == 0 for x in stride[:3]) and head_dim == width
+# The kernels address a (b, h) slice, and the 128 rows of one tile step, with 32-bit buffer
+# offsets: a row stride below 2^23 elements keeps 128 rows below 2^31 bytes, and a slice
+# must stay below 2^31 bytes (the same bounds the C ABI enforces).
+_ROW_STRIDE_LIMIT = 1 << 23
+_SLICE_BYTES_LIMIT = 1 << 31
+
+
+def _strides_ok(stride, shape, width: int) -> bool:
+    """Whether the kernels can read a [B, H, S, D] view with these element strides in place:
+    unit last stride; the others non-negative multiples of 8 (16-byte rows); rows that do
+    not overlap (row stride at least the width read; a zero row stride, as ``expand`` along
+    S gives, would make a slice's buffer range empty and read zeros); and the 32-bit buffer
+    ranges above.  Anything else is copied to a dense tensor first, as the reference copies
+    every input (flash_fwd.py:865-867)."""
+    seq_len, head_dim = int(shape[2]), int(shape[3])
+    row = int(stride[2])
+    return (stride[3] == 1 and all(x >= 0 and x % 8 == 0 for x in stride[:3]) and head_dim == width
+            and width <= row < _ROW_STRIDE_LIMIT and seq_len * row * 2 < _SLICE_BYTES_LIMIT)
 
 
 # Knobs this module reads, re-read on every call as in the reference.  A launch plan is
@@ -443,15 +424,27 @@ def _raw_stream(torch_mod, device_index: int) -> int:
     return int(torch_mod.cuda.current_stream(device_index).cuda_stream)
 
 
-def _build_plan(torch_mod, lib, q, k, v, causal: bool) -> _LaunchPlan:
-    """Resolve knobs and policies for a call (flash_fwd.py:821-969), up to the launch."""
+def _build_plan(torch_mod, lib, q, k, v, causal: bool, tile: tuple[int, int] | None = None,
+                accum: str | None = None) -> _LaunchPlan:
+    """Resolve knobs and policies for a call (flash_fwd.py:821-969), up to the launch.
+    ``tile`` / ``accum`` ('fp32' | 'fp16'), when given, take the place of the
+    ``TILEDATTN_TILE_M/N`` and ``TILEDATTN_ACCUM_MODE`` knobs (the operator's arguments)."""
     opt_level, occupancy, num_ctas = _resolve_kernel_options()
     sync_mode = _resolve_sync_mode()
 
     batch, heads, seq_len, head_dim = map(int, q.shape)
-    accum_mode = _resolve_accum_mode(seq_len=seq_len, head_dim=head_dim, causal=causal)
+    if accum is not None:
+        if accum not in ("fp32", "fp16"):
+            raise ValueError(f"Unsupported accumulation mode {accum!r}. Use fp32 or fp16.")
+        accum_mode = accum
+    else:
+        accum_mode = _resolve_accum_mode(seq_len=seq_len, head_dim=head_dim, causal=causal)
     bh = batch * heads
-    if os.getenv("TILEDATTN_TILE_M") or os.getenv("TILEDATTN_TILE_N"):
+    explicit_tile = tile is not None or bool(os.getenv("TILEDATTN_TILE_M") or os.getenv("TILEDATTN_TILE_N"))
+    if tile is not None:
+        tile_m, tile_n = int(tile[0]), int(tile[1])
+        _check_tile_supported(tile_m, tile_n)
+    elif explicit_tile:
         tile_m, tile_n = _resolve_tile_config()
         _check_tile_supported(tile_m, tile_n)
     else:
@@ -462,7 +455,7 @@ def _build_plan(torch_mod, lib, q, k, v, causal: bool) -> _LaunchPlan:
     chunk_plan = _resolve_chunk_plan(head_dim)
     kernel_head_dim, pad_dim = _resolve_kernel_head_dim_gfx950(head_dim)
     if kernel_head_dim > 128 and tile_n != _WIDE_HEAD_DIM_TILE_N:
-        if os.getenv("TILEDATTN_TILE_M") or os.getenv("TILEDATTN_TILE_N"):
+        if explicit_tile:
             raise ValueError(
                 f"TILEDATTN_TILE_N={tile_n} is not supported for head dimension D={head_dim} "
                 f"on gfx950: head dims above 128 run with TILE_N=64."
@@ -490,22 +483,13 @@ def _build_plan(torch_mod, lib, q, k, v, causal: bool) -> _LaunchPlan:
     if plan.empty:
         return plan
 
-    use_aligned_fastpath = _should_use_aligned_noncausal_fastpath(
-        seq_len=seq_len,
-        head_dim=head_dim,
-        causal=causal,
-        pad_dim=pad_dim,
-        chunk_plan=chunk_plan,
-        tile_m=tile_m,
-        tile_n=tile_n,
-    )
+    aligned = int(_use_unmasked_tail_kernel(seq_len=seq_len, tile_m=tile_m, tile_n=tile_n))
     if chunk_plan is not None:
         kernel_variant = "chunked"
-    elif use_aligned_fastpath:
-        kernel_variant = "direct_aligned_noncausal"
+    elif aligned:
+        kernel_variant = "direct_aligned"
     else:
         kernel_variant = "direct"
-    aligned = int(seq_len % tile_m == 0 and seq_len % tile_n == 0)
     device_index = q.device.index if q.device.index is not None else torch_mod.cuda.current_device()
     plan.device_index = device_index
 
@@ -528,12 +512,13 @@ def _build_plan(torch_mod, lib, q, k, v, causal: bool) -> _LaunchPlan:
 
     # Which inputs the kernel cannot read in place (host padding or strides); addresses are
     # checked per call.
-    plan.copy = tuple(plan.pad_dim > 0 or not _strides_ok(t.stride(), head_dim, width)
+    plan.copy = tuple(plan.pad_dim > 0 or not _strides_ok(t.stride(), t.shape, width)
                       for t in (q, k, v))
     n_qblk = (seq_len + tile_m - 1) // tile_m
     args = _lib.FwdArgs()
     args.B, args.H, args.S, args.D = batch, heads, seq_len, kernel_head_dim
     args.d_real = head_dim if pad_in_kernel else 0
+    args.aligned = aligned
     contiguous = (heads * seq_len * width, seq_len * width, width, 1)
     for name, t, cp in (("q_stride", q, plan.copy[0]), ("k_stride", k, plan.copy[1]),
                         ("v_stride", v, plan.copy[2])):
@@ -569,6 +554,8 @@ def run_flash_fwd(
     *,
     causal: bool,
     scale: float,
+    tile: tuple[int, int] | None = None,
+    accum: str | None = None,
 ):
     """Run the gfx950 SDPA forward on validated [B,H,S,D] fp16/bf16 tensors; returns o.
 
@@ -579,12 +566,17 @@ def run_flash_fwd(
     transposed view or per-call copy is made unless the inputs' strides require one.  The
     resolution is cached per configuration and knob values (``_build_plan``); a call then
     allocates the output, fills the tensor addresses and scale, and launches.
+
+    ``tile`` (TILE_M, TILE_N) and ``accum`` ('fp32' | 'fp16'), when given, override the
+    corresponding knobs (the custom operator passes its arguments this way); ``sdpa`` leaves
+    them unset, as the reference's call does.
     """
     torch_mod = _runtime.get_torch_module()
-    key = (q.shape, q.stride(), k.stride(), v.stride(), q.dtype, q.device, causal, _knob_snapshot())
+    key = (q.shape, q.stride(), k.stride(), v.stride(), q.dtype, q.device, causal, _knob_snapshot(),
+           tile, accum)
     plan = _PLANS.get(key)
     if plan is None or plan.generation != _compile_cache.generation():
-        plan = _build_plan(torch_mod, _runtime.get_native_library(), q, k, v, causal)
+        plan = _build_plan(torch_mod, _runtime.get_native_library(), q, k, v, causal, tile, accum)
         if len(_PLANS) >= _PLANS_MAX:
             _PLANS.clear()
         _PLANS[key] = plan

@@ -11,7 +11,7 @@ Same checks in the same order as the reference (src/tiledattention/sdpa.py:14-48
 5. ``run_flash_fwd``, looked up in this module's namespace at call time so tests can
    replace it.
 
-Unlike the reference, this module is itself callable: importing ``tiledattention_amd.sdpa``
+Unlike the reference, this module is itself callable: importing ``tiledattention.sdpa``
 as a submodule rebinds the package attribute ``sdpa`` from the function to this module
 (Python's import system sets the attribute on the parent package), and in the reference
 that leaves ``tiledattention.sdpa`` uncallable after the first call.  Making the module
@@ -49,6 +49,12 @@ def sdpa(
     Returns:
         o, [B, H, S, D] in the input dtype.
     """
+    return _sdpa_checked(q, k, v, causal=causal, scale=scale)
+
+
+def _sdpa_checked(q, k, v, *, causal, scale, **overrides):
+    """``sdpa``'s checks and launch; ``overrides`` (``tile``, ``accum``) reach
+    ``run_flash_fwd`` only when given, so ``sdpa`` calls it exactly as the reference does."""
     if not isinstance(causal, bool):
         raise InvalidShapeError("causal must be a bool.")
     if scale is not None and (not isinstance(scale, Real) or float(scale) <= 0):
@@ -60,7 +66,7 @@ def sdpa(
 
     head_dim = int(q.shape[-1])
     resolved_scale = float(scale) if scale is not None else 1.0 / math.sqrt(head_dim)
-    return run_flash_fwd(q, k, v, causal=causal, scale=resolved_scale)
+    return run_flash_fwd(q, k, v, causal=causal, scale=resolved_scale, **overrides)
 
 
 class _CallableModule(types.ModuleType):

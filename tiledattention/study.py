@@ -24,7 +24,7 @@ fused backends (flash, efficient), because PyTorch's bf16 math path issues batch
 with a transposed operand that have faulted these GPUs; the eager baseline makes Kᵀ
 contiguous for the same reason.  No figures are drawn (matplotlib is not a dependency).
 
-Run: ``python -m tiledattention_amd.study --out DIR [--seqs ...] [--dims ...]``.
+Run: ``python -m tiledattention.study --out DIR [--seqs ...] [--dims ...]``.
 """
 
 from __future__ import annotations
@@ -362,7 +362,7 @@ def collect_repro_info() -> dict[str, str]:
         info["hipcc"] = "Unavailable in PATH"
     from . import __version__
 
-    info["tiledattention_amd"] = __version__
+    info["tiledattention"] = __version__
     info["flashattention"] = "installed" if _flash_attn_func() is not None else \
         "Not installed (baseline used: torch SDPA)"
     info["host"] = f"{platform.machine()} {platform.system()} {platform.release()}"

@@ -1,47 +1,30 @@
-"""MI355X-native SDPA forward with the public API of TiledAttention.
+"""Native side of the MI355X SDPA forward: the gfx950 HIP kernels and the C-ABI library.
 
-``sdpa(q, k, v, *, causal=False, scale=None) -> o`` on [B, H, S, D] fp16/bf16 tensors,
-backed by hand-written gfx950 HIP kernels behind a C ABI (``include/tiledattn.h``).
-The names exported here match ``src/tiledattention/__init__.py:47-55`` of the reference.
+* ``csrc/`` holds the sources (kernels, the ``include/tiledattn.h`` implementation) and the
+  build recipe, ``python -m tiledattention_amd.csrc.build``;
+* ``lib/`` receives what that recipe builds: ``libtiledattn.so`` and the ``.hsaco`` code
+  objects it loads.
+
+The Python API lives in the ``tiledattention`` package, under the reference's module path
+(``src/tiledattention/__init__.py:20-55``); it loads this package's library through
+``tiledattention._lib``.  Importing ``tiledattention_amd`` re-exports that API unchanged
+(the same function and exception objects), for callers written against the earlier name.
 """
 
 from __future__ import annotations
 
-from typing import TYPE_CHECKING
+from pathlib import Path
 
-from ._errors import (
+from tiledattention import (  # noqa: F401  (re-exported)
     DependencyError,
     DTypeNotSupportedError,
     InvalidShapeError,
     TiledAttentionError,
     UnsupportedPlatformError,
+    __all__,
+    __version__,
+    sdpa,
 )
-from ._version import __version__
 
-if TYPE_CHECKING:
-    import torch
-
-
-def sdpa(
-    q: torch.Tensor,
-    k: torch.Tensor,
-    v: torch.Tensor,
-    *,
-    causal: bool = False,
-    scale: float | None = None,
-) -> torch.Tensor:
-    """Scaled dot-product attention forward; see ``tiledattention_amd.sdpa.sdpa``."""
-    from .sdpa import sdpa as _sdpa
-
-    return _sdpa(q, k, v, causal=causal, scale=scale)
-
-
-__all__ = [
-    "__version__",
-    "sdpa",
-    "TiledAttentionError",
-    "UnsupportedPlatformError",
-    "InvalidShapeError",
-    "DTypeNotSupportedError",
-    "DependencyError",
-]
+CSRC_DIR = Path(__file__).resolve().parent / "csrc"
+LIB_DIR = Path(__file__).resolve().parent / "lib"

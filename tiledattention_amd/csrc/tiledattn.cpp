@@ -343,23 +343,33 @@ ta_status validate_args(const ta_fwd_args* a, int64_t* n_bh_out, int64_t* n_qblk
     return fail(TA_EINVAL, "q/k/v/o must be 16-byte aligned");
   const int64_t* st[4] = {a->q_stride, a->k_stride, a->v_stride, a->o_stride};
   const char* nm[4] = {"q", "k", "v", "o"};
+  // Rows are read (and o written) as whole rows of the head dim actually present; a row
+  // stride below that width makes rows overlap, and a zero one (a tensor expanded along S)
+  // would give every buffer resource below a size of zero, so its loads would read zeros.
+  const int64_t width = a->d_real ? a->d_real : a->D;
   for (int i = 0; i < 4; ++i) {
     if (st[i][3] != 1) return fail(TA_EINVAL, "%s: last-dim stride must be 1", nm[i]);
     for (int j = 0; j < 3; ++j)
       if (st[i][j] < 0 || (st[i][j] & 7) != 0)
         return fail(TA_EINVAL, "%s: stride[%d]=%lld must be a non-negative multiple of 8", nm[i], j,
                     (long long)st[i][j]);
+    if (st[i][2] < width)
+      return fail(TA_EINVAL, "%s: row stride %lld is below the row width %lld (rows overlap)",
+                  nm[i], (long long)st[i][2], (long long)width);
+    // Bounded first, so that the products below cannot overflow (S < 2^31).
+    if (st[i][2] >= (1LL << 23))
+      return fail(TA_EINVAL, "%s: row stride %lld must stay below 2^23 elements", nm[i],
+                  (long long)st[i][2]);
   }
   // K and V are read with buffer instructions whose byte range is 32-bit: a (b, h) slice,
-  // and the 128 rows one tile step addresses, must stay below 2^31 bytes.
+  // and the 128 rows one tile step addresses (below 2^31 by the bound above), must stay
+  // below 2^31 bytes.
   if (a->S * a->k_stride[2] * 2 > 0x7fffffffLL || a->S * a->v_stride[2] * 2 > 0x7fffffffLL)
     return fail(TA_EINVAL, "k/v: S * row stride must stay below 2^31 bytes per (b, h) slice");
-  if (a->k_stride[2] * 2 * 128 >= 0x80000000LL || a->v_stride[2] * 2 * 128 >= 0x80000000LL)
-    return fail(TA_EINVAL, "k/v: 128 * row stride must stay below 2^31 bytes");
   // The eight-wave kernel stages Q the same way (one buffer resource per query block).
-  if (eight_wave(a->tile_m, a->tile_n, a->accum, a->D) &&
-      (a->S * a->q_stride[2] * 2 > 0x7fffffffLL || a->q_stride[2] * 2 * 128 >= 0x80000000LL))
+  if (eight_wave(a->tile_m, a->tile_n, a->accum, a->D) && a->S * a->q_stride[2] * 2 > 0x7fffffffLL)
     return fail(TA_EINVAL, "q: S * row stride must stay below 2^31 bytes per (b, h) slice");
+  if (a->aligned != 0 && a->aligned != 1) return fail(TA_EINVAL, "aligned %d", a->aligned);
   *n_qblk_out = n_qblk;
   return TA_OK;
 }
@@ -381,6 +391,13 @@ void fill_params(const ta_fwd_args* a, int64_t n_bh, int64_t n_qblk, ta::FwdPara
   p->scale_log2 = static_cast<float>(static_cast<double>(a->scale) * 1.4426950408889634);
   p->sched = a->sched;
   p->d_real = a->d_real ? a->d_real : static_cast<int32_t>(a->D);
+}
+
+// Whether a launch runs the kernel variant without tail masking: the caller allows it
+// (args->aligned, the aligned fast-path decision, flash_fwd.py:199-238) and every tile is
+// whole (S a multiple of both tile sizes).
+bool unmasked_tail(const ta_fwd_args* a) {
+  return a->aligned == 1 && a->S % a->tile_m == 0 && a->S % a->tile_n == 0;
 }
 
 // Whether the split path exists for this configuration (the eight-wave kernel).
@@ -445,7 +462,7 @@ ta_status ta_sdpa_fwd(const ta_fwd_args* a, void* stream) {
   ta_status vst = validate_args(a, &n_bh, &n_qblk);
   if (vst != TA_OK || n_qblk == 0) return vst;
 
-  const bool aligned = (a->S % a->tile_m == 0) && (a->S % a->tile_n == 0);
+  const bool aligned = unmasked_tail(a);
   const KernelId id =
       kernel_id(a->dtype, (int)a->D, a->tile_m, a->tile_n, a->causal, !aligned, a->accum);
   ta_status gst = check_grid(n_bh * n_qblk, id.block, "kernel");
@@ -547,7 +564,7 @@ ta_status ta_sdpa_fwd_split(const ta_fwd_args* a, int32_t chunk_steps, void* wor
   if (gst == TA_OK) gst = check_grid(merge_wgs, merge_block, "merge kernel");
   if (gst != TA_OK) return gst;
 
-  const bool aligned = (a->S % a->tile_m == 0) && (a->S % a->tile_n == 0);
+  const bool aligned = unmasked_tail(a);
   const char* dt = a->dtype == TA_BF16 ? "bf16" : "f16";
   char name[96];
   snprintf(name, sizeof(name), "ta_fwd_pp_split_%s_d%d_c%d_t%d", dt, (int)a->D, a->causal ? 1 : 0,
