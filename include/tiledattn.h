@@ -139,6 +139,20 @@ ta_status ta_split_workspace_size(const ta_fwd_args* args, int32_t chunk_steps, 
 ta_status ta_sdpa_fwd_split(const ta_fwd_args* args, int32_t chunk_steps, void* workspace,
                             int64_t workspace_bytes, void* stream);
 
+/* Bytes of the static split workspace of ta_sdpa_fwd_split_static, per device. */
+#define TA_STATIC_SCRATCH_BYTES (64LL << 20)
+
+/* ta_sdpa_fwd_split with the workspace in a static device array of
+ * TA_STATIC_SCRATCH_BYTES held by each GPU the library runs on, so that the call allocates
+ * no device memory.  No counterpart in the reference: it is for callers that cannot call
+ * hipMalloc (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation).  Same arguments, kernels and result as ta_sdpa_fwd_split; a chunk length
+ * whose workspace (ta_split_workspace_size) exceeds TA_STATIC_SCRATCH_BYTES is rejected
+ * with TA_EINVAL.  Every call on one GPU shares that GPU's array: calls whose work overlaps
+ * on the same GPU (other streams, other threads) race on it and must be serialized by the
+ * caller. */
+ta_status ta_sdpa_fwd_split_static(const ta_fwd_args* args, int32_t chunk_steps, void* stream);
+
 /* Unload every cached module on every device (compile_cache.reset_cache_for_tests). */
 ta_status ta_cache_reset(void);
 

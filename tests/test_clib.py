@@ -207,3 +207,18 @@ def test_kernel_symbol_names_exist_in_code_objects(tiles, accum):
                                                 accum=accum)
                     data = (_lib.lib_dir() / f).read_bytes()
                     assert sym.encode() + b"\x00" in data, (f, sym)
+
+
+def test_static_scratch_entry_rejects_oversize_before_any_device_call(lib):
+    """ta_sdpa_fwd_split_static checks the workspace against its static array first: B1 H64
+    S=16384 D=128 causal in one-step chunks needs gigabytes of partials."""
+    st = (64 * 16384 * 128, 16384 * 128, 128, 1)
+    a = _args(B=1, H=64, S=16384, D=128, tile_m=128, tile_n=64, causal=1,
+              q_stride=st, k_stride=st, v_stride=st, o_stride=st)
+    need = ctypes.c_int64(0)
+    assert lib.ta_split_workspace_size(ctypes.byref(a), 1, ctypes.byref(need)) == _lib.TA_OK
+    assert need.value > _lib.STATIC_SCRATCH_BYTES
+    assert lib.ta_sdpa_fwd_split_static(ctypes.byref(a), 1, None) == _lib.TA_EINVAL
+    assert "exceeds the static scratch of 67108864 bytes" in _lib.last_error(lib)
+    assert lib.ta_sdpa_fwd_split_static(None, 1, None) == _lib.TA_EINVAL
+    assert lib.ta_sdpa_fwd_split_static(ctypes.byref(_args(D=96)), 1, None) == _lib.TA_EUNSUPPORTED

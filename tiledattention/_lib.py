@@ -31,6 +31,7 @@ TA_ACC_FP32 = 0
 TA_ACC_INPUT = 1
 
 TILE_SHAPES = ((64, 64), (64, 128), (128, 64), (128, 128))
+STATIC_SCRATCH_BYTES = 64 << 20  # TA_STATIC_SCRATCH_BYTES
 
 
 def kernel_symbol(*, dtype: int, head_dim: int, tile_m: int, tile_n: int, causal: bool,
@@ -59,6 +60,7 @@ EXPORTED_SYMBOLS = (
     "ta_split_plan_model",
     "ta_split_workspace_size",
     "ta_sdpa_fwd_split",
+    "ta_sdpa_fwd_split_static",
     "ta_cache_reset",
     "ta_cache_size",
     "ta_last_error",
@@ -142,6 +144,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ta_sdpa_fwd_split.argtypes = [ctypes.POINTER(FwdArgs), i32, ctypes.c_void_p, ctypes.c_int64,
                                       ctypes.c_void_p]
     lib.ta_sdpa_fwd_split.restype = i32
+    lib.ta_sdpa_fwd_split_static.argtypes = [ctypes.POINTER(FwdArgs), i32, ctypes.c_void_p]
+    lib.ta_sdpa_fwd_split_static.restype = i32
     lib.ta_cache_reset.argtypes = []
     lib.ta_cache_reset.restype = i32
     lib.ta_cache_size.argtypes = []

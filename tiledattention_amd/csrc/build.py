@@ -7,7 +7,9 @@ Outputs (into ``tiledattention_amd/lib/`` unless told otherwise):
   ``attn_fwd.hip`` with ``hipcc --genco --offload-arch=gfx950``;
 * ``attn_fwd_pp.hsaco``: the eight-wave kernels (dtype x head dim x causal x tail) that
   serve the (128, 64) tile shape with fp32 accumulation, from ``attn_fwd_pp.hip``;
-* ``libtiledattn.so``: the host library implementing ``include/tiledattn.h``.
+* ``libtiledattn.so``: the host library implementing ``include/tiledattn.h``, linked from
+  ``tiledattn.cpp`` (g++) and ``tiledattn_static.hip`` (hipcc; the static device scratch of
+  ``ta_sdpa_fwd_split_static``).
 
 Run as ``python -m tiledattention_amd.csrc.build``.
 """
@@ -19,6 +21,7 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
 from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
@@ -79,7 +82,12 @@ def pp_code_object_cmd(out_dir: Path) -> list[str]:
     ]
 
 
-def library_cmd(out_dir: Path) -> list[str]:
+def static_object_cmd(obj: Path) -> list[str]:
+    """The library's HIP translation unit (a device array, no kernels) as a PIC object."""
+    return [_hipcc(), *HIP_FLAGS, "-fPIC", "-Wall", "-c", "-o", str(obj), str(HERE / "tiledattn_static.hip")]
+
+
+def library_cmd(out_dir: Path, static_obj: Path) -> list[str]:
     return [
         os.environ.get("CXX", "g++"),
         "-O2",
@@ -93,11 +101,20 @@ def library_cmd(out_dir: Path) -> list[str]:
         "-o",
         str(out_dir / "libtiledattn.so"),
         str(HERE / "tiledattn.cpp"),
+        str(static_obj),
         f"-L{ROCM / 'lib'}",
         f"-Wl,-rpath,{ROCM / 'lib'}",
+        "-Wl,--no-undefined",
         "-lamdhip64",
         "-ldl",
     ]
+
+
+def _build_library(out_dir: Path) -> None:
+    with tempfile.TemporaryDirectory(prefix="tiledattn_build_") as tmp:
+        obj = Path(tmp) / "tiledattn_static.o"
+        _run(static_object_cmd(obj))
+        _run(library_cmd(out_dir, obj))
 
 
 def build(out_dir: Path | None = None, jobs: int | None = None) -> Path:
@@ -105,10 +122,11 @@ def build(out_dir: Path | None = None, jobs: int | None = None) -> Path:
     out = Path(out_dir) if out_dir is not None else LIB_DIR
     out.mkdir(parents=True, exist_ok=True)
     cmds = [code_object_cmd(tm, tn, out) for tm, tn in TILES]
-    cmds += [pp_code_object_cmd(out), library_cmd(out)]
-    workers = jobs or min(len(cmds), max(1, (os.cpu_count() or 2)))
+    cmds += [pp_code_object_cmd(out)]
+    workers = jobs or min(len(cmds) + 1, max(1, (os.cpu_count() or 2)))
     with cf.ThreadPoolExecutor(max_workers=workers) as pool:
-        for fut in [pool.submit(_run, c) for c in cmds]:
+        futs = [pool.submit(_run, c) for c in cmds] + [pool.submit(_build_library, out)]
+        for fut in futs:
             fut.result()
     return out
 

@@ -409,6 +409,12 @@ bool split_capable(const ta_fwd_args* a) {
 
 extern "C" {
 
+// Error channel for the library's other translation unit (tiledattn_static.hip): records
+// `msg` for ta_last_error() on this thread and returns `st`.
+__attribute__((visibility("hidden"))) ta_status ta_internal_fail(ta_status st, const char* msg) {
+  return fail(st, "%s", msg);
+}
+
 int ta_abi_version(void) { return TA_ABI_VERSION; }
 
 const char* ta_last_error(void) { return g_last_error.c_str(); }
