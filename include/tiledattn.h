@@ -73,8 +73,11 @@ typedef struct ta_fwd_args {
   int32_t tile_n;  /* keys per tile: 64 or 128 (TILEDATTN_TILE_N) */
   int32_t accum;   /* ta_accum */
   int32_t device;  /* HIP device ordinal the pointers and stream belong to */
-  int32_t sched;   /* workgroup -> tile order: 0 plain, 1 XCD-grouped, 2 XCD-grouped with
-                      causal heavy/light complementary order */
+  int32_t sched;   /* workgroup -> tile order: 0 plain, 1 XCD-grouped (causal grids of two
+                      or more workgroups per CU on tiles (128, 64) / (128, 128) with fp32
+                      accumulation then run query blocks in pairs nq - 1 - j and j, one
+                      workgroup each), 2 XCD-grouped with causal heavy/light complementary
+                      order, 3 as 1 with pairs whatever the grid size */
   int32_t d_real;  /* 0, or the head-dim columns q/k/v/o actually have (a multiple of 8 below
                       D): the kernel for D reads the missing columns as zero and does not
                       write them, so a narrower head dim needs no padded copies (the

@@ -3,7 +3,8 @@
 // both issue orders, the items must cover every key step of every (b, h, query block)
 // exactly once, partial slots must be unique, in range and used exactly by the blocks of
 // more than one chunk, and the merge grid must name exactly those blocks with their
-// chunks' slots in key order.  Prints "ok <cases>" or the first failure.
+// chunks' slots in key order; the pair grid must cover every query block exactly once with
+// nq + 1 key steps an item.  Prints "ok <cases>" or the first failure.
 #include <algorithm>
 #include <cstdio>
 #include <map>
@@ -107,6 +108,31 @@ static void check_case(int S, int n_bh, bool causal, int c, int sched) {
   CHECK(merged.size() == split_blocks.size(), "S=%d c=%d merged %zu of %zu", S, c, merged.size(), split_blocks.size());
 }
 
+// Pair grid: every (b, h, query block) exactly once over the first and second blocks of
+// all items, the first block the heavier one, and every item nq + 1 key steps (the middle
+// block of an odd nq alone).
+static void check_pairs(int S, int n_bh, int sched) {
+  const int nq = (S + ta::kPPRows - 1) / ta::kPPRows;
+  const int np = (nq + 1) / 2;
+  std::set<std::pair<int, int>> seen;
+  for (int blk = 0; blk < n_bh * np; ++blk) {
+    ta::WorkItem a, b;
+    ta::pair_items(blk, n_bh, nq, sched, &a, &b);
+    CHECK(a.bh >= 0 && a.bh < n_bh && a.bh == b.bh, "pair bh %d %d", a.bh, b.bh);
+    CHECK(a.qt >= 0 && a.qt < nq, "pair a.qt %d", a.qt);
+    CHECK(seen.insert({a.bh, a.qt}).second, "S=%d block (%d, %d) twice", S, a.bh, a.qt);
+    if (b.qt >= 0) {
+      CHECK(b.qt < a.qt, "second block %d not lighter than %d", b.qt, a.qt);
+      CHECK(seen.insert({b.bh, b.qt}).second, "S=%d block (%d, %d) twice", S, b.bh, b.qt);
+      CHECK(a.qt + 1 + b.qt + 1 == nq + 1, "pair steps %d + %d", a.qt + 1, b.qt + 1);
+    } else {
+      CHECK(nq % 2 == 1 && a.qt == nq / 2, "single item qt %d of nq %d", a.qt, nq);
+    }
+    CHECK(a.t_beg == 0 && a.t_end == -1 && a.slot == -1 && b.t_beg == 0 && b.slot == -1, "pair ranges");
+  }
+  CHECK((int)seen.size() == n_bh * nq, "S=%d n_bh=%d pairs cover %zu of %d", S, n_bh, seen.size(), n_bh * nq);
+}
+
 int main() {
   int cases = 0;
   const int seqs[] = {1, 100, 128, 129, 255, 256, 300, 1000, 1024, 2048, 2100, 4096, 8192, 16384};
@@ -121,6 +147,17 @@ int main() {
             ++cases;
           }
         }
+  for (int S : seqs)
+    for (int n_bh : bhs)
+      for (int sched = 0; sched < 4; ++sched) {
+        if (S > 128) check_pairs(S, n_bh, sched);
+        ++cases;
+      }
+  for (int n_bh = 1; n_bh <= 40; ++n_bh)
+    for (int nq = 2; nq <= 70; ++nq) {
+      check_pairs(nq * 128 - 5, n_bh, 1);
+      ++cases;
+    }
   if (fails) {
     printf("%d failures\n", fails);
     return 1;

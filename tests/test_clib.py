@@ -72,7 +72,7 @@ def _call(lib, a):
     (dict(dtype=2), _lib.TA_EINVAL, "dtype"),
     (dict(accum=5), _lib.TA_EINVAL, "accum"),
     (dict(causal=2), _lib.TA_EINVAL, "causal"),
-    (dict(sched=3), _lib.TA_EINVAL, "sched"),
+    (dict(sched=4), _lib.TA_EINVAL, "sched"),
     (dict(S=-1), _lib.TA_EINVAL, "negative"),
     (dict(D=96), _lib.TA_EUNSUPPORTED, "head_dim"),
     (dict(D=160, tile_n=128), _lib.TA_EUNSUPPORTED, "tile_n 128 with head_dim 160"),

@@ -239,5 +239,8 @@ def test_sched_env(monkeypatch):
     monkeypatch.setenv("TILEDATTN_SCHED", "0")
     assert ff._resolve_sched(n_blocks=512, causal=True, tile_m=128, tile_n=64) == 0
     monkeypatch.setenv("TILEDATTN_SCHED", "3")
-    with pytest.raises(ValueError, match="TILEDATTN_SCHED"):
-        ff._resolve_sched(n_blocks=512, causal=True, tile_m=128, tile_n=64)
+    assert ff._resolve_sched(n_blocks=512, causal=True, tile_m=128, tile_n=64) == 3
+    for bad in ("4", "-1", "x"):
+        monkeypatch.setenv("TILEDATTN_SCHED", bad)
+        with pytest.raises(ValueError, match="TILEDATTN_SCHED"):
+            ff._resolve_sched(n_blocks=512, causal=True, tile_m=128, tile_n=64)

@@ -37,8 +37,10 @@ Environment knobs are re-read on every call, as in the reference:
     unchunked one, so here it runs the kernel that serves the head dim unchunked (96 on the
     D = 128 kernel with in-kernel padding, 160 on the native D = 160 kernel).
 ``TILEDATTN_SCHED`` (this build only)
-    Workgroup-to-tile order: ``0`` plain, ``1`` XCD-grouped, ``2`` XCD-grouped with causal
-    heavy/light complementary order; default: see ``_resolve_sched``.
+    Workgroup-to-tile order: ``0`` plain, ``1`` XCD-grouped (large causal grids on the
+    eight-wave kernel run query blocks in pairs, see ``ta_fwd_args.sched``), ``2``
+    XCD-grouped with causal heavy/light complementary order, ``3`` pairs whatever the grid
+    size; default: see ``_resolve_sched``.
 ``TILEDATTN_SPLIT`` (this build only)
     Split key ranges (``ta_sdpa_fwd_split``): ``auto`` (default) asks the library's
     dispatch model (``ta_split_plan``), ``0``/``off`` never splits, a positive integer
@@ -264,8 +266,8 @@ def _resolve_sched(*, n_blocks: int, causal: bool, tile_m: int, tile_n: int,
         resident = _CU_COUNT * _workgroups_per_cu(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code,
                                                   head_dim=head_dim, causal=causal)
         return 2 if causal and n_blocks <= resident else 1
-    if raw not in {"0", "1", "2"}:
-        raise ValueError(f"Unsupported TILEDATTN_SCHED={raw!r}. Use 0, 1 or 2.")
+    if raw not in {"0", "1", "2", "3"}:
+        raise ValueError(f"Unsupported TILEDATTN_SCHED={raw!r}. Use 0, 1, 2 or 3.")
     return int(raw)
 
 

@@ -53,8 +53,14 @@ __device__ static inline int pp_swz_v(int row) {
   return D == 128 ? ((row & 3) << 2) : (((row >> 1) & 1) << 2);
 }
 
+// Stage size of the eight-wave kernel at head dim D: 128 key rows of 2 D bytes.
+constexpr int pp_stage_bytes(int d) { return kPPKeys * 2 * d; }
+
+// One query block (or, with SPLIT, one chunk of its key steps) on the whole workgroup: the
+// prologue, the key loop and the merge of the two key halves with the output stores.
 template <int DT, int D, bool CAUSAL, bool TAIL, bool SPLIT>
-__device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
+__device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const WorkItem wi, char* lds_k0,
+                                                  char* lds_k1, char* lds_v0, char* lds_v1) {
   constexpr int TM = 128;            // query rows per workgroup
   constexpr int TK = 128;            // keys per workgroup step (64 per wave group)
   constexpr int KB = 2;              // 32-key blocks per wave per step
@@ -84,13 +90,7 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   constexpr bool kPrioMfma = !SPLIT && D == 64 && !CAUSAL;
   using DTy = DType<DT>;
 
-  // One array per (tensor, stage): the stage of every access is a compile-time constant
-  // (the key loop is unrolled by two), so the compiler can tell the loads in flight into
-  // one stage from the reads of the other and does not wait on the former for the latter.
-  __shared__ __attribute__((aligned(1024))) char lds_k0[STAGE];
-  __shared__ __attribute__((aligned(1024))) char lds_k1[STAGE];
-  __shared__ __attribute__((aligned(1024))) char lds_v0[STAGE];
-  __shared__ __attribute__((aligned(1024))) char lds_v1[STAGE];
+  static_assert(STAGE == pp_stage_bytes(D), "stage layout");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -100,17 +100,8 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   const int l32 = lane & 31;
   const int hl = lane >> 5;
 
-  // ---- block -> (bh, q tile, key steps) -------------------------------------------
-  // One workgroup per CU (LDS and registers).  The numbering (attn_fwd_split.h) regroups
-  // block ids per XCD with sched >= 1 (one head's K/V in one L2) and issues causal tiles
-  // heaviest first, so each CU takes the next tile when its current one ends and heavy
-  // tiles pair with light ones.  Split items cover a chunk of key steps of a block and
-  // leave a partial (slot >= 0) when the block has more than one chunk.
-  const int nq = p.n_qblk;
+  // ---- the work item: (bh, q tile, key steps) -----------------------------------------
   const int S = p.S;
-  const WorkItem wi = SPLIT ? split_item(blockIdx.x, p.n_bh, p.split_items, p.sched, CAUSAL,
-                                         p.split_c, p.split_ns, p.split_slots, S)
-                            : whole_item(blockIdx.x, p.n_bh, nq, p.sched, CAUSAL);
   const int bh = wi.bh;
   const int qt = wi.qt;
   const int t_beg = wi.t_beg;
@@ -317,21 +308,37 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
         }
       }
     }
-    // P = 2^(s c - m c) packed into pk, and the sum of the rounded P: four independent
-    // partial sums so the dot2 chain is short, each started without a zeroed accumulator
-    // (four VALU ops fewer in this cluster; 0.3-2 % per call measured).
+    // P = 2^(s c - mc) packed into pk, and the sum of the rounded P.  Each kind of op runs
+    // over all 32 of the lane's scores before the next kind (FMA, exp, pack), so dependent
+    // ops sit many instructions apart (C3 -1 %); the sum uses four independent dot2 chains,
+    // each started without a zeroed accumulator (four VALU ops fewer; 0.3-2 %).
     auto make_p = [&](float mc) {
+      float x[KB][16];
+#pragma unroll
+      for (int bk = 0; bk < KB; ++bk) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x[bk][r] = __builtin_fmaf(s[bk][r], c, -mc);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int bk = 0; bk < KB; ++bk) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x[bk][r] = fast_exp2(x[bk][r]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int bk = 0; bk < KB; ++bk) {
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) pk[bk][r >> 1] = DTy::pack(x[bk][r], x[bk][r + 1]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
       float l4[4];
 #pragma unroll
       for (int bk = 0; bk < KB; ++bk) {
 #pragma unroll
         for (int r = 0; r < 16; r += 2) {
-          const float p0 = fast_exp2(__builtin_fmaf(s[bk][r], c, -mc));
-          const float p1 = fast_exp2(__builtin_fmaf(s[bk][r + 1], c, -mc));
-          const uint32_t w = DTy::pack(p0, p1);
-          pk[bk][r >> 1] = w;
           const int j = (r >> 1) & 3;
-          l4[j] = bk == 0 && r < 8 ? DTy::sum2_head(w) : DTy::sum2(w, l4[j]);
+          l4[j] = bk == 0 && r < 8 ? DTy::sum2_head(pk[bk][r >> 1]) : DTy::sum2(pk[bk][r >> 1], l4[j]);
         }
       }
       return (l4[0] + l4[1]) + (l4[2] + l4[3]);
@@ -504,9 +511,124 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   wait_dma();  // the zero-filling loads of the last two steps, before the merge reuses LDS
   barrier();
 
+  // Merge of d blocks [LO, LO + DB/2) of this wave's row block with the partner wave's
+  // (same rows, the other key half).  Exchange regions: group 0's waves send from lds_k0,
+  // group 1's from lds_k1 (DB/2 blocks x 16 floats x 64 lanes each, laid out as 16-byte
+  // chunks [block][g][lane]: conflict-free 16-byte writes and reads), (m, l) at the start
+  // of lds_v0; the merged tile is staged in lds_v1 for row-contiguous stores.
+  auto merge_half = [&](auto lo_tag) {
+    constexpr int LO = decltype(lo_tag)::value;
+    constexpr int NB = DB / 2;
+    constexpr int RGN = NB * 16 * 64 * 4;  // bytes a wave sends
+    static_assert(4 * RGN <= STAGE, "a group's exchange regions fit one stage");
+    constexpr int PLO = LO == 0 ? NB : 0;  // first block the partner merges
+    f32x4* mine = (f32x4*)((grp == 0 ? lds_k0 : lds_k1) + wr * RGN);
+    const f32x4* theirs = (const f32x4*)((grp == 0 ? lds_k1 : lds_k0) + wr * RGN);
+    float* ml = (float*)lds_v0;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int db = PLO + b;
+        mine[(b * 4 + g) * 64 + lane] =
+            f32x4{o_acc[db][4 * g], o_acc[db][4 * g + 1], o_acc[db][4 * g + 2], o_acc[db][4 * g + 3]};
+      }
+    }
+    ml[(grp * 4 + wr) * 128 + lane] = m_run;
+    ml[(grp * 4 + wr) * 128 + 64 + lane] = l_part;
+    barrier();
+    f32x4 x1[NB][4];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) x1[b][g] = theirs[(b * 4 + g) * 64 + lane];
+    }
+    const float m1 = ml[((1 - grp) * 4 + wr) * 128 + lane];
+    const float l1 = ml[((1 - grp) * 4 + wr) * 128 + 64 + lane];
+    __builtin_amdgcn_sched_barrier(0);
+    const float m = vmax(m_run, m1);
+    const float a0 = fast_exp2((m_run - m) * c);
+    const float a1 = fast_exp2((m1 - m) * c);
+    float la, lb;
+    swap32(l_part * a0 + l1 * a1, la, lb);
+    const float l_tot = la + lb;
+    const float inv = 1.0f / l_tot;
+    const float w0s = a0 * inv, w1s = a1 * inv;
+    auto merged = [&](int b, int g) {
+      f32x4 o4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o4[e] = o_acc[LO + b][4 * g + e] * w0s + x1[b][g][e] * w1s;
+      return o4;
+    };
+    if (SPLIT && slot >= 0) {
+      // One chunk of a split block: its output normalised by its own l, in fp32, and
+      // log2 of its softmax denominator in units of the scaled scores, m c + log2(l).
+      if (TAIL && my_q >= S) return;
+      float* prow = p.part_o + ((int64_t)slot * TM + (my_q - q0)) * D;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) *(f32x4*)(prow + 32 * (LO + b) + 8 * g + 4 * hl) = merged(b, g);
+      }
+      if (grp == 0 && hl == 0) p.part_lse[(int64_t)slot * TM + (my_q - q0)] = m * c + fast_log2(l_tot);
+      return;
+    }
+    // Whole-row kernels at D = 128, and causal ones at D = 64, stage the wave's 32 rows x
+    // D/2 columns in lds_v1 (16-byte chunks swizzled with the row's low bits, CH a row) so
+    // each store writes 16 bytes a lane, CH lanes a row; the non-causal D = 64 kernels (two
+    // workgroups per CU) store 8 bytes a lane directly.
+    constexpr bool kStageOut = !SPLIT && (D == 128 || (D == 64 && CAUSAL));
+    if constexpr (kStageOut) {
+      constexpr int CH = 4 * NB;           // 16-byte chunks per staged row (D/2 columns)
+      constexpr int RPI = 64 / CH;         // rows per store instruction
+      constexpr int SWZ = CH - 1;
+      char* ob = lds_v1 + (grp * 4 + wr) * (32 * CH * 16);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 o4 = merged(b, g);
+          const int ch = 4 * b + g;
+          *(u32x2*)(ob + l32 * (CH * 16) + 16 * (ch ^ (l32 & SWZ)) + 8 * hl) =
+              u32x2{DTy::pack(o4[0], o4[1]), DTy::pack(o4[2], o4[3])};
+        }
+      }
+      asm volatile("" ::: "memory");
+      const int ch = lane % CH;
+#pragma unroll
+      for (int i = 0; i < 32 / RPI; ++i) {
+        const int row = RPI * i + lane / CH;
+        const u32x4 v = *(const u32x4*)(ob + row * (CH * 16) + 16 * (ch ^ (row & SWZ)));
+        const int q = wq0 + row;
+        const int col = 32 * LO + 8 * ch;
+        if ((!TAIL || q < S) && col < d_real) *(u32x4*)(op + (int64_t)q * p.o_ss + col) = v;
+      }
+      return;
+    }
+    if (TAIL && my_q >= S) return;
+    uint16_t* orow = op + (int64_t)my_q * p.o_ss;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 o4 = merged(b, g);
+        const int d = 32 * (LO + b) + 8 * g + 4 * hl;
+        if (d < d_real) *(u32x2*)(orow + d) = u32x2{DTy::pack(o4[0], o4[1]), DTy::pack(o4[2], o4[3])};
+      }
+    }
+  };
+
   // ---- merge the two key halves of each row block, O = acc / l ---------------------------
-  // Group 1 leaves (m, l, O^T) in LDS (the stages are free: every load has landed and
-  // every read has retired before the last barrier); group 0 merges and writes O.
+  if constexpr (DB % 2 == 0) {
+    // Both groups merge, each half of the d blocks (group 0 blocks [0, DB/2), group 1 the
+    // rest): every wave sends its partner (the wave of the other group with the same row
+    // block) the blocks the partner merges, as 16-byte chunks, and its (m, l).  The stages
+    // are free: every load has landed and every read has retired before the last barrier.
+    if (grp == 0) merge_half(std::integral_constant<int, 0>{});
+    else merge_half(std::integral_constant<int, DB / 2>{});
+    return;
+  }
+  // Group 1 leaves (m, l, O^T) in LDS; group 0 merges and writes O.
   float* xo = (float*)((wr < 2 ? lds_k0 : lds_k1) + (wr & 1) * (STAGE / 2));
   float* xml = (float*)lds_v0 + wr * 128;
   static_assert(DB * 16 * 64 * 4 <= STAGE / 2, "merge buffer must fit half a stage");
@@ -657,6 +779,45 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   }
 }
 
+// A workgroup's work: one query block of the whole-row grid, one chunk of the split grid,
+// or (PAIR) the causal pair of query blocks nq - 1 - j and j of one head, one after the
+// other, so that every pair has nq + 1 key steps (balanced without relying on the order in
+// which the hardware hands out workgroups) and the grid is half as many workgroups.
+// One workgroup per CU (LDS and registers).  The numbering (attn_fwd_split.h) regroups
+// block ids per XCD with sched >= 1 (one head's K/V in one L2) and issues causal tiles
+// heaviest first, so each CU takes the next tile when its current one ends and heavy
+// tiles pair with light ones.  Split items cover a chunk of key steps of a block and
+// leave a partial (slot >= 0) when the block has more than one chunk.
+template <int DT, int D, bool CAUSAL, bool TAIL, bool SPLIT, bool PAIR>
+__device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
+  constexpr int STAGE = pp_stage_bytes(D);
+  // One array per (tensor, stage): the stage of every access is a compile-time constant
+  // (the key loop is unrolled by two), so the compiler can tell the loads in flight into
+  // one stage from the reads of the other and does not wait on the former for the latter.
+  __shared__ __attribute__((aligned(1024))) char lds_k0[STAGE];
+  __shared__ __attribute__((aligned(1024))) char lds_k1[STAGE];
+  __shared__ __attribute__((aligned(1024))) char lds_v0[STAGE];
+  __shared__ __attribute__((aligned(1024))) char lds_v1[STAGE];
+  if constexpr (PAIR) {
+    static_assert(CAUSAL && !SPLIT, "pairs of causal query blocks");
+    WorkItem a, b;
+    pair_items(blockIdx.x, p.n_bh, p.n_qblk, p.sched, &a, &b);
+    attn_fwd_pp_block<DT, D, CAUSAL, TAIL, SPLIT>(p, a, lds_k0, lds_k1, lds_v0, lds_v1);
+    if (b.qt >= 0) {
+      // Every wave is past its last LDS access of the first block before the second
+      // block's prologue loads overwrite the stages.
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      __builtin_amdgcn_s_barrier();
+      attn_fwd_pp_block<DT, D, CAUSAL, TAIL, SPLIT>(p, b, lds_k0, lds_k1, lds_v0, lds_v1);
+    }
+  } else {
+    const WorkItem wi = SPLIT ? split_item(blockIdx.x, p.n_bh, p.split_items, p.sched, CAUSAL,
+                                           p.split_c, p.split_ns, p.split_slots, p.S)
+                              : whole_item(blockIdx.x, p.n_bh, p.n_qblk, p.sched, CAUSAL);
+    attn_fwd_pp_block<DT, D, CAUSAL, TAIL, SPLIT>(p, wi, lds_k0, lds_k1, lds_v0, lds_v1);
+  }
+}
+
 // Merge of the chunks of one split query block (after the split kernel on the same
 // stream): per row, with L_i the chunks' log-sum-exps, O = sum_i 2^(L_i - max L) O_i /
 // sum_i 2^(L_i - max L), the same rescale the online softmax applies between key tiles,
@@ -721,12 +882,20 @@ __device__ __forceinline__ void attn_merge_body(const FwdParams& p) {
   extern "C" __global__ void __launch_bounds__(512)                                       \
       __attribute__((amdgpu_waves_per_eu(TA_PP_WAVES(D, C), TA_PP_WAVES(D, C))))           \
       ta_fwd_pp_##DTN##_d##D##_c##C##_t##T(ta::FwdParams p) {                              \
-    ta::attn_fwd_pp_body<DT, D, (C != 0), (T != 0), false>(p);                            \
+    ta::attn_fwd_pp_body<DT, D, (C != 0), (T != 0), false, false>(p);                     \
   }                                                                                       \
   extern "C" __global__ void __launch_bounds__(512)                                       \
       __attribute__((amdgpu_waves_per_eu(2, 2)))                                          \
       ta_fwd_pp_split_##DTN##_d##D##_c##C##_t##T(ta::FwdParams p) {                        \
-    ta::attn_fwd_pp_body<DT, D, (C != 0), (T != 0), true>(p);                             \
+    ta::attn_fwd_pp_body<DT, D, (C != 0), (T != 0), true, false>(p);                      \
+  }
+
+// Causal query-block pairs (whole rows, D = 64 and 128): ta_fwd_pp_pair_<f16|bf16>_d<D>_c1_t<0|1>.
+#define TA_PP_PAIR_DEFINE(DTN, DT, D, T)                                                   \
+  extern "C" __global__ void __launch_bounds__(512)                                       \
+      __attribute__((amdgpu_waves_per_eu(2, 2)))                                          \
+      ta_fwd_pp_pair_##DTN##_d##D##_c1_t##T(ta::FwdParams p) {                             \
+    ta::attn_fwd_pp_body<DT, D, true, (T != 0), false, true>(p);                          \
   }
 
 // Merge kernels of the split path: ta_fwd_merge_<f16|bf16>_d<D>_c<0|1>, merge_threads(D)
@@ -751,3 +920,11 @@ TA_PP_DEFINE_CT(f16, 0, 160)
 TA_PP_DEFINE_CT(bf16, 1, 64)
 TA_PP_DEFINE_CT(bf16, 1, 128)
 TA_PP_DEFINE_CT(bf16, 1, 160)
+TA_PP_PAIR_DEFINE(f16, 0, 64, 0)
+TA_PP_PAIR_DEFINE(f16, 0, 64, 1)
+TA_PP_PAIR_DEFINE(f16, 0, 128, 0)
+TA_PP_PAIR_DEFINE(f16, 0, 128, 1)
+TA_PP_PAIR_DEFINE(bf16, 1, 64, 0)
+TA_PP_PAIR_DEFINE(bf16, 1, 64, 1)
+TA_PP_PAIR_DEFINE(bf16, 1, 128, 0)
+TA_PP_PAIR_DEFINE(bf16, 1, 128, 1)

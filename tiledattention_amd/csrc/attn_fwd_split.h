@@ -123,6 +123,27 @@ TA_HD inline WorkItem whole_item(int blk, int n_bh, int nq, int sched, bool caus
   return w;
 }
 
+// Pair grid (causal whole rows): ceil(nq / 2) items per (b, h); item j of a head covers
+// query blocks nq - 1 - j (first) and j, nq + 1 key steps in all, or the middle block alone
+// when nq is odd (b->qt = -1 then).  sched >= 1 (with 8 | total) maps block ids per XCD as
+// xcd_order describes; otherwise block ids run head by head.
+TA_HD inline void pair_items(int blk, int n_bh, int nq, int sched, WorkItem* a, WorkItem* b) {
+  const int np = (nq + 1) >> 1;
+  int bh, j;
+  if (sched >= 1 && ((np * n_bh) & 7) == 0) {
+    xcd_order(blk, n_bh, np, &bh, &j);
+  } else {
+    bh = blk / np;
+    j = blk - bh * np;
+  }
+  a->bh = b->bh = bh;
+  a->qt = nq - 1 - j;
+  b->qt = j < nq - 1 - j ? j : -1;
+  a->t_beg = b->t_beg = 0;
+  a->t_end = b->t_end = -1;
+  a->slot = b->slot = -1;
+}
+
 // Split grid: `items` per (b, h), ranked from the heaviest block down; sched >= 1 (with
 // 8 | total) maps block ids per XCD as xcd_order describes, otherwise block ids run
 // item-major across heads (heavy items of every head first).  A block of more than one

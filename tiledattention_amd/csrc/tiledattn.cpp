@@ -113,6 +113,14 @@ KernelId kernel_id(int dtype, int d, int tm, int tn, int causal, int tail, int a
   return {file, buf, static_cast<unsigned>(tm * 2)};  // tm / 32 waves of 64
 }
 
+// The causal query-block pair kernel of the eight-wave family (use_pairs).
+KernelId pair_kernel_id(int dtype, int d, int tail) {
+  char buf[96];
+  snprintf(buf, sizeof(buf), "ta_fwd_pp_pair_%s_d%d_c1_t%d", dtype == TA_BF16 ? "bf16" : "f16", d,
+           tail ? 1 : 0);
+  return {"attn_fwd_pp.hsaco", buf, 512u};
+}
+
 bool valid_tile(int t) { return t == 64 || t == 128; }
 
 bool valid_head_dim(int64_t d) { return d == 64 || d == 128 || d == 160 || d == 256; }
@@ -315,7 +323,7 @@ ta_status validate_args(const ta_fwd_args* a, int64_t* n_bh_out, int64_t* n_qblk
   if (a->accum != TA_ACC_FP32 && a->accum != TA_ACC_INPUT)
     return fail(TA_EINVAL, "accum %d", a->accum);
   if (a->causal != 0 && a->causal != 1) return fail(TA_EINVAL, "causal %d", a->causal);
-  if (a->sched < 0 || a->sched > 2) return fail(TA_EINVAL, "sched %d", a->sched);
+  if (a->sched < 0 || a->sched > 3) return fail(TA_EINVAL, "sched %d", a->sched);
   if (a->d_real != 0) {
     if (a->d_real < 8 || a->d_real > a->D || (a->d_real & 7) != 0)
       return fail(TA_EINVAL, "d_real %d (0, or a multiple of 8 in [8, D])", a->d_real);
@@ -400,6 +408,22 @@ bool unmasked_tail(const ta_fwd_args* a) {
   return a->aligned == 1 && a->S % a->tile_m == 0 && a->S % a->tile_n == 0;
 }
 
+// Whether a whole-row launch runs causal query blocks in pairs (nq - 1 - j, then j; one
+// workgroup each pair, attn_fwd_split.h pair_items): the eight-wave kernel at D <= 128,
+// causal, at least two blocks a head, and either forced (sched 3) or, with XCD grouping
+// (sched 1), a grid of two or more workgroups per CU.  Below that every block runs at once and pairing would
+// only lengthen the longest workgroup.  With two waves of workgroups or more, the hardware
+// hands block ids to the XCDs in a fixed round-robin, so an XCD whose CUs finish early
+// waits for the others before it gets its next block; pairs give every workgroup the same
+// work (nq + 1 key steps) instead of relying on that order.
+bool use_pairs(const ta_fwd_args* a, int64_t n_bh, int64_t n_qblk, int ncu) {
+  // (D = 160 pairs measured slower: B1 H8 S8192 bf16 147.6 -> 153.9 us)
+  if (!a->causal || n_qblk < 2 || a->D > 128 || !eight_wave(a->tile_m, a->tile_n, a->accum, a->D))
+    return false;
+  if (a->sched == 3) return true;
+  return a->sched == 1 && n_bh * n_qblk >= 2 * (int64_t)ncu;
+}
+
 // Whether the split path exists for this configuration (the eight-wave kernel).
 bool split_capable(const ta_fwd_args* a) {
   return eight_wave(a->tile_m, a->tile_n, a->accum, a->D);
@@ -469,7 +493,7 @@ ta_status ta_sdpa_fwd(const ta_fwd_args* a, void* stream) {
   if (vst != TA_OK || n_qblk == 0) return vst;
 
   const bool aligned = unmasked_tail(a);
-  const KernelId id =
+  KernelId id =
       kernel_id(a->dtype, (int)a->D, a->tile_m, a->tile_n, a->causal, !aligned, a->accum);
   ta_status gst = check_grid(n_bh * n_qblk, id.block, "kernel");
   if (gst != TA_OK) return gst;
@@ -482,11 +506,21 @@ ta_status ta_sdpa_fwd(const ta_fwd_args* a, void* stream) {
   DeviceGuard guard(a->device);
   if (guard.err != hipSuccess)
     return fail(TA_EHIP, "set device %d: %s", a->device, hipGetErrorString(guard.err));
+  int64_t blocks = n_bh * n_qblk;
+  if (a->causal && eight_wave(a->tile_m, a->tile_n, a->accum, a->D)) {
+    int ncu = 0;
+    ta_status cst = cu_count_locked(a->device, &ncu);
+    if (cst != TA_OK) return cst;
+    if (use_pairs(a, n_bh, n_qblk, ncu)) {
+      id = pair_kernel_id(a->dtype, (int)a->D, !aligned);
+      blocks = n_bh * ((n_qblk + 1) / 2);
+    }
+  }
   hipFunction_t fn = nullptr;
   ta_status s = get_function_locked(a->device, id, &fn);
   if (s != TA_OK) return s;
   void* params[] = {&p};
-  const unsigned grid = static_cast<unsigned>(n_bh * n_qblk);
+  const unsigned grid = static_cast<unsigned>(blocks);
   hipError_t e = hipModuleLaunchKernel(fn, grid, 1, 1, id.block, 1, 1, 0,
                                        static_cast<hipStream_t>(stream), params, nullptr);
   if (e != hipSuccess) return fail(TA_EHIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
