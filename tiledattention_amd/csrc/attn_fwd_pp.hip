@@ -288,6 +288,22 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
     }
   };
 
+  // Row max of the scores in s (NaN-propagating), over the wave's two lane halves.
+  auto row_max = [&]() {
+    float mxa = kMasked, mxb = kMasked;
+#pragma unroll
+    for (int bk = 0; bk < KB; ++bk) {
+#pragma unroll
+      for (int r = 0; r < 16; r += 4) {
+        mxa = vmax3(mxa, s[bk][r], s[bk][r + 1]);
+        mxb = vmax3(mxb, s[bk][r + 2], s[bk][r + 3]);
+      }
+    }
+    float a0, a1;
+    swap32(vmax(mxa, mxb), a0, a1);
+    return vmax(a0, a1);
+  };
+
   // VALU cluster of step t: mask, row max, rescale, P = 2^(s*c - m*c) packed, l.  One
   // code path for every step (blocks without a needed key are masked whole), so the
   // rescale of O exists once and O keeps one register assignment through the loop.
@@ -353,21 +369,7 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
     // saved.
     float l_step = make_p(m_run * c);
     if (__ballot(!(l_step < kRescaleBound))) {
-      float mxa = kMasked, mxb = kMasked;
-#pragma unroll
-      for (int bk = 0; bk < KB; ++bk) {
-#pragma unroll
-        for (int r = 0; r < 16; r += 4) {
-          mxa = vmax3(mxa, s[bk][r], s[bk][r + 1]);
-          mxb = vmax3(mxb, s[bk][r + 2], s[bk][r + 3]);
-        }
-      }
-      float mx;
-      {
-        float a0, a1;
-        swap32(vmax(mxa, mxb), a0, a1);
-        mx = vmax(a0, a1);
-      }
+      const float mx = row_max();
       const bool need = (mx - m_run) * c > kRescaleLog2;
       if (__ballot(need)) {
         const float m_new = need ? mx : m_run;
@@ -462,7 +464,15 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
     }
   }
   // S_0.
-  auto first = [&]() { qk(lds_k0); };
+  // The reference point for a row's first step is its row max when that step needs no
+  // mask, so the first softmax computes P once (from the initial point it would find every
+  // P above the bound, reduce the max and compute P again); a masked first step keeps the
+  // initial point and takes the exact rule over its masked scores.  O and l start at zero,
+  // so the result is the same either way.
+  auto first = [&]() {
+    qk(lds_k0);
+    if (no_mask(t_beg) && all_active(t_beg)) m_run = row_max();
+  };
 
   // Step t with stage parity PAR: the stages of K_t (consumed; receives K_{t+2}), K_{t+1},
   // V_t and V_{t-1} (consumed; receives V_{t+1}).
