@@ -222,3 +222,31 @@ def test_static_scratch_entry_rejects_oversize_before_any_device_call(lib):
     assert "exceeds the static scratch of 67108864 bytes" in _lib.last_error(lib)
     assert lib.ta_sdpa_fwd_split_static(None, 1, None) == _lib.TA_EINVAL
     assert lib.ta_sdpa_fwd_split_static(ctypes.byref(_args(D=96)), 1, None) == _lib.TA_EUNSUPPORTED
+
+
+@pytest.mark.parametrize("dtype", [_lib.TA_FP16, _lib.TA_BF16])
+def test_pair_kernel_symbols_exist(dtype):
+    """Every configuration the pairing rule accepts names a symbol of the eight-wave object."""
+    data = (_lib.lib_dir() / "attn_fwd_pp.hsaco").read_bytes()
+    for d in (64, 128):
+        for tail in (False, True):
+            assert _lib.uses_pairs(causal=True, head_dim=d, tile_m=128, tile_n=64, accum=_lib.TA_ACC_FP32,
+                                   n_bh=8, n_qblk=64, sched=1, compute_units=256)
+            f, sym = _lib.kernel_symbol(dtype=dtype, head_dim=d, tile_m=128, tile_n=64, causal=True,
+                                        tail=tail, accum=_lib.TA_ACC_FP32, pair=True)
+            assert f == "attn_fwd_pp.hsaco" and sym.encode() + b"\x00" in data, sym
+
+
+@pytest.mark.parametrize("kw,expected", [
+    (dict(), True),                                   # C3 S=8192: 512 blocks on 256 CUs
+    (dict(n_qblk=32), False),                          # one wave of workgroups
+    (dict(n_qblk=32, sched=3), True),                  # forced
+    (dict(sched=0), False), (dict(sched=2), False),
+    (dict(causal=False), False), (dict(head_dim=160), False),
+    (dict(accum=_lib.TA_ACC_INPUT), False), (dict(tile_m=64), False), (dict(n_qblk=1, sched=3), False),
+])
+def test_pairing_rule(kw, expected):
+    args = dict(causal=True, head_dim=128, tile_m=128, tile_n=64, accum=_lib.TA_ACC_FP32, n_bh=8,
+                n_qblk=64, sched=1, compute_units=256)
+    args.update(kw)
+    assert _lib.uses_pairs(**args) is expected

@@ -34,15 +34,29 @@ TILE_SHAPES = ((64, 64), (64, 128), (128, 64), (128, 128))
 STATIC_SCRATCH_BYTES = 64 << 20  # TA_STATIC_SCRATCH_BYTES
 
 
+def uses_pairs(*, causal: bool, head_dim: int, tile_m: int, tile_n: int, accum: int, n_bh: int,
+               n_qblk: int, sched: int, compute_units: int) -> bool:
+    """Whether a whole-row launch runs causal query blocks in pairs; the same rule as
+    use_pairs() in csrc/tiledattn.cpp."""
+    if not causal or n_qblk < 2 or head_dim > 128:
+        return False
+    if not (tile_m == 128 and tile_n in (64, 128) and accum == TA_ACC_FP32):
+        return False
+    if sched == 3:
+        return True
+    return sched == 1 and n_bh * n_qblk >= 2 * compute_units
+
+
 def kernel_symbol(*, dtype: int, head_dim: int, tile_m: int, tile_n: int, causal: bool,
-                  tail: bool, accum: int, split: bool = False) -> tuple[str, str]:
+                  tail: bool, accum: int, split: bool = False, pair: bool = False) -> tuple[str, str]:
     """(code object file, kernel symbol) the C ABI launches for a configuration; the same
     rule as kernel_id() in csrc/tiledattn.cpp (used to label measurements).  ``split``
-    names the split-key-range kernel (its merge kernel is ta_fwd_merge_<dt>_d<D>_c<c>)."""
+    names the split-key-range kernel (its merge kernel is ta_fwd_merge_<dt>_d<D>_c<c>),
+    ``pair`` the causal pair kernel (``uses_pairs``)."""
     dt = "bf16" if dtype == TA_BF16 else "f16"
     c, t = int(bool(causal)), int(bool(tail))
     if tile_m == 128 and tile_n in (64, 128) and accum == TA_ACC_FP32 and head_dim <= 160:
-        kind = "pp_split" if split else "pp"
+        kind = "pp_split" if split else ("pp_pair" if pair else "pp")
         return "attn_fwd_pp.hsaco", f"ta_fwd_{kind}_{dt}_d{head_dim}_c{c}_t{t}"
     if split:
         raise ValueError("split key ranges exist for tiles (128, 64) and (128, 128), fp32 "
