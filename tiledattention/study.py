@@ -18,11 +18,13 @@ Restates the reference's study pipeline (``benchmark-gb10/run_study.py``) for th
 
 Differences, all recorded in ``status_detail`` where they apply: FLOPs are counted as the
 reference study does (``2·B·H·S·(S+1)·D`` causal, ``:95-112``); inputs are seeded
-``torch.manual_seed(1234)`` N(0,1) on the GPU as there (``:526-529``).  On this platform the
-bf16 math path of ``torch_sdpa_math`` is not run, and ``torch_sdpa`` in bf16 is limited to the
-fused backends (flash, efficient), because PyTorch's bf16 math path issues batched products
-with a transposed operand that have faulted these GPUs; the eager baseline makes Kᵀ
-contiguous for the same reason.  No figures are drawn (matplotlib is not a dependency).
+``torch.manual_seed(1234)`` N(0,1) on the GPU as there (``:526-529``).  The bf16 math path
+of ``torch_sdpa_math`` is not run, and ``torch_sdpa`` in bf16 is limited to the fused
+backends (flash, efficient): PyTorch's bf16 math path calls batched products
+(``torch.bmm``) whose right operand is a transposed view, a form known to fault MI355X GPUs
+of the pool these measurements run on (a platform notice; it was never run here, so no run
+of this build has shown the fault).  The eager baseline makes Kᵀ contiguous for the same
+reason.  No figures are drawn (matplotlib is not a dependency).
 
 Run: ``python -m tiledattention.study --out DIR [--seqs ...] [--dims ...]``.
 """
