@@ -243,6 +243,25 @@ def test_wide_head_dim_input_dtype_accumulation(gpu):
                 what="D=160 fp16 accum")
 
 
+@pytest.mark.parametrize("tiles", [(None, None), (64, 64)])
+@pytest.mark.parametrize("s,causal,dtype", [
+    (512, False, "bfloat16"), (512, True, "float16"), (1000, False, "float16"), (1536, True, "bfloat16"),
+])
+def test_d256_direct_staging(gpu, tiles, s, causal, dtype):
+    """D = 256 kernels load K/V tiles straight into LDS (swizzled rows; the 64-row tiles
+    refill K and V separately through one stage): aligned and ragged lengths, many tiles,
+    fp32 and input-dtype accumulation, against the oracle on sampled rows."""
+    tm, tn = tiles
+    q, k, v = inputs((1, 2, s, 256), dtype, 2560 + s + (tm or 0))
+    rows = sample_rows(s, 64)
+    ref = oracle_f32(q, k, v, causal=causal, rows=rows)
+    for accum in ("fp32", "fp16"):
+        say(f"D=256 {dtype} (1,2,{s},256) causal={causal} tiles=({tm},{tn}) accum={accum}")
+        out = run_gpu(q, k, v, causal=causal, tile_m=tm, tile_n=tn, accum_mode=accum)
+        tol = TOL[dtype] if accum == "fp32" else LOWP_TOL[dtype]
+        check_close(as_f32(out, rows), ref, dtype, tol=tol, what=f"D=256 accum={accum}")
+
+
 def test_wide_head_dim_rejects_128_key_tiles(gpu):
     q, k, v = inputs((1, 1, 64, 160), "float16", 5)
     say("wide D=160 with TILE_N=128 -> ValueError before launch")

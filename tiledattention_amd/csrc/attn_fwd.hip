@@ -21,6 +21,9 @@
 //   tile t+1 is fetched (buffer loads, range-checked so rows past S read as zero) while
 //   tile t is consumed; one barrier per tile (two with one stage).  LDS rows are padded (K: 2D+16 bytes, V: 2D+64 bytes) so the b128 K
 //   reads and the b64 transposed V reads are free of bank conflicts on the 64-bank LDS.
+//   At D = 256 the tiles go HBM -> LDS directly instead (buffer loads with the LDS-write
+//   form) into unpadded rows with XOR-swizzled 16-byte chunks: the 64-128 staging
+//   registers per lane would not fit beside O (128) and Q (64).
 // * exp is v_exp_f32 (2^x) with scale*log2(e) folded into one FMA per score.
 // * Causal: tiles above the diagonal are never loaded by a wave that does not need them,
 //   32-key blocks above a wave's rows are skipped, and only the diagonal block is masked.
@@ -77,6 +80,21 @@ struct LdsLayout {
   static_assert((KS / 16) % 2 == 1 && (VS / 16) % 8 == 4, "conflict-free strides");
 };
 
+// D = 256, loaded straight into LDS: rows of 512 bytes (two 64-bank rows), 16-byte chunks
+// XOR-swizzled per row instead of padded:
+// * K: physical chunk = logical ^ (row & 15).  A b128 read pass covers 16 consecutive rows
+//   at one logical chunk -> 16 distinct chunks mod 16 -> conflict-free.
+// * V: physical chunk = logical ^ 4 (row & 3).  A b64 transposed read pass covers 4
+//   consecutive rows x 4 logical chunks (64 bytes) -> 4 distinct 64-byte groups.
+template <int D>
+struct LdsSwizzled {
+  static_assert(D == 256, "swizzled staging is built for D = 256");
+  static constexpr int KS = 2 * D;
+  static constexpr int VS = 2 * D;
+  __device__ static inline int swz_k(int row) { return row & 15; }
+  __device__ static inline int swz_v(int row) { return (row & 3) << 2; }
+};
+
 template <int DT, int D, int TM, int TN, bool CAUSAL, bool TAIL, bool LOWP>
 __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
   constexpr int NW = TM / 32;        // waves per workgroup
@@ -89,7 +107,8 @@ __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
   // Rows one staging pass covers when a pass is whole rows (CPR divides NT), else 0.
   constexpr int RPP = (NT % CPR == 0) ? NT / CPR : 0;
   static_assert((TN * CPR) % NT == 0, "tile must split evenly over threads");
-  using L = LdsLayout<D>;
+  constexpr bool DMA = D == 256;  // tiles straight into LDS (swizzled rows)
+  using L = std::conditional_t<DMA, LdsSwizzled<D>, LdsLayout<D>>;
   constexpr int K_BYTES = TN * L::KS;
   constexpr int STAGE = K_BYTES + TN * L::VS;
   using DTy = DType<DT>;
@@ -195,16 +214,86 @@ __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
       *(u32x4*)(base + st_off(i, st_vlds, L::VS, K_BYTES)) = stv[i];
     }
   };
+  // Direct-to-LDS tiles (D = 256).  A tile of one tensor is NCH chunks of 1 KiB (RPC rows
+  // each); wave w fills chunks g = w + NW i, lane l writing physical chunk l % CPR of row
+  // RPC g + l / CPR, so it loads logical chunk (l % CPR) ^ swz(row) of that row.  Rows
+  // RPC NW i apart: K's swizzle repeats every 16 rows (KP distinct per-lane offsets, the
+  // rest a uniform row step), V's every 4 (one offset).  Rows past S are outside the
+  // tile's buffer resource and read as zero.
+  constexpr int RPC = 1024 / (2 * D);
+  constexpr int NCH = TN * 2 * D / 1024;
+  constexpr int NLW = NCH / NW;  // loads per wave per tensor per tile
+  // s_waitcnt immediate: vmcnt(NLW) (its low 4 bits at 3:0, the high 2 at 15:14), expcnt
+  // and lgkmcnt at their maxima.
+  constexpr int kWaitNLW = 0x0F70 | (NLW & 15) | ((NLW >> 4) << 14);
+  static_assert(NLW < 64, "vmcnt field");
+  constexpr int RSTEP = RPC * NW;  // rows between a wave's consecutive chunks
+  constexpr int KP = DMA ? 16 / RSTEP : 1;
+  static_assert(!DMA || (NCH % NW == 0 && 16 % RSTEP == 0 && RSTEP % 4 == 0), "DMA tiling");
+  int dm_k[KP];
+  int dm_v = 0;
+  if constexpr (DMA) {
+    const int row0 = RPC * wave + lane / CPR;
+    const int pc = lane % CPR;
+#pragma unroll
+    for (int j = 0; j < KP; ++j) {
+      const int row = row0 + RSTEP * j;
+      dm_k[j] = row * k_rb + ((pc ^ L::swz_k(row)) << 4);
+    }
+    dm_v = row0 * v_rb + ((pc ^ L::swz_v(row0)) << 4);
+  }
+  auto dma_k = [&](int kt, int stage) {
+    const __amdgpu_buffer_rsrc_t kr = row_rsrc(kp + (int64_t)kt * TN * p.k_ss, S - kt * TN, k_rb);
+    char* base = smem + stage * STAGE;
+#pragma unroll
+    for (int i = 0; i < NLW; ++i) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          kr, (__attribute__((address_space(3))) void*)(base + (wave + NW * i) * 1024), 16,
+          dm_k[i % KP], (i / KP) * 16 * k_rb, 0, 0);
+    }
+  };
+  auto dma_v = [&](int kt, int stage) {
+    const __amdgpu_buffer_rsrc_t vr = row_rsrc(vp + (int64_t)kt * TN * p.v_ss, S - kt * TN, v_rb);
+    char* base = smem + stage * STAGE + K_BYTES;
+#pragma unroll
+    for (int i = 0; i < NLW; ++i) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          vr, (__attribute__((address_space(3))) void*)(base + (wave + NW * i) * 1024), 16,
+          dm_v, i * RSTEP * v_rb, 0, 0);
+    }
+  };
 
   // ---- per-lane LDS read offsets --------------------------------------------------------
   // K (A operand of S^T = K Q^T): lane reads row l32 of a 32-key block, 16 bytes at
   // column 16 * (2 kk + hl).
-  const int k_rd = l32 * L::KS + hl * 16;
+  // With swizzled rows: row l32 of a block has m = swz_k(l32) (blocks are 32 rows, so
+  // swz_k(32 bk + l32) = swz_k(l32)); logical chunk 2 kk + hl is physical
+  // (2 kk + hl) ^ m, i.e. byte 32 (kk ^ (m >> 1)) + 16 (hl ^ (m & 1)) of the row: k_rd
+  // below XOR 32 kk.
+  int k_rd = l32 * L::KS + hl * 16;
+  if constexpr (DMA) {
+    const int m = L::swz_k(l32);
+    k_rd = l32 * L::KS + 32 * (m >> 1) + 16 * (hl ^ (m & 1));
+  }
   // V^T (A operand of O^T = V^T P^T) via the transposed read: lane l of 16-lane group G
   // addresses row (key) 4 * hl + (l % 16) / 4 of a 16-key chunk and d = 16 * (G % 2) +
   // 4 * (l % 4); the hardware hands lane l column d = 16 * (G % 2) + l % 16 of those 4 rows.
-  const int v_rd = K_BYTES + (4 * hl + ((lane & 15) >> 2)) * L::VS +
-                   (16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2;
+  int v_rd = K_BYTES + (4 * hl + ((lane & 15) >> 2)) * L::VS +
+             (16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2;
+  // With swizzled rows: the row's swizzle 4 r (r = row & 3 = (lane >> 2) & 3, the same for
+  // every 16-key chunk and its + 8 rows) moves the 64-byte group of d block db to
+  // db ^ r: v_rd below XOR 64 db.
+  if constexpr (DMA) {
+    const int r = (lane >> 2) & 3;
+    v_rd = K_BYTES + (4 * hl + r) * L::VS + ((64 * r) ^ ((16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2));
+  }
+  auto k_addr = [&](int bk, int kk) {
+    return DMA ? bk * 32 * L::KS + (k_rd ^ (32 * kk)) : k_rd + bk * 32 * L::KS + 32 * kk;
+  };
+  auto v_addr = [&](int bk, int kc, int db) {
+    return DMA ? (v_rd ^ (64 * db)) + (32 * bk + 16 * kc) * L::VS
+               : v_rd + (32 * bk + 16 * kc) * L::VS + 64 * db;
+  };
 
   // ---- running state (lane = query l32 of this wave) ----------------------------------
   float m_run = kNegLarge;   // reference point of the exponent, raw score units
@@ -221,24 +310,35 @@ __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
   }
   const float c = p.scale_log2;
 
+  // P of the current tile (packed) and its rescale factor, kept between the two parts of a
+  // tile when it runs in two parts (a whole tile keeps its own).
+  uint32_t pk_part[KB][8];
+  float alpha_part = 1.0f;
+
   // One key tile.  FULL: every 32-key block of the tile is visible to every row of the
   // wave (no mask, no skipped block) - the common case, compiled without any per-block
-  // condition.
-  auto tile = [&](const char* st, int k0, auto full_tag) {
+  // condition.  PART 0 is the whole tile; PART 1 ends with P (reads the K tile), PART 2 is
+  // P.V (reads the V tile), for the loop that refills K and V separately.
+  auto tile = [&](const char* st, int k0, auto full_tag, auto part_tag) {
     constexpr bool FULL = decltype(full_tag)::value;
+    constexpr int PART = decltype(part_tag)::value;
+    uint32_t pk_whole[KB][8];
+    float alpha_whole = 1.0f;
+    uint32_t(&pk)[KB][8] = PART == 0 ? pk_whole : pk_part;
+    float& alpha = PART == 0 ? alpha_whole : alpha_part;
     bool active[KB];
 #pragma unroll
     for (int bk = 0; bk < KB; ++bk) active[bk] = FULL || (k0 + 32 * bk) < wave_kv_end;
+    if constexpr (PART != 2) {
 
     // -- S^T blocks ------------------------------------------------------------------
     f32x16 s[KB];
 #pragma unroll
     for (int bk = 0; bk < KB; ++bk) {
       if (active[bk]) {
-        const char* kb = st + k_rd + bk * 32 * L::KS;
-        f32x16 acc = DTy::mfma(*(const u32x4*)kb, qf[0], f32x16{});
+        f32x16 acc = DTy::mfma(*(const u32x4*)(st + k_addr(bk, 0)), qf[0], f32x16{});
 #pragma unroll
-        for (int kk = 1; kk < DK; ++kk) acc = DTy::mfma(*(const u32x4*)(kb + 32 * kk), qf[kk], acc);
+        for (int kk = 1; kk < DK; ++kk) acc = DTy::mfma(*(const u32x4*)(st + k_addr(bk, kk)), qf[kk], acc);
         s[bk] = acc;
       }
     }
@@ -283,7 +383,7 @@ __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
     }
 
     // -- new reference point, rescale of running state ---------------------------------
-    float alpha = 1.0f;
+    alpha = 1.0f;
     if (LOWP) {
       const float m_new = vmax(m_run, mx);
       alpha = fast_exp2((m_run - m_new) * c);
@@ -306,7 +406,6 @@ __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
     // is not exactly 1 and its rounding would otherwise not cancel).  Input-dtype
     // accumulation keeps the reference's fp32 sum of the unrounded P (flash_fwd.py:429).
     const float mc = m_run * c;
-    uint32_t pk[KB][8];
 #pragma unroll
     for (int bk = 0; bk < KB; ++bk) {
       if (active[bk]) {
@@ -329,6 +428,9 @@ __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
       }
     }
 
+    }  // PART != 2
+    if constexpr (PART == 1) return;
+
     // -- O^T += V^T P^T ------------------------------------------------------------------
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
@@ -338,7 +440,7 @@ __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
         if (active[bk]) {
 #pragma unroll
           for (int kc = 0; kc < 2; ++kc) {
-            const char* a0p = st + v_rd + (32 * bk + 16 * kc) * L::VS + 64 * db;
+            const char* a0p = st + v_addr(bk, kc, db);
             s16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)a0p);
             s16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a0p + 8 * L::VS));
             u32x2 w0 = __builtin_bit_cast(u32x2, r0);
@@ -366,39 +468,89 @@ __device__ __forceinline__ void attn_fwd_body(const FwdParams& p) {
     }
   };
 
-  if (n_tiles > 0) {
-    load_tile(0);
-    store_tile(0);
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+  using P2 = std::integral_constant<int, 2>;
+  // Fully visible: every key of the tile is <= the wave's first query (causal) and < S.
+  auto is_full = [&](int k0) { return (!CAUSAL || k0 + TN - 1 <= wq0) && (!TAIL || k0 + TN <= S); };
+  // The unmasked tile body is a second copy of the tile in the code.  At D = 256, and at
+  // D >= 128 with 64-row tiles, the two copies together need more registers than the
+  // kernel has (the tail-masked kernels spilled 14-168 registers to scratch), so there
+  // every tile takes the masked body, whose masks are wave-uniform per-block branches that
+  // unmasked tiles skip.
+  constexpr bool kFullBody = D <= 64 || (TM == 128 && D <= 160);
+  auto run_tile = [&](const char* st, int k0, auto part_tag) {
+    if (kFullBody && is_full(k0)) {
+      tile(st, k0, std::true_type{}, part_tag);
+    } else if (k0 < wave_kv_end) {
+      tile(st, k0, std::false_type{}, part_tag);
+    }
+  };
+
+  if constexpr (!DMA) {
+    if (n_tiles > 0) {
+      load_tile(0);
+      store_tile(0);
+    }
+  } else if (n_tiles > 0) {
+    dma_k(0, 0);
+    dma_v(0, 0);
   }
-  // Drain the Q-fragment loads here, on every path into the loop: otherwise the
-  // waitcnt insertion merges a "Q still in flight" state into the loop header and puts a
-  // vmcnt wait on the next tile's prefetch in front of every QK^T MFMA.
+  // Drain the Q-fragment loads (and the first tile's direct loads) here, on every path into
+  // the loop: otherwise the waitcnt insertion merges a "Q still in flight" state into the
+  // loop header and puts a vmcnt wait on the next tile's prefetch in front of every QK^T
+  // MFMA.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
   for (int kt = 0; kt < n_tiles; ++kt) {
     const bool has_next = kt + 1 < n_tiles;
-    if (has_next) load_tile(kt + 1);
-
     const int k0 = kt * TN;
     const char* st = smem + (NST == 2 ? (kt & 1) * STAGE : 0);
-    // Fully visible: every key of the tile is <= the wave's first query (causal) and < S.
-    const bool full = (!CAUSAL || k0 + TN - 1 <= wq0) && (!TAIL || k0 + TN <= S);
-    if (full) {
-      tile(st, k0, std::true_type{});
-    } else if (k0 < wave_kv_end) {
-      tile(st, k0, std::false_type{});
-    }
-
-    if constexpr (NST == 2) {
-      if (has_next) store_tile((kt + 1) & 1);
+    if constexpr (!DMA) {
+      if (has_next) load_tile(kt + 1);
+      run_tile(st, k0, P0{});
+      if constexpr (NST == 2) {
+        if (has_next) store_tile((kt + 1) & 1);
+        __syncthreads();
+      } else {
+        // One stage: the next tile (in registers since the top of this iteration) replaces
+        // the current one once every wave is done reading it.
+        __syncthreads();
+        if (has_next) {
+          store_tile(0);
+          __syncthreads();
+        }
+      }
+    } else if constexpr (NST == 2) {
+      // The other stage was read last in the previous tile, before its closing barrier.
+      if (has_next) {
+        dma_k(kt + 1, (kt + 1) & 1);
+        dma_v(kt + 1, (kt + 1) & 1);
+      }
+      run_tile(st, k0, P0{});
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of the next tile
       __syncthreads();
     } else {
-      // One stage: the next tile (in registers since the top of this iteration) replaces
-      // the current one once every wave is done reading it.
+      // One stage, K and V refilled separately: K(kt + 1) once every wave has its P of
+      // tile kt (its latency hidden by P.V), V(kt + 1) once every wave is done with P.V
+      // (hidden by the next tile's S and softmax).  On entry V(kt) may be in flight (kt >
+      // 0); every wave runs the same barriers whether or not it has keys in this tile.
+      run_tile(st, k0, P1{});
+      __syncthreads();
+      if (has_next) dma_k(kt + 1, 0);
+      // V(kt) was issued before K(kt + 1): wait until at most K(kt + 1)'s loads are left.
+      if (has_next) {
+        __builtin_amdgcn_s_waitcnt(kWaitNLW);
+      } else {
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+      }
+      __syncthreads();
+      run_tile(st, k0, P2{});
       __syncthreads();
       if (has_next) {
-        store_tile(0);
+        dma_v(kt + 1, 0);
+        __builtin_amdgcn_s_waitcnt(kWaitNLW);  // K(kt + 1) landed, V(kt + 1) may not have
         __syncthreads();
       }
     }

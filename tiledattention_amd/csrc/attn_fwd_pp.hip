@@ -88,6 +88,9 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   // Raised MFMA-cluster priority only in the kernels built for two workgroups per CU (the
   // non-causal D = 64 whole-row ones, TA_PP_WAVES below).
   constexpr bool kPrioMfma = !SPLIT && D == 64 && !CAUSAL;
+  // Those kernels have 128 VGPRs a lane (four waves per SIMD): P is formed two scores at a
+  // time there, since a phased softmax holds 32 exponent arguments beside the 32 scores.
+  constexpr bool kPhasedP = !kPrioMfma;
   using DTy = DType<DT>;
 
   static_assert(STAGE == pp_stage_bytes(D), "stage layout");
@@ -329,25 +332,36 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
     // ops sit many instructions apart (C3 -1 %); the sum uses four independent dot2 chains,
     // each started without a zeroed accumulator (four VALU ops fewer; 0.3-2 %).
     auto make_p = [&](float mc) {
-      float x[KB][16];
+      if constexpr (kPhasedP) {
+        float x[KB][16];
 #pragma unroll
-      for (int bk = 0; bk < KB; ++bk) {
+        for (int bk = 0; bk < KB; ++bk) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) x[bk][r] = __builtin_fmaf(s[bk][r], c, -mc);
+          for (int r = 0; r < 16; ++r) x[bk][r] = __builtin_fmaf(s[bk][r], c, -mc);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int bk = 0; bk < KB; ++bk) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) x[bk][r] = fast_exp2(x[bk][r]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int bk = 0; bk < KB; ++bk) {
+#pragma unroll
+          for (int r = 0; r < 16; r += 2) pk[bk][r >> 1] = DTy::pack(x[bk][r], x[bk][r + 1]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+#pragma unroll
+        for (int bk = 0; bk < KB; ++bk) {
+#pragma unroll
+          for (int r = 0; r < 16; r += 2) {
+            pk[bk][r >> 1] = DTy::pack(fast_exp2(__builtin_fmaf(s[bk][r], c, -mc)),
+                                       fast_exp2(__builtin_fmaf(s[bk][r + 1], c, -mc)));
+          }
+        }
       }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int bk = 0; bk < KB; ++bk) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) x[bk][r] = fast_exp2(x[bk][r]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int bk = 0; bk < KB; ++bk) {
-#pragma unroll
-        for (int r = 0; r < 16; r += 2) pk[bk][r >> 1] = DTy::pack(x[bk][r], x[bk][r + 1]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
       float l4[4];
 #pragma unroll
       for (int bk = 0; bk < KB; ++bk) {
