@@ -354,16 +354,17 @@ def main() -> int:
 
     # The kernel this configuration launches (the C ABI's choice, mirrored in _lib); the
     # committed HBM-traffic figure is used only if it was measured on that kernel.
-    tm, tn = flash_fwd._default_tile_config_for_shape_gfx950(seq_len=s, head_dim=d, causal=causal)
+    tm, tn = flash_fwd._default_tile_config_for_shape_gfx950(seq_len=s, head_dim=d, causal=causal,
+                                                             n_bh=b * h)
     n_qblk = (s + tm - 1) // tm
     sched = flash_fwd._resolve_sched(n_blocks=b * h * n_qblk, causal=causal, tile_m=tm, tile_n=tn,
                                      head_dim=d)
     pair = _lib.uses_pairs(causal=causal, head_dim=d, tile_m=tm, tile_n=tn, accum=_lib.TA_ACC_FP32,
                            n_bh=b * h, n_qblk=n_qblk, sched=sched,
                            compute_units=torch.cuda.get_device_properties(dev).multi_processor_count)
+    tail = _lib.tail_masked(seq_len=s, tile_m=tm, tile_n=tn, accum=_lib.TA_ACC_FP32, head_dim=d)
     _, kernel = _lib.kernel_symbol(dtype=_lib.TA_BF16, head_dim=d, tile_m=tm, tile_n=tn,
-                                   causal=causal, tail=(s % tm != 0 or s % tn != 0),
-                                   accum=_lib.TA_ACC_FP32, pair=pair)
+                                   causal=causal, tail=tail, accum=_lib.TA_ACC_FP32, pair=pair)
     traffic = None
     tp = Path(args.traffic_json)
     if tp.exists():

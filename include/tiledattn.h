@@ -61,8 +61,9 @@ typedef struct ta_fwd_args {
                           non-negative multiples of 8; the row stride stride[2] at least
                           the row width (D, or d_real when set: rows must not overlap)
                           and below 2^23; S * stride[2] * 2 bytes below 2^31 for k and v
-                          (and for q on tiles (128, 64) / (128, 128) with fp32
-                          accumulation), which are read with 32-bit buffer offsets */
+                          (and for q on the eight-wave kernels: fp32 accumulation with
+                          tiles (128, 64) / (128, 128), D <= 160, or (64, 64) / (64, 128),
+                          D = 64 or 128), which are read with 32-bit buffer offsets */
   int64_t k_stride[4];
   int64_t v_stride[4];
   int64_t o_stride[4];
@@ -81,10 +82,12 @@ typedef struct ta_fwd_args {
   int32_t d_real;  /* 0, or the head-dim columns q/k/v/o actually have (a multiple of 8 below
                       D): the kernel for D reads the missing columns as zero and does not
                       write them, so a narrower head dim needs no padded copies (the
-                      reference pads on the host, flash_fwd.py:868-872).  Tiles (128, 64)
-                      and (128, 128) with fp32 accumulation and D <= 160 only. */
+                      reference pads on the host, flash_fwd.py:868-872).  The eight-wave
+                      kernels only (fp32 accumulation; tiles (128, 64) and (128, 128) with
+                      D <= 160, tiles (64, 64) and (64, 128) with D = 64 or 128). */
   int32_t aligned; /* 1: the kernel variant without tail masking runs when S is a multiple
-                      of tile_m and tile_n (the reference's aligned fast path,
+                      of tile_m and tile_n, and on the eight-wave kernels of their 128-key
+                      step (the reference's aligned fast path,
                       flash_fwd.py:199-238, 880-921); 0: the tail-masked variant always
                       runs (TILEDATTN_DISABLE_ALIGNED_FASTPATH).  Both give the same
                       result on such S; zero-initialised arguments get the masked one. */
@@ -105,7 +108,8 @@ ta_status ta_prepare(int32_t device, int32_t dtype, int32_t head_dim, int32_t ti
                      int32_t tile_n, int32_t causal, int32_t accum, int32_t aligned);
 
 /* Enqueue one SDPA forward on `stream`.  Picks the unmasked-tail kernel when
- * args->aligned is 1 and S is a multiple of both tiles.  Zero-size problems (B*H == 0 or
+ * args->aligned is 1 and S is a multiple of both tiles (and of 128 on the eight-wave
+ * kernels, see `aligned`).  Zero-size problems (B*H == 0 or
  * S == 0) return TA_OK with no launch. */
 ta_status ta_sdpa_fwd(const ta_fwd_args* args, void* stream);
 

@@ -135,9 +135,10 @@ def test_tails_all_tiles(gpu, s, causal, dtype, d):
 
 @pytest.mark.parametrize("d", [8, 32, 48, 80, 96, 100])
 def test_head_dim_padding(gpu, d):
-    """D outside {64,128}: a multiple of 8 runs in place on the default (eight-wave) kernel,
-    whose missing columns read as zero (dense output of width D); other D, and the other
-    tiles, are zero-padded on the host and the output is a sliced view."""
+    """D outside {64,128}: a multiple of 8 runs in place on the eight-wave kernels (default
+    tile and the 64-row tiles with fp32 accumulation), whose missing columns read as zero
+    (dense output of width D); other D, and the four-wave kernels (input-dtype
+    accumulation), are zero-padded on the host and the output is a sliced view."""
     q, k, v = inputs((1, 2, 200, d), "float16", 7 + d)
     for causal in (False, True):
         ref = oracle_f32(q, k, v, causal=causal)
@@ -146,10 +147,14 @@ def test_head_dim_padding(gpu, d):
         assert out.shape == (1, 2, 200, d)
         assert out.is_contiguous() == (d % 8 == 0)
         check_close(as_f32(out), ref, "float16", what=f"pad D={d}")
-        say(f"pad fp16 (1,2,200,{d}) causal={causal} tile 64x64 (host padding)")
-        host = run_gpu(q, k, v, causal=causal, tile_m=64, tile_n=64)
+        say(f"pad fp16 (1,2,200,{d}) causal={causal} tile 64x64 (64-row eight-wave kernel)")
+        out = run_gpu(q, k, v, causal=causal, tile_m=64, tile_n=64)
+        assert out.shape == (1, 2, 200, d) and out.is_contiguous() == (d % 8 == 0)
+        check_close(as_f32(out), ref, "float16", what=f"64-row pad D={d}")
+        say(f"pad fp16 (1,2,200,{d}) causal={causal} tile 64x64 input-dtype accumulation (host padding)")
+        host = run_gpu(q, k, v, causal=causal, tile_m=64, tile_n=64, accum_mode="fp16")
         assert host.shape == (1, 2, 200, d) and not host.is_contiguous()
-        check_close(as_f32(host), ref, "float16", what=f"host pad D={d}")
+        check_close(as_f32(host), ref, "float16", tol=LOWP_TOL["float16"], what=f"host pad D={d}")
 
 
 @pytest.mark.parametrize("d,dtype,causal,s", [
@@ -223,6 +228,41 @@ def test_eight_wave_d160(gpu, d, dtype, causal, s):
     out = sdpa(*bshd, causal=causal)
     torch.cuda.synchronize()
     check_close(as_f32(out, rows), ref, dtype, what=f"eight-wave D={d} BSHD")
+
+
+@pytest.mark.parametrize("tn", [64, 128])
+@pytest.mark.parametrize("s,causal,dtype", [
+    (64, True, "float16"), (100, False, "bfloat16"), (320, True, "bfloat16"), (448, False, "float16"),
+    (1000, True, "float16"), (1536, False, "bfloat16"),
+])
+def test_eight_wave_64_row_tiles(gpu, tn, s, causal, dtype):
+    """Tiles (64, tn) with fp32 accumulation run the 64-row eight-wave kernel (four key
+    slices per row block, merged at the end): lengths that are multiples of 64 but not of
+    the 128-key step (320, 448: the tail-masked variant), ragged ones, D = 64 and 128, and
+    narrower head dims padded in place (D = 48 and 96); [B,S,H,D] views for one case."""
+    import torch
+
+    from tiledattention import _lib, sdpa
+
+    for d in (64, 128):
+        assert _lib.kernel_symbol(dtype=_lib.TA_BF16, head_dim=d, tile_m=64, tile_n=tn, causal=causal,
+                                  tail=True, accum=_lib.TA_ACC_FP32)[1].startswith("ta_fwd_pp64_")
+    for d in (64, 128, 48, 96):
+        q, k, v = inputs((2, 3, s, d), dtype, 6400 + s + d + tn)
+        say(f"64-row eight-wave {dtype} (2,3,{s},{d}) causal={causal} tiles=(64,{tn})")
+        out = run_gpu(q, k, v, causal=causal, tile_m=64, tile_n=tn)
+        assert out.shape == (2, 3, s, d)
+        ref = oracle_f32(q, k, v, causal=causal)
+        check_close(as_f32(out), ref, dtype, what=f"64-row D={d}")
+        if d == 96 and s == 1000:
+            dev = torch.device("cuda:0")
+            bshd = [t.transpose(1, 2).contiguous().to(dev).transpose(1, 2) for t in (q, k, v)]
+            say(f"64-row eight-wave {dtype} (2,3,{s},{d}) [B,S,H,D] views")
+            from tests.parity_util import knobs
+            with knobs(tile_m=64, tile_n=tn):
+                out = sdpa(*bshd, causal=causal)
+            torch.cuda.synchronize()
+            check_close(as_f32(out), ref, dtype, what="64-row BSHD")
 
 
 @pytest.mark.parametrize("d", [144, 200])

@@ -244,3 +244,42 @@ def test_sched_env(monkeypatch):
         monkeypatch.setenv("TILEDATTN_SCHED", bad)
         with pytest.raises(ValueError, match="TILEDATTN_SCHED"):
             ff._resolve_sched(n_blocks=512, causal=True, tile_m=128, tile_n=64)
+
+
+# ---------------------------------------------------------------- default tile on gfx950
+
+@pytest.mark.parametrize("s,d,n_bh,accum,expected", [
+    (8192, 128, 8, "fp32", (128, 64)),   # C3: 1024 blocks of 64 rows > 256 CUs
+    (2048, 128, 8, "fp32", (64, 64)),    # 256 blocks of 64 rows fit the CUs once
+    (1024, 128, 8, "fp32", (64, 64)),
+    (2049, 128, 8, "fp32", (128, 64)),   # 8 * 33 > 256
+    (1024, 128, 32, "fp32", (128, 64)),  # B2 H16: 512 blocks of 64 rows
+    (512, 64, 8, "fp32", (64, 64)),
+    (512, 96, 8, "fp32", (64, 64)),      # kernel head dim 128 (in-place padding)
+    (512, 160, 8, "fp32", (128, 64)),    # no 64-row eight-wave kernel above D = 128
+    (512, 128, 8, "fp16", (128, 64)),    # input-dtype accumulation: the four-wave kernels
+    (512, 128, 0, "fp32", (128, 64)),    # no head count given
+])
+def test_default_tile_prefers_64_rows_when_one_wave_of_blocks_fits(s, d, n_bh, accum, expected):
+    assert ff._default_tile_config_for_shape_gfx950(seq_len=s, head_dim=d, causal=True, n_bh=n_bh,
+                                                    accum_mode=accum) == expected
+
+
+def test_64_row_tiles_select_the_eight_wave_kernel():
+    """Tiles (64, 64) / (64, 128) with fp32 accumulation at D = 64 / 128 run ta_fwd_pp64_*;
+    the tail-masked variant whenever S is not a multiple of the 128-key step."""
+    f, sym = _lib.kernel_symbol(dtype=_lib.TA_BF16, head_dim=128, tile_m=64, tile_n=128, causal=True,
+                                tail=False, accum=_lib.TA_ACC_FP32)
+    assert (f, sym) == ("attn_fwd_pp.hsaco", "ta_fwd_pp64_bf16_d128_c1_t0")
+    assert _lib.kernel_symbol(dtype=_lib.TA_FP16, head_dim=64, tile_m=64, tile_n=64, causal=False,
+                              tail=True, accum=_lib.TA_ACC_FP32)[1] == "ta_fwd_pp64_f16_d64_c0_t1"
+    assert _lib.kernel_symbol(dtype=_lib.TA_FP16, head_dim=64, tile_m=64, tile_n=64, causal=False,
+                              tail=True, accum=_lib.TA_ACC_INPUT)[1].startswith("ta_fwd_f16_d64_m64_n64")
+    assert _lib.kernel_symbol(dtype=_lib.TA_FP16, head_dim=160, tile_m=64, tile_n=64, causal=False,
+                              tail=True, accum=_lib.TA_ACC_FP32)[1].startswith("ta_fwd_f16_d160_m64_n64")
+    tm = dict(tile_m=64, tile_n=64, accum=_lib.TA_ACC_FP32, head_dim=128)
+    assert not _lib.tail_masked(seq_len=512, **tm)
+    assert _lib.tail_masked(seq_len=320, **tm)   # multiple of 64, not of the 128-key step
+    assert _lib.tail_masked(seq_len=512, aligned=False, **tm)
+    four = dict(tile_m=64, tile_n=64, accum=_lib.TA_ACC_INPUT, head_dim=128)
+    assert not _lib.tail_masked(seq_len=320, **four)  # four-wave kernels step by the tile

@@ -173,14 +173,18 @@ def test_split_knob_rejects(monkeypatch, raw, capable, msg):
 
 def test_split_capability_rule():
     ok = dict(tile_m=128, tile_n=64, accum_code=_lib.TA_ACC_FP32, kernel_head_dim=128)
-    rule = flash_fwd._eight_wave_kernel
+    rule = flash_fwd._split_capable
     assert rule(**ok)
     assert rule(**{**ok, "kernel_head_dim": 64})
     assert rule(**{**ok, "kernel_head_dim": 160})
     assert not rule(**{**ok, "kernel_head_dim": 256})
-    assert not rule(**{**ok, "tile_m": 64})
+    assert not rule(**{**ok, "tile_m": 64})  # the 64-row eight-wave kernel has no split form
     assert rule(**{**ok, "tile_n": 128})  # the eight-wave step is 128 keys
     assert not rule(**{**ok, "accum_code": _lib.TA_ACC_INPUT})
+    # in-place padding (d_real) exists on both eight-wave forms
+    ew = flash_fwd._eight_wave_kernel
+    assert ew(**ok) and ew(**{**ok, "tile_m": 64}) and ew(**{**ok, "tile_m": 64, "tile_n": 128})
+    assert not ew(**{**ok, "tile_m": 64, "kernel_head_dim": 160})
     with pytest.raises(ValueError, match="D <= 160"):
         _lib.kernel_symbol(dtype=_lib.TA_BF16, head_dim=256, tile_m=128, tile_n=64, causal=True,
                            tail=False, accum=_lib.TA_ACC_FP32, split=True)

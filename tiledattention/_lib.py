@@ -47,17 +47,40 @@ def uses_pairs(*, causal: bool, head_dim: int, tile_m: int, tile_n: int, accum: 
     return sched == 1 and n_bh * n_qblk >= 2 * compute_units
 
 
+def eight_wave_family(*, tile_m: int, tile_n: int, accum: int, head_dim: int) -> bool:
+    """The eight-wave kernels (attn_fwd_pp.hsaco): fp32 accumulation with tiles (128, 64) /
+    (128, 128) at D <= 160, or tiles (64, 64) / (64, 128) at D = 64 or 128; the same rule as
+    eight_wave_family() in csrc/tiledattn.cpp."""
+    if accum != TA_ACC_FP32 or tile_n not in (64, 128):
+        return False
+    return (tile_m == 128 and head_dim <= 160) or (tile_m == 64 and head_dim in (64, 128))
+
+
+def tail_masked(*, seq_len: int, tile_m: int, tile_n: int, accum: int, head_dim: int,
+                aligned: bool = True) -> bool:
+    """Whether the C ABI launches the tail-masked variant; unmasked_tail() in
+    csrc/tiledattn.cpp: S a multiple of both tiles (and of the 128-key step on the
+    eight-wave kernels) and the aligned fast path allowed."""
+    steps = not eight_wave_family(tile_m=tile_m, tile_n=tile_n, accum=accum, head_dim=head_dim) \
+        or seq_len % 128 == 0
+    return not (aligned and seq_len % tile_m == 0 and seq_len % tile_n == 0 and steps)
+
+
 def kernel_symbol(*, dtype: int, head_dim: int, tile_m: int, tile_n: int, causal: bool,
                   tail: bool, accum: int, split: bool = False, pair: bool = False) -> tuple[str, str]:
     """(code object file, kernel symbol) the C ABI launches for a configuration; the same
     rule as kernel_id() in csrc/tiledattn.cpp (used to label measurements).  ``split``
     names the split-key-range kernel (its merge kernel is ta_fwd_merge_<dt>_d<D>_c<c>),
-    ``pair`` the causal pair kernel (``uses_pairs``)."""
+    ``pair`` the causal pair kernel (``uses_pairs``).  ``tail`` is the variant the C ABI
+    picks (``tail_masked``)."""
     dt = "bf16" if dtype == TA_BF16 else "f16"
     c, t = int(bool(causal)), int(bool(tail))
     if tile_m == 128 and tile_n in (64, 128) and accum == TA_ACC_FP32 and head_dim <= 160:
         kind = "pp_split" if split else ("pp_pair" if pair else "pp")
         return "attn_fwd_pp.hsaco", f"ta_fwd_{kind}_{dt}_d{head_dim}_c{c}_t{t}"
+    if (tile_m == 64 and tile_n in (64, 128) and accum == TA_ACC_FP32 and head_dim in (64, 128)
+            and not split and not pair):
+        return "attn_fwd_pp.hsaco", f"ta_fwd_pp64_{dt}_d{head_dim}_c{c}_t{t}"
     if split:
         raise ValueError("split key ranges exist for tiles (128, 64) and (128, 128), fp32 "
                          "accumulation, D <= 160")

@@ -209,14 +209,26 @@ def _use_unmasked_tail_kernel(*, seq_len: int, tile_m: int, tile_n: int) -> bool
     return seq_len % tile_m == 0 and seq_len % tile_n == 0
 
 
-def _default_tile_config_for_shape_gfx950(*, seq_len: int, head_dim: int, causal: bool) -> tuple[int, int]:
+def _default_tile_config_for_shape_gfx950(*, seq_len: int, head_dim: int, causal: bool,
+                                         n_bh: int = 0, accum_mode: str = "fp32") -> tuple[int, int]:
     """Default (TILE_M, TILE_N) on gfx950 when neither env knob is set.
 
-    128 query rows per workgroup.  With fp32 accumulation this shape runs the eight-wave
-    kernel (two waves per SIMD splitting every 128-key step, one workgroup per CU); with
-    input-dtype accumulation the four-wave kernel with 64-key tiles (two workgroups per CU).
+    128 query rows per workgroup: with fp32 accumulation the eight-wave kernel (two waves per
+    SIMD splitting every 128-key step, one workgroup per CU), with input-dtype accumulation
+    the four-wave kernel with 64-key tiles (two workgroups per CU).  When the 64-row blocks
+    of all ``n_bh`` heads fit the CUs in one wave (B*H*ceil(S/64) <= CUs; fp32, kernel head
+    dim 64 or 128), 64 rows instead: the 64-row eight-wave kernel halves each block's key
+    loop and the grid is still one workgroup per CU (B1 H8 bf16: causal S=1024 15.0 -> 12.0
+    us, S=2048 23.5 -> 18.8; non-causal S=1024 14.4 -> 11.9, S=2048 23.3 -> 20.3; D=64 causal
+    S=2048 18.2 -> 13.5).  With more blocks than CUs, the second block of a CU pays the
+    fixed cost of a workgroup again (B2 H16 S1024 causal: 16.4 -> 21.4 us), so 128 rows.
+    The caller keeps 128 rows where the 128-row kernel would split key ranges
+    (``_split_preferred``).
     """
-    del seq_len, head_dim, causal
+    del causal
+    if (accum_mode == "fp32" and 0 < head_dim <= 128 and n_bh > 0 and seq_len > 0
+            and n_bh * ((seq_len + 63) // 64) <= _CU_COUNT):
+        return 64, 64
     return 128, 64
 
 
@@ -235,21 +247,20 @@ _CU_COUNT = 256  # MI355X
 
 def _workgroups_per_cu(*, tile_m: int, tile_n: int, accum_code: int, head_dim: int = 128,
                        causal: bool = True) -> int:
-    """Workgroups of one launch resident on a CU at once: two for the four-wave 128x64
-    kernel (input-dtype accumulation), for the four-wave 64x128 kernel (one LDS stage; four
-    for 64x64 up to D = 128, two above) and
-    for the non-causal eight-wave kernel at kernel head dim 64 (built for 128 VGPRs, 64 KiB
-    of LDS), one otherwise (the eight-wave kernel at D = 128 or causal, and the other tile
-    shapes, fill a CU's LDS or registers)."""
+    """Workgroups of one launch resident on a CU at once: two for the non-causal eight-wave
+    kernels at kernel head dim 64 (built for 128 VGPRs, 64 KiB of LDS), one for the other
+    eight-wave kernels (their stages fill a CU's LDS); for the four-wave kernels two at
+    128x64 (input-dtype accumulation), two at 64x128 (one LDS stage), four at 64x64 up to
+    D = 128 and two above (one LDS stage), one otherwise (LDS or registers)."""
+    if _eight_wave_kernel(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code,
+                          kernel_head_dim=head_dim):
+        return 2 if head_dim <= 64 and not causal else 1
     if (tile_m, tile_n) == (128, 64) and accum_code == _lib.TA_ACC_INPUT:
         return 2
     if (tile_m, tile_n) == (64, 128) and head_dim <= 128:
         return 2  # one LDS stage (76 KiB at D = 128), one wave per SIMD
     if (tile_m, tile_n) == (64, 64):
         return 4 if head_dim <= 128 else 2  # one LDS stage; two waves per SIMD up to D = 128
-    if _eight_wave_kernel(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code,
-                          kernel_head_dim=head_dim) and head_dim <= 64 and not causal:
-        return 2
     return 1
 
 
@@ -300,12 +311,19 @@ _SPLIT_PLANS: dict[tuple[int, int, int, int], int] = {}
 
 
 def _eight_wave_kernel(*, tile_m: int, tile_n: int, accum_code: int, kernel_head_dim: int) -> bool:
-    """Whether the configuration runs the eight-wave kernel (tile (128, 64) or (128, 128),
-    fp32 accumulation, kernel head dim 64, 128 or 160): the one with split key ranges and
-    in-place padding of narrower head dims.  Its workgroup step is 128 rows x 128 keys, 64
-    keys per wave group, so it serves both 128-row tiles."""
-    return (tile_m == 128 and tile_n in (64, 128) and accum_code == _lib.TA_ACC_FP32
-            and kernel_head_dim <= 160)
+    """Whether the configuration runs an eight-wave kernel, the ones with in-place padding of
+    narrower head dims: fp32 accumulation with tile (128, 64) or (128, 128) at kernel head
+    dim 64, 128 or 160 (workgroup step 128 rows x 128 keys, 64 keys per wave group, so it
+    serves both 128-row tiles), or with tile (64, 64) or (64, 128) at 64 or 128 (the
+    64-row form, the same 128-key steps)."""
+    return _lib.eight_wave_family(tile_m=tile_m, tile_n=tile_n, accum=accum_code,
+                                  head_dim=kernel_head_dim)
+
+
+def _split_capable(*, tile_m: int, tile_n: int, accum_code: int, kernel_head_dim: int) -> bool:
+    """Whether split key ranges exist: the 128-row eight-wave kernel."""
+    return tile_m == 128 and _eight_wave_kernel(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code,
+                                                kernel_head_dim=kernel_head_dim)
 
 
 
@@ -336,6 +354,27 @@ def _resolve_split(lib, args: _lib.FwdArgs, *, capable: bool) -> int:
             "of at most 160."
         )
     return chunk
+
+
+def _split_preferred(lib, q, batch: int, heads: int, seq_len: int, head_dim: int, causal: bool,
+                     torch_mod) -> bool:
+    """Whether the 128-row kernel runs split key ranges for this shape (a forced chunk
+    length, or the library's dispatch model under ``TILEDATTN_SPLIT=auto``): the default
+    tile then stays at 128 rows, the tile the split path exists for."""
+    raw = os.getenv("TILEDATTN_SPLIT", "").strip().lower()
+    if raw in ("0", "off"):
+        return False
+    if raw not in ("", "auto"):
+        return True
+    kernel_head_dim, _ = _resolve_kernel_head_dim_gfx950(head_dim)
+    args = _lib.FwdArgs()
+    args.B, args.H, args.S, args.D = batch, heads, seq_len, kernel_head_dim
+    args.causal = int(causal)
+    args.dtype = _dtype_code_for_torch_dtype(q.dtype)
+    args.tile_m, args.tile_n = 128, 64
+    args.accum = _lib.TA_ACC_FP32
+    args.device = q.device.index if q.device.index is not None else torch_mod.cuda.current_device()
+    return _resolve_split(lib, args, capable=True) > 0
 
 
 def _raise_for_status(lib, status: int) -> None:
@@ -451,8 +490,10 @@ def _build_plan(torch_mod, lib, q, k, v, causal: bool, tile: tuple[int, int] | N
         _check_tile_supported(tile_m, tile_n)
     else:
         tile_m, tile_n = _default_tile_config_for_shape_gfx950(
-            seq_len=seq_len, head_dim=head_dim, causal=causal
+            seq_len=seq_len, head_dim=head_dim, causal=causal, n_bh=bh, accum_mode=accum_mode
         )
+        if tile_m == 64 and _split_preferred(lib, q, batch, heads, seq_len, head_dim, causal, torch_mod):
+            tile_m, tile_n = 128, 64
 
     chunk_plan = _resolve_chunk_plan(head_dim)
     kernel_head_dim, pad_dim = _resolve_kernel_head_dim_gfx950(head_dim)
@@ -534,8 +575,8 @@ def _build_plan(torch_mod, lib, q, k, v, causal: bool, tile: tuple[int, int] | N
     args.sched = _resolve_sched(n_blocks=bh * n_qblk, causal=causal, tile_m=tile_m, tile_n=tile_n,
                                 accum_code=accum_code, head_dim=kernel_head_dim)
 
-    capable = _eight_wave_kernel(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code,
-                                 kernel_head_dim=kernel_head_dim)
+    capable = _split_capable(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code,
+                             kernel_head_dim=kernel_head_dim)
     plan.chunk = _resolve_split(lib, args, capable=capable)
     plan.ws_bytes = 0
     if plan.chunk:

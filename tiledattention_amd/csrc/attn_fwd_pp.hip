@@ -57,13 +57,18 @@ __device__ static inline int pp_swz_v(int row) {
 constexpr int pp_stage_bytes(int d) { return kPPKeys * 2 * d; }
 
 // One query block (or, with SPLIT, one chunk of its key steps) on the whole workgroup: the
-// prologue, the key loop and the merge of the two key halves with the output stores.
-template <int DT, int D, bool CAUSAL, bool TAIL, bool SPLIT>
+// prologue, the key loop and the merge of the key slices with the output stores.  TMR is
+// the block's query rows: 128 (four 32-row blocks; a wave group's four waves take one row
+// block each and the group's 64 keys of every step), or 64 (two row blocks; a group's
+// waves are two row blocks x two 32-key slots, so four waves share each row block).
+template <int DT, int D, bool CAUSAL, bool TAIL, bool SPLIT, int TMR = 128>
 __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const WorkItem wi, char* lds_k0,
                                                   char* lds_k1, char* lds_v0, char* lds_v1) {
-  constexpr int TM = 128;            // query rows per workgroup
+  constexpr int TM = TMR;            // query rows per workgroup
   constexpr int TK = 128;            // keys per workgroup step (64 per wave group)
-  constexpr int KB = 2;              // 32-key blocks per wave per step
+  constexpr int NRB = TM / 32;       // 32-row blocks
+  constexpr int NKS = 4 / NRB;       // key slots of a group's 64 keys (1 or 2)
+  constexpr int KB = 2 / NKS;        // 32-key blocks per wave per step
   // A stage holds 128 key rows: the first DA = min(D, 128) columns of each row in a main
   // part (rows of 2 DA bytes), the rest (D = 160: 32 columns) in a tail part of 64-byte
   // rows behind it, so both parts have power-of-two rows.
@@ -84,7 +89,8 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   constexpr int NLDT = DT2 ? 1 : 0;  // tail loads (a group's 64 tail rows are 4 KiB)
   constexpr int NLDS = NLD + NLDT;   // loads per wave per tensor per step (own half)
   static_assert(STAGE_A % (8 * 1024) == 0, "stage must split over the eight waves");
-  static_assert(TM == kPPRows && TK == kPPKeys, "grid numbering assumes 128 x 128 steps");
+  static_assert(TK == kPPKeys && (TM == kPPRows || TM == 64), "steps of 128 keys, blocks of 128 or 64 rows");
+  static_assert(TM == 128 || (!SPLIT && (D == 64 || D == 128)), "64-row blocks: whole rows, D 64 or 128");
   // Raised MFMA-cluster priority only in the kernels built for two workgroups per CU (the
   // non-causal D = 64 whole-row ones, TA_PP_WAVES below).
   constexpr bool kPrioMfma = !SPLIT && D == 64 && !CAUSAL;
@@ -99,7 +105,9 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps it in SGPRs
   const int grp = wave >> 2;  // key half of every step
-  const int wr = wave & 3;    // row block
+  const int wr = wave & 3;    // wave within its group
+  const int rb = wr % NRB;    // row block
+  const int ks = wr / NRB;    // key slot within the group's 64 keys of a step
   const int l32 = lane & 31;
   const int hl = lane >> 5;
 
@@ -120,7 +128,7 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   const int v_rb = (int)p.v_ss * 2;
 
   const int q0 = qt * TM;
-  const int wq0 = q0 + wr * 32;  // first query row of this wave
+  const int wq0 = q0 + rb * 32;  // first query row of this wave
   const int my_q = wq0 + l32;    // this lane's query row
 
   // ---- Q fragment: B operand of S^T = K Q^T, kept for the whole key loop ------------
@@ -134,19 +142,20 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   // block needs.
   const int t_end = SPLIT ? wi.t_end : ((CAUSAL ? min(S, q0 + TM) : S) + TK - 1) / TK;
   const int wave_kv_end = CAUSAL ? min(S, wq0 + 32) : S;
-  const int koff = 64 * grp;  // this wave's keys in a step: [TK * t + koff, + 64)
+  const int gkoff = 64 * grp;              // the group's keys in a step: [TK t + gkoff, + 64)
+  const int koff = gkoff + 32 * KB * ks;   // this wave's: [TK t + koff, + 32 KB)
 
   // ---- staging: HBM -> LDS directly -------------------------------------------------
   // A stage is 1 KiB chunks g; lane l of the wave instruction that fills chunk g writes
   // physical chunk l % CPR of row g * RPL + l / CPR, so it loads logical chunk
   // (l % CPR) ^ swz(row) of that row.  Each wave group reads only its own half of a stage
-  // (rows koff .. koff + 63) and loads it itself: wave (grp, wr) fills the chunks
+  // (rows gkoff .. gkoff + 63) and loads it itself: wave (grp, wr) fills the chunks
   // g = 64 grp / RPL + wr + 4 i.  swz depends on g only through g & 3 (K, D = 128) or g & 1
   // (K, D = 64), fixed by wr, so one per-lane byte offset plus 4 i RPL rows serves every
   // load of a tensor.  One buffer resource per step starts at the step's first key; rows
   // past S are outside it and read as zero, and a step past the last gets an empty
   // resource (its loads write zeros into a stage half nobody reads any more).
-  const int ld_g0 = koff / RPL + wr;  // first chunk this wave fills
+  const int ld_g0 = gkoff / RPL + wr;  // first chunk this wave fills
   const int ld_row = ld_g0 * RPL + lane / CPR;
   const int ld_pc = lane % CPR;
   // A logical chunk at or past d_real gets an offset of 2^31 or more: every buffer resource
@@ -157,12 +166,12 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   const int lcv = ld_pc ^ pp_swz_v<DA>(ld_row);
   const int kvo = 8 * lck < d_real ? ld_row * k_rb + (lck << 4) : kZeroChunk;
   const int vvo = 8 * lcv < d_real ? ld_row * v_rb + (lcv << 4) : kZeroChunk;
-  // Tail part: wave (grp, wr) fills the group's tail rows koff + 16 wr .. + 15, lane l
+  // Tail part: wave (grp, wr) fills the group's tail rows gkoff + 16 wr .. + 15, lane l
   // writing physical chunk l % 4 of row l / 4 of them.  K's tail chunks are swizzled with
   // (row >> 2) & 3 (a b128 read pass covers 16 consecutive rows at one chunk, rows 256
   // bytes apart repeat every 4); V's tail needs none (a transposed read pass covers 4 rows
   // x 64 bytes).  For these rows (row >> 2) & 3 = (l >> 4) & 3.
-  const int tl_row = koff + 16 * wr + (lane >> 2);
+  const int tl_row = gkoff + 16 * wr + (lane >> 2);
   const int tl_lck = (lane & 3) ^ ((lane >> 4) & 3);
   const int tl_lcv = lane & 3;
   const int tkvo = DA + 8 * tl_lck < d_real ? tl_row * k_rb + 2 * DA + (tl_lck << 4) : kZeroChunk;
@@ -184,7 +193,7 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
     }
     if constexpr (NLDT != 0) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          r, (__attribute__((address_space(3))) void*)(stage + STAGE_A + koff * RBT + wr * 1024),
+          r, (__attribute__((address_space(3))) void*)(stage + STAGE_A + gkoff * RBT + wr * 1024),
           16, tvo, 0, 0, 0);
     }
   };
@@ -203,7 +212,7 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
     }
     if constexpr (NLDT != 0) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          r, (__attribute__((address_space(3))) void*)(stage + STAGE_A + koff * RBT + wr * 1024),
+          r, (__attribute__((address_space(3))) void*)(stage + STAGE_A + gkoff * RBT + wr * 1024),
           16, tqvo, 0, 0, 0);
     }
   };
@@ -245,7 +254,7 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   auto key0 = [&](int t) { return t * TK + koff; };
   auto all_active = [&](int t) { return key0(t) + 32 * (KB - 1) < wave_kv_end; };
   auto no_mask = [&](int t) {
-    return (!CAUSAL || key0(t) + 63 <= wq0) && (!TAIL || key0(t) + 64 <= S);
+    return (!CAUSAL || key0(t) + 32 * KB - 1 <= wq0) && (!TAIL || key0(t) + 32 * KB <= S);
   };
 
   f32x16 s[KB];        // S^T blocks of the step whose softmax comes next
@@ -460,7 +469,7 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   // softmax cluster, like the loads of every MFMA cluster.
   static_assert(2 * NLDS < 16, "vmcnt field");
   dma(kp, p.k_ss, k_rb, kvo, tkvo, t_beg, lds_k0);
-  dma_q(lds_v1);
+  if (TM == 128 || grp == 0) dma_q(lds_v1);  // 64-row blocks: group 0's chunks hold every row
   dma(kp, p.k_ss, k_rb, kvo, tkvo, t_beg + 1, lds_k1);
   dma(vp, p.v_ss, v_rb, vvo, tvvo, t_beg, lds_v0);
   __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * NLDS));
@@ -468,7 +477,7 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   // Q fragment from lds_v1 (rows 32 wr + l32, read like a K operand); lds_v1 receives V_1
   // only in the first MFMA cluster, at least two barriers later.
   {
-    const int qr = 32 * wr + l32;
+    const int qr = 32 * rb + l32;
 #pragma unroll
     for (int kk = 0; kk < DK; ++kk) {
       const char* ap = kk < DKA ? lds_v1 + qr * RB + ((k_rd - (koff + l32) * RB) ^ (32 * kk))
@@ -642,8 +651,91 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
     }
   };
 
-  // ---- merge the two key halves of each row block, O = acc / l ---------------------------
-  if constexpr (DB % 2 == 0) {
+  // ---- 64-row blocks: merge the four key slices of each row block, O = acc / l ----------
+  // Waves (g, rb + 2 k) of both groups g and key slots k hold the same 32 rows over
+  // different keys.  Part P = 2 g + k of them merges the lane's 16-byte O^T chunks
+  // [P DB, (P + 1) DB) (chunk u = 4 db + j holds d = 32 db + 8 j + 4 hl + e, e < 4): each
+  // wave sends the other three the chunks they merge, in slots ordered by part (its own
+  // part skipped), plus its (m, l); region of wave w: half w % 2 of stage w / 2, (m, l)
+  // behind both halves.  The stages are free: every load has landed and every read has
+  // retired before the last barrier.
+  if constexpr (TM == 64) {
+    constexpr int CPW = DB;                // chunks a part merges
+    constexpr int RG = 3 * CPW * 64 * 16;  // bytes a wave sends
+    static_assert(2 * RG + 2 * 512 <= STAGE, "exchange regions fit the stages");
+    auto stage_of = [&](int i) -> char* {
+      return i == 0 ? lds_k0 : i == 1 ? lds_k1 : i == 2 ? lds_v0 : lds_v1;
+    };
+    const int part = 2 * grp + ks;
+    {
+      f32x4* mine = (f32x4*)(stage_of(wave >> 1) + (wave & 1) * RG);
+#pragma unroll
+      for (int u = 0; u < 4 * DB; ++u) {
+        const int tp = u / CPW;  // the part that merges chunk u
+        if (tp == part) continue;
+        const int slot = tp < part ? tp : tp - 1;
+        mine[(slot * CPW + u % CPW) * 64 + lane] =
+            f32x4{o_acc[u / 4][4 * (u % 4)], o_acc[u / 4][4 * (u % 4) + 1], o_acc[u / 4][4 * (u % 4) + 2],
+                  o_acc[u / 4][4 * (u % 4) + 3]};
+      }
+      float* ml = (float*)(stage_of(wave >> 1) + 2 * RG + (wave & 1) * 512);
+      ml[lane] = m_run;
+      ml[64 + lane] = l_part;
+    }
+    barrier();
+    auto merge_part = [&](auto p_tag) {
+      constexpr int P = decltype(p_tag)::value;
+      f32x4 x[3][CPW];
+      float mq[3], lq[3];
+#pragma unroll
+      for (int n = 0; n < 3; ++n) {
+        const int q = n < P ? n : n + 1;  // partner part
+        const int wq = 4 * (q >> 1) + rb + 2 * (q & 1);
+        const f32x4* src = (const f32x4*)(stage_of(wq >> 1) + (wq & 1) * RG);
+        const int slot = P < q ? P : P - 1;  // our part's slot in the partner's region
+#pragma unroll
+        for (int cc = 0; cc < CPW; ++cc) x[n][cc] = src[(slot * CPW + cc) * 64 + lane];
+        const float* ml = (const float*)(stage_of(wq >> 1) + 2 * RG + (wq & 1) * 512);
+        mq[n] = ml[lane];
+        lq[n] = ml[64 + lane];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      const float m = vmax(vmax(m_run, mq[0]), vmax(mq[1], mq[2]));
+      const float a0 = fast_exp2((m_run - m) * c);
+      float an[3];
+#pragma unroll
+      for (int n = 0; n < 3; ++n) an[n] = fast_exp2((mq[n] - m) * c);
+      float la, lb;
+      swap32(l_part * a0 + (lq[0] * an[0] + lq[1] * an[1]) + lq[2] * an[2], la, lb);
+      const float inv = 1.0f / (la + lb);
+      const float w0 = a0 * inv;
+      float wn[3];
+#pragma unroll
+      for (int n = 0; n < 3; ++n) wn[n] = an[n] * inv;
+      if (TAIL && my_q >= S) return;
+      uint16_t* orow = op + (int64_t)my_q * p.o_ss;
+#pragma unroll
+      for (int cc = 0; cc < CPW; ++cc) {
+        constexpr int U0 = P * CPW;
+        const int u = U0 + cc;
+        f32x4 o4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          o4[e] = o_acc[u / 4][4 * (u % 4) + e] * w0 + (x[0][cc][e] * wn[0] + x[1][cc][e] * wn[1]) +
+                  x[2][cc][e] * wn[2];
+        }
+        const int d = 32 * (u / 4) + 8 * (u % 4) + 4 * hl;
+        if (d < d_real) *(u32x2*)(orow + d) = u32x2{DTy::pack(o4[0], o4[1]), DTy::pack(o4[2], o4[3])};
+      }
+    };
+    switch (part) {
+      case 0: merge_part(std::integral_constant<int, 0>{}); break;
+      case 1: merge_part(std::integral_constant<int, 1>{}); break;
+      case 2: merge_part(std::integral_constant<int, 2>{}); break;
+      default: merge_part(std::integral_constant<int, 3>{}); break;
+    }
+    return;
+  } else if constexpr (DB % 2 == 0) {
     // Both groups merge, each half of the d blocks (group 0 blocks [0, DB/2), group 1 the
     // rest): every wave sends its partner (the wave of the other group with the same row
     // block) the blocks the partner merges, as 16-byte chunks, and its (m, l).  The stages
@@ -812,7 +904,7 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
 // heaviest first, so each CU takes the next tile when its current one ends and heavy
 // tiles pair with light ones.  Split items cover a chunk of key steps of a block and
 // leave a partial (slot >= 0) when the block has more than one chunk.
-template <int DT, int D, bool CAUSAL, bool TAIL, bool SPLIT, bool PAIR>
+template <int DT, int D, bool CAUSAL, bool TAIL, bool SPLIT, bool PAIR, int TMR = 128>
 __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   constexpr int STAGE = pp_stage_bytes(D);
   // One array per (tensor, stage): the stage of every access is a compile-time constant
@@ -838,7 +930,7 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
     const WorkItem wi = SPLIT ? split_item(blockIdx.x, p.n_bh, p.split_items, p.sched, CAUSAL,
                                            p.split_c, p.split_ns, p.split_slots, p.S)
                               : whole_item(blockIdx.x, p.n_bh, p.n_qblk, p.sched, CAUSAL);
-    attn_fwd_pp_block<DT, D, CAUSAL, TAIL, SPLIT>(p, wi, lds_k0, lds_k1, lds_v0, lds_v1);
+    attn_fwd_pp_block<DT, D, CAUSAL, TAIL, SPLIT, TMR>(p, wi, lds_k0, lds_k1, lds_v0, lds_v1);
   }
 }
 
@@ -922,6 +1014,20 @@ __device__ __forceinline__ void attn_merge_body(const FwdParams& p) {
     ta::attn_fwd_pp_body<DT, D, true, (T != 0), false, true>(p);                          \
   }
 
+// 64-row blocks (tiles (64, 64) and (64, 128) with fp32 accumulation, D = 64 and 128):
+// ta_fwd_pp64_<f16|bf16>_d<D>_c<0|1>_t<0|1>, the same residency as the 128-row kernels.
+#define TA_PP64_DEFINE(DTN, DT, D, C, T)                                                   \
+  extern "C" __global__ void __launch_bounds__(512)                                       \
+      __attribute__((amdgpu_waves_per_eu(TA_PP_WAVES(D, C), TA_PP_WAVES(D, C))))           \
+      ta_fwd_pp64_##DTN##_d##D##_c##C##_t##T(ta::FwdParams p) {                            \
+    ta::attn_fwd_pp_body<DT, D, (C != 0), (T != 0), false, false, 64>(p);                 \
+  }
+#define TA_PP64_DEFINE_CT(DTN, DT, D) \
+  TA_PP64_DEFINE(DTN, DT, D, 0, 0)    \
+  TA_PP64_DEFINE(DTN, DT, D, 0, 1)    \
+  TA_PP64_DEFINE(DTN, DT, D, 1, 0)    \
+  TA_PP64_DEFINE(DTN, DT, D, 1, 1)
+
 // Merge kernels of the split path: ta_fwd_merge_<f16|bf16>_d<D>_c<0|1>, merge_threads(D)
 // threads.
 #define TA_MERGE_DEFINE(DTN, DT, D, C)                                                     \
@@ -952,3 +1058,7 @@ TA_PP_PAIR_DEFINE(bf16, 1, 64, 0)
 TA_PP_PAIR_DEFINE(bf16, 1, 64, 1)
 TA_PP_PAIR_DEFINE(bf16, 1, 128, 0)
 TA_PP_PAIR_DEFINE(bf16, 1, 128, 1)
+TA_PP64_DEFINE_CT(f16, 0, 64)
+TA_PP64_DEFINE_CT(f16, 0, 128)
+TA_PP64_DEFINE_CT(bf16, 1, 64)
+TA_PP64_DEFINE_CT(bf16, 1, 128)

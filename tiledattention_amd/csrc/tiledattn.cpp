@@ -97,6 +97,19 @@ bool eight_wave(int64_t tm, int64_t tn, int64_t accum, int64_t d) {
   return tm == 128 && (tn == 64 || tn == 128) && accum == TA_ACC_FP32 && d <= 160;
 }
 
+// Its 64-row form (ta_fwd_pp64_*) serves the 64-row tiles with fp32 accumulation at D = 64
+// and 128: the same 128-key steps, each group's 64 keys split between two waves per row
+// block, and no split key ranges or causal pairs.
+bool eight_wave64(int64_t tm, int64_t tn, int64_t accum, int64_t d) {
+  return tm == 64 && (tn == 64 || tn == 128) && accum == TA_ACC_FP32 && (d == 64 || d == 128);
+}
+
+// Either form: direct-to-LDS staging of Q, K and V (in-place padding of narrower head dims
+// through d_real; 128-key steps).
+bool eight_wave_family(int64_t tm, int64_t tn, int64_t accum, int64_t d) {
+  return eight_wave(tm, tn, accum, d) || eight_wave64(tm, tn, accum, d);
+}
+
 KernelId kernel_id(int dtype, int d, int tm, int tn, int causal, int tail, int accum) {
   const char* dt = dtype == TA_BF16 ? "bf16" : "f16";
   char buf[96];
@@ -104,6 +117,10 @@ KernelId kernel_id(int dtype, int d, int tm, int tn, int causal, int tail, int a
     // Eight waves: two per SIMD sharing the rows of a 32-row block, splitting every
     // 128-key step between them.
     snprintf(buf, sizeof(buf), "ta_fwd_pp_%s_d%d_c%d_t%d", dt, d, causal ? 1 : 0, tail ? 1 : 0);
+    return {"attn_fwd_pp.hsaco", buf, 512u};
+  }
+  if (eight_wave64(tm, tn, accum, d)) {
+    snprintf(buf, sizeof(buf), "ta_fwd_pp64_%s_d%d_c%d_t%d", dt, d, causal ? 1 : 0, tail ? 1 : 0);
     return {"attn_fwd_pp.hsaco", buf, 512u};
   }
   snprintf(buf, sizeof(buf), "ta_fwd_%s_d%d_m%d_n%d_c%d_t%d_a%d", dt, d, tm, tn, causal ? 1 : 0,
@@ -327,9 +344,10 @@ ta_status validate_args(const ta_fwd_args* a, int64_t* n_bh_out, int64_t* n_qblk
   if (a->d_real != 0) {
     if (a->d_real < 8 || a->d_real > a->D || (a->d_real & 7) != 0)
       return fail(TA_EINVAL, "d_real %d (0, or a multiple of 8 in [8, D])", a->d_real);
-    if (!eight_wave(a->tile_m, a->tile_n, a->accum, a->D))
+    if (!eight_wave_family(a->tile_m, a->tile_n, a->accum, a->D))
       return fail(TA_EUNSUPPORTED,
-                  "d_real needs tile (128, 64) or (128, 128), fp32 accumulation and D <= 160");
+                  "d_real needs fp32 accumulation and tile (128, 64) or (128, 128) with D <= 160, "
+                  "or tile (64, 64) or (64, 128) with D = 64 or 128");
   }
   if (a->B < 0 || a->H < 0 || a->S < 0) return fail(TA_EINVAL, "negative shape");
   ta_status shape_st = check_shape(a->D, a->tile_m, a->tile_n);
@@ -374,8 +392,9 @@ ta_status validate_args(const ta_fwd_args* a, int64_t* n_bh_out, int64_t* n_qblk
   // below 2^31 bytes.
   if (a->S * a->k_stride[2] * 2 > 0x7fffffffLL || a->S * a->v_stride[2] * 2 > 0x7fffffffLL)
     return fail(TA_EINVAL, "k/v: S * row stride must stay below 2^31 bytes per (b, h) slice");
-  // The eight-wave kernel stages Q the same way (one buffer resource per query block).
-  if (eight_wave(a->tile_m, a->tile_n, a->accum, a->D) && a->S * a->q_stride[2] * 2 > 0x7fffffffLL)
+  // The eight-wave kernels stage Q the same way (one buffer resource per query block).
+  if (eight_wave_family(a->tile_m, a->tile_n, a->accum, a->D) &&
+      a->S * a->q_stride[2] * 2 > 0x7fffffffLL)
     return fail(TA_EINVAL, "q: S * row stride must stay below 2^31 bytes per (b, h) slice");
   if (a->aligned != 0 && a->aligned != 1) return fail(TA_EINVAL, "aligned %d", a->aligned);
   *n_qblk_out = n_qblk;
@@ -403,9 +422,11 @@ void fill_params(const ta_fwd_args* a, int64_t n_bh, int64_t n_qblk, ta::FwdPara
 
 // Whether a launch runs the kernel variant without tail masking: the caller allows it
 // (args->aligned, the aligned fast-path decision, flash_fwd.py:199-238) and every tile is
-// whole (S a multiple of both tile sizes).
+// whole (S a multiple of both tile sizes, and of the 128-key step for the eight-wave
+// kernels).
 bool unmasked_tail(const ta_fwd_args* a) {
-  return a->aligned == 1 && a->S % a->tile_m == 0 && a->S % a->tile_n == 0;
+  const bool steps = !eight_wave_family(a->tile_m, a->tile_n, a->accum, a->D) || a->S % ta::kPPKeys == 0;
+  return a->aligned == 1 && a->S % a->tile_m == 0 && a->S % a->tile_n == 0 && steps;
 }
 
 // Whether a whole-row launch runs causal query blocks in pairs (nq - 1 - j, then j; one
