@@ -103,8 +103,7 @@ def _call(lib, a):
     (dict(d_real=72), _lib.TA_EINVAL, "d_real 72"),        # above D = 64
     (dict(d_real=-8), _lib.TA_EINVAL, "d_real"),
     (dict(d_real=36, D=128, tile_m=128), _lib.TA_EINVAL, "multiple of 8"),
-    (dict(d_real=96, D=128, accum=1), _lib.TA_EUNSUPPORTED, "d_real needs fp32"),  # tile 64x64
-    (dict(d_real=96, D=128, tile_m=128, accum=1), _lib.TA_EUNSUPPORTED, "d_real needs"),
+    (dict(d_real=136, D=160, accum=1, tile_m=128), _lib.TA_EUNSUPPORTED, "d_real needs"),
     (dict(d_real=136, D=160), _lib.TA_EUNSUPPORTED, "d_real needs"),  # 64-row tiles: D <= 128
     (dict(d_real=200, D=256, tile_m=128), _lib.TA_EUNSUPPORTED, "D <= 160"),
 ])

@@ -135,10 +135,10 @@ def test_tails_all_tiles(gpu, s, causal, dtype, d):
 
 @pytest.mark.parametrize("d", [8, 32, 48, 80, 96, 100])
 def test_head_dim_padding(gpu, d):
-    """D outside {64,128}: a multiple of 8 runs in place on the eight-wave kernels (default
-    tile and the 64-row tiles with fp32 accumulation), whose missing columns read as zero
-    (dense output of width D); other D, and the four-wave kernels (input-dtype
-    accumulation), are zero-padded on the host and the output is a sliced view."""
+    """D outside {64,128}: a multiple of 8 runs in place on the eight-wave kernels (every
+    tile, fp32 or input-dtype accumulation), whose missing columns read as zero (dense
+    output of width D); other D are zero-padded on the host and the output is a sliced
+    view."""
     q, k, v = inputs((1, 2, 200, d), "float16", 7 + d)
     for causal in (False, True):
         ref = oracle_f32(q, k, v, causal=causal)
@@ -151,10 +151,10 @@ def test_head_dim_padding(gpu, d):
         out = run_gpu(q, k, v, causal=causal, tile_m=64, tile_n=64)
         assert out.shape == (1, 2, 200, d) and out.is_contiguous() == (d % 8 == 0)
         check_close(as_f32(out), ref, "float16", what=f"64-row pad D={d}")
-        say(f"pad fp16 (1,2,200,{d}) causal={causal} tile 64x64 input-dtype accumulation (host padding)")
-        host = run_gpu(q, k, v, causal=causal, tile_m=64, tile_n=64, accum_mode="fp16")
-        assert host.shape == (1, 2, 200, d) and not host.is_contiguous()
-        check_close(as_f32(host), ref, "float16", tol=LOWP_TOL["float16"], what=f"host pad D={d}")
+        say(f"pad fp16 (1,2,200,{d}) causal={causal} tile 64x64 input-dtype accumulation")
+        low = run_gpu(q, k, v, causal=causal, tile_m=64, tile_n=64, accum_mode="fp16")
+        assert low.shape == (1, 2, 200, d) and low.is_contiguous() == (d % 8 == 0)
+        check_close(as_f32(low), ref, "float16", tol=LOWP_TOL["float16"], what=f"input-dtype pad D={d}")
 
 
 @pytest.mark.parametrize("d,dtype,causal,s", [

@@ -218,8 +218,10 @@ def test_dtype_codes():
     (256, True, (128, 64), "fp32", 128, 2),   # every workgroup resident
     (512, True, (128, 64), "fp32", 64, 1),    # causal eight-wave D=64: one per CU, heavy first
     (256, True, (128, 64), "fp32", 64, 2),
-    (512, True, (128, 64), "input", 128, 2),  # four-wave kernel: all 512 resident (2 per CU)
-    (1024, True, (128, 64), "input", 128, 1),
+    (512, True, (128, 64), "input", 128, 1),  # eight-wave input-dtype kernel: one per CU
+    (256, True, (128, 64), "input", 128, 2),
+    (512, True, (128, 64), "input", 160, 2),  # four-wave kernel (D = 160): all 512 resident (2 per CU)
+    (1024, True, (128, 64), "input", 160, 1),
     (256, True, (128, 128), "fp32", 128, 2),
     (512, True, (128, 128), "fp32", 128, 1),
     (512, True, (128, 128), "fp32", 64, 1),   # other tiles: one per CU at any D
@@ -257,7 +259,8 @@ def test_sched_env(monkeypatch):
     (512, 64, 8, "fp32", (64, 64)),
     (512, 96, 8, "fp32", (64, 64)),      # kernel head dim 128 (in-place padding)
     (512, 160, 8, "fp32", (128, 64)),    # no 64-row eight-wave kernel above D = 128
-    (512, 128, 8, "fp16", (128, 64)),    # input-dtype accumulation: the four-wave kernels
+    (512, 128, 8, "fp16", (64, 64)),     # input-dtype accumulation: its 64-row eight-wave kernel
+    (512, 160, 8, "fp16", (128, 64)),    # D = 160: the four-wave kernels
     (512, 128, 0, "fp32", (128, 64)),    # no head count given
 ])
 def test_default_tile_prefers_64_rows_when_one_wave_of_blocks_fits(s, d, n_bh, accum, expected):
@@ -274,12 +277,16 @@ def test_64_row_tiles_select_the_eight_wave_kernel():
     assert _lib.kernel_symbol(dtype=_lib.TA_FP16, head_dim=64, tile_m=64, tile_n=64, causal=False,
                               tail=True, accum=_lib.TA_ACC_FP32)[1] == "ta_fwd_pp64_f16_d64_c0_t1"
     assert _lib.kernel_symbol(dtype=_lib.TA_FP16, head_dim=64, tile_m=64, tile_n=64, causal=False,
-                              tail=True, accum=_lib.TA_ACC_INPUT)[1].startswith("ta_fwd_f16_d64_m64_n64")
+                              tail=True, accum=_lib.TA_ACC_INPUT)[1] == "ta_fwd_ppl64_f16_d64_c0_t1"
+    assert _lib.kernel_symbol(dtype=_lib.TA_FP16, head_dim=128, tile_m=128, tile_n=128, causal=True,
+                              tail=False, accum=_lib.TA_ACC_INPUT)[1] == "ta_fwd_ppl_f16_d128_c1_t0"
+    assert _lib.kernel_symbol(dtype=_lib.TA_FP16, head_dim=160, tile_m=128, tile_n=64, causal=True,
+                              tail=False, accum=_lib.TA_ACC_INPUT)[1].startswith("ta_fwd_f16_d160_m128_n64")
     assert _lib.kernel_symbol(dtype=_lib.TA_FP16, head_dim=160, tile_m=64, tile_n=64, causal=False,
                               tail=True, accum=_lib.TA_ACC_FP32)[1].startswith("ta_fwd_f16_d160_m64_n64")
     tm = dict(tile_m=64, tile_n=64, accum=_lib.TA_ACC_FP32, head_dim=128)
     assert not _lib.tail_masked(seq_len=512, **tm)
     assert _lib.tail_masked(seq_len=320, **tm)   # multiple of 64, not of the 128-key step
     assert _lib.tail_masked(seq_len=512, aligned=False, **tm)
-    four = dict(tile_m=64, tile_n=64, accum=_lib.TA_ACC_INPUT, head_dim=128)
+    four = dict(tile_m=64, tile_n=64, accum=_lib.TA_ACC_INPUT, head_dim=160)
     assert not _lib.tail_masked(seq_len=320, **four)  # four-wave kernels step by the tile

@@ -49,10 +49,13 @@ def uses_pairs(*, causal: bool, head_dim: int, tile_m: int, tile_n: int, accum: 
 
 def eight_wave_family(*, tile_m: int, tile_n: int, accum: int, head_dim: int) -> bool:
     """The eight-wave kernels (attn_fwd_pp.hsaco): fp32 accumulation with tiles (128, 64) /
-    (128, 128) at D <= 160, or tiles (64, 64) / (64, 128) at D = 64 or 128; the same rule as
-    eight_wave_family() in csrc/tiledattn.cpp."""
-    if accum != TA_ACC_FP32 or tile_n not in (64, 128):
+    (128, 128) at D <= 160, or tiles (64, 64) / (64, 128) at D = 64 or 128; input-dtype
+    accumulation with any tile at D = 64 or 128.  The same rule as eight_wave_family() in
+    csrc/tiledattn.cpp."""
+    if tile_n not in (64, 128) or tile_m not in (64, 128):
         return False
+    if accum != TA_ACC_FP32:  # input-dtype accumulation: ta_fwd_ppl_* / ta_fwd_ppl64_*
+        return head_dim in (64, 128)
     return (tile_m == 128 and head_dim <= 160) or (tile_m == 64 and head_dim in (64, 128))
 
 
@@ -78,9 +81,10 @@ def kernel_symbol(*, dtype: int, head_dim: int, tile_m: int, tile_n: int, causal
     if tile_m == 128 and tile_n in (64, 128) and accum == TA_ACC_FP32 and head_dim <= 160:
         kind = "pp_split" if split else ("pp_pair" if pair else "pp")
         return "attn_fwd_pp.hsaco", f"ta_fwd_{kind}_{dt}_d{head_dim}_c{c}_t{t}"
-    if (tile_m == 64 and tile_n in (64, 128) and accum == TA_ACC_FP32 and head_dim in (64, 128)
+    if (eight_wave_family(tile_m=tile_m, tile_n=tile_n, accum=accum, head_dim=head_dim)
             and not split and not pair):
-        return "attn_fwd_pp.hsaco", f"ta_fwd_pp64_{dt}_d{head_dim}_c{c}_t{t}"
+        kind = "pp64" if accum == TA_ACC_FP32 else ("ppl" if tile_m == 128 else "ppl64")
+        return "attn_fwd_pp.hsaco", f"ta_fwd_{kind}_{dt}_d{head_dim}_c{c}_t{t}"
     if split:
         raise ValueError("split key ranges exist for tiles (128, 64) and (128, 128), fp32 "
                          "accumulation, D <= 160")

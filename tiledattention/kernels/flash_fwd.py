@@ -213,11 +213,11 @@ def _default_tile_config_for_shape_gfx950(*, seq_len: int, head_dim: int, causal
                                          n_bh: int = 0, accum_mode: str = "fp32") -> tuple[int, int]:
     """Default (TILE_M, TILE_N) on gfx950 when neither env knob is set.
 
-    128 query rows per workgroup: with fp32 accumulation the eight-wave kernel (two waves per
-    SIMD splitting every 128-key step, one workgroup per CU), with input-dtype accumulation
-    the four-wave kernel with 64-key tiles (two workgroups per CU).  When the 64-row blocks
-    of all ``n_bh`` heads fit the CUs in one wave (B*H*ceil(S/64) <= CUs; fp32, kernel head
-    dim 64 or 128), 64 rows instead: the 64-row eight-wave kernel halves each block's key
+    128 query rows per workgroup: the eight-wave kernel (two waves per SIMD splitting every
+    128-key step, one workgroup per CU; at kernel head dims above 128 with input-dtype
+    accumulation the four-wave kernel with 64-key tiles).  When the 64-row blocks of all
+    ``n_bh`` heads fit the CUs in one wave (B*H*ceil(S/64) <= CUs; kernel head dim 64 or
+    128), 64 rows instead: the 64-row eight-wave kernel halves each block's key
     loop and the grid is still one workgroup per CU (B1 H8 bf16: causal S=1024 15.0 -> 12.0
     us, S=2048 23.5 -> 18.8; non-causal S=1024 14.4 -> 11.9, S=2048 23.3 -> 20.3; D=64 causal
     S=2048 18.2 -> 13.5).  With more blocks than CUs, the second block of a CU pays the
@@ -226,7 +226,7 @@ def _default_tile_config_for_shape_gfx950(*, seq_len: int, head_dim: int, causal
     (``_split_preferred``).
     """
     del causal
-    if (accum_mode == "fp32" and 0 < head_dim <= 128 and n_bh > 0 and seq_len > 0
+    if (0 < head_dim <= 128 and n_bh > 0 and seq_len > 0
             and n_bh * ((seq_len + 63) // 64) <= _CU_COUNT):
         return 64, 64
     return 128, 64
@@ -248,13 +248,15 @@ _CU_COUNT = 256  # MI355X
 def _workgroups_per_cu(*, tile_m: int, tile_n: int, accum_code: int, head_dim: int = 128,
                        causal: bool = True) -> int:
     """Workgroups of one launch resident on a CU at once: two for the non-causal eight-wave
-    kernels at kernel head dim 64 (built for 128 VGPRs, 64 KiB of LDS), one for the other
-    eight-wave kernels (their stages fill a CU's LDS); for the four-wave kernels two at
-    128x64 (input-dtype accumulation), two at 64x128 (one LDS stage), four at 64x64 up to
-    D = 128 and two above (one LDS stage), one otherwise (LDS or registers)."""
+    kernels at kernel head dim 64 with fp32 accumulation (built for 128 VGPRs, 64 KiB of
+    LDS), one for the other eight-wave kernels (their stages fill a CU's LDS, or their
+    registers two waves per SIMD); for the four-wave kernels two at 128x64 (input-dtype
+    accumulation), two at 64x128 (one LDS stage), four at 64x64 up to D = 128 and two above
+    (one LDS stage), one otherwise (LDS or registers)."""
     if _eight_wave_kernel(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code,
                           kernel_head_dim=head_dim):
-        return 2 if head_dim <= 64 and not causal else 1
+        fp32 = accum_code == _lib.TA_ACC_FP32
+        return 2 if fp32 and head_dim <= 64 and not causal else 1
     if (tile_m, tile_n) == (128, 64) and accum_code == _lib.TA_ACC_INPUT:
         return 2
     if (tile_m, tile_n) == (64, 128) and head_dim <= 128:
@@ -315,15 +317,16 @@ def _eight_wave_kernel(*, tile_m: int, tile_n: int, accum_code: int, kernel_head
     narrower head dims: fp32 accumulation with tile (128, 64) or (128, 128) at kernel head
     dim 64, 128 or 160 (workgroup step 128 rows x 128 keys, 64 keys per wave group, so it
     serves both 128-row tiles), or with tile (64, 64) or (64, 128) at 64 or 128 (the
-    64-row form, the same 128-key steps)."""
+    64-row form, the same 128-key steps); input-dtype accumulation with any tile at 64 or
+    128."""
     return _lib.eight_wave_family(tile_m=tile_m, tile_n=tile_n, accum=accum_code,
                                   head_dim=kernel_head_dim)
 
 
 def _split_capable(*, tile_m: int, tile_n: int, accum_code: int, kernel_head_dim: int) -> bool:
-    """Whether split key ranges exist: the 128-row eight-wave kernel."""
-    return tile_m == 128 and _eight_wave_kernel(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code,
-                                                kernel_head_dim=kernel_head_dim)
+    """Whether split key ranges exist: the 128-row eight-wave kernel with fp32 accumulation."""
+    return tile_m == 128 and accum_code == _lib.TA_ACC_FP32 and _eight_wave_kernel(
+        tile_m=tile_m, tile_n=tile_n, accum_code=accum_code, kernel_head_dim=kernel_head_dim)
 
 
 

@@ -61,7 +61,13 @@ constexpr int pp_stage_bytes(int d) { return kPPKeys * 2 * d; }
 // the block's query rows: 128 (four 32-row blocks; a wave group's four waves take one row
 // block each and the group's 64 keys of every step), or 64 (two row blocks; a group's
 // waves are two row blocks x two 32-key slots, so four waves share each row block).
-template <int DT, int D, bool CAUSAL, bool TAIL, bool SPLIT, int TMR = 128>
+// LOWP: input-dtype accumulation (the reference's flash_fwd.py:301-372): every step of a
+// wave takes the exact running max, l sums the unrounded P in fp32, and O is rounded to the
+// input dtype once per 64 keys of the wave's slice, rnd((acc + P.V) rnd(alpha)), the P.V
+// products accumulated onto the rounded acc in fp32 by the MFMAs.  The
+// key slices of a row (each accumulated that way) are combined in fp32 at the end, rounded
+// to the input dtype, and multiplied by rnd(1/l) (one more rounding).
+template <int DT, int D, bool CAUSAL, bool TAIL, bool SPLIT, int TMR = 128, bool LOWP = false>
 __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const WorkItem wi, char* lds_k0,
                                                   char* lds_k1, char* lds_v0, char* lds_v1) {
   constexpr int TM = TMR;            // query rows per workgroup
@@ -91,6 +97,7 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   static_assert(STAGE_A % (8 * 1024) == 0, "stage must split over the eight waves");
   static_assert(TK == kPPKeys && (TM == kPPRows || TM == 64), "steps of 128 keys, blocks of 128 or 64 rows");
   static_assert(TM == 128 || (!SPLIT && (D == 64 || D == 128)), "64-row blocks: whole rows, D 64 or 128");
+  static_assert(!LOWP || (!SPLIT && (D == 64 || D == 128)), "input-dtype accumulation: whole rows, D 64 or 128");
   // Raised MFMA-cluster priority only in the kernels built for two workgroups per CU (the
   // non-causal D = 64 whole-row ones, TA_PP_WAVES below).
   constexpr bool kPrioMfma = !SPLIT && D == 64 && !CAUSAL;
@@ -319,7 +326,8 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   // VALU cluster of step t: mask, row max, rescale, P = 2^(s*c - m*c) packed, l.  One
   // code path for every step (blocks without a needed key are masked whole), so the
   // rescale of O exists once and O keeps one register assignment through the loop.
-  auto softmax = [&](int t) {
+  auto softmax = [&](int t, auto par_tag) {
+    constexpr int PAR = decltype(par_tag)::value;  // t & 1 (whole rows start at step 0)
     // Blocks past the wave's last key are masked whole by the same test: all their keys
     // are past the wave's last query (causal) or past S.
     if (!(no_mask(t) && all_active(t))) {
@@ -390,6 +398,57 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
     // exact one (max grew by more than the threshold -> rescale O and l, recompute P).
     // A VALU cluster is bound by one wave's issue rate, so the skipped reduction is time
     // saved.
+    if constexpr (LOWP) {
+      // Exact running max; P from it (fp32), packed for P.V; l from the unrounded P.
+      const float mx = row_max();
+      const float m_new = vmax(m_run, mx);
+      const float alpha = fast_exp2((m_run - m_new) * c);  // 1 where the max holds
+      m_run = m_new;
+      const float mc = m_run * c;
+      float l4[4];
+#pragma unroll
+      for (int bk = 0; bk < KB; ++bk) {
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+          const float p0 = fast_exp2(__builtin_fmaf(s[bk][r], c, -mc));
+          const float p1 = fast_exp2(__builtin_fmaf(s[bk][r + 1], c, -mc));
+          pk[bk][r >> 1] = DTy::pack(p0, p1);
+          const int j = (r >> 1) & 3;
+          l4[j] = bk == 0 && r < 8 ? p0 + p1 : l4[j] + (p0 + p1);
+        }
+      }
+      l_part = l_part * alpha + ((l4[0] + l4[1]) + (l4[2] + l4[3]));
+      // The previous tile's accumulation (acc + P.V in fp32) rounded to the input dtype,
+      // rescaled first when some row's max moved: rnd((acc + P.V) rnd(alpha)).  A tile is 64
+      // keys of the wave's slice: with 64-row blocks (32 keys a step) every other step, the
+      // steps between only rescale.
+      const bool moved = __ballot(!(alpha == 1.0f)) != 0;
+      const float al = DTy::round(alpha);
+      constexpr bool kRoundHere = TM == 128 || PAR == 1;
+      if (kRoundHere || moved) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+#pragma unroll
+          for (int r = 0; r < 16; r += 2) {
+            if constexpr (kRoundHere) {
+              const uint32_t w = moved ? DTy::pack(o_acc[db][r] * al, o_acc[db][r + 1] * al)
+                                       : DTy::pack(o_acc[db][r], o_acc[db][r + 1]);
+              o_acc[db][r] = DTy::lo(w);
+              o_acc[db][r + 1] = DTy::hi(w);
+            } else {
+              o_acc[db][r] *= al;
+              o_acc[db][r + 1] *= al;
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int bk = 0; bk < KB; ++bk) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(pk[bk][i]));
+      }
+      return;
+    }
     float l_step = make_p(m_run * c);
     if (__ballot(!(l_step < kRescaleBound))) {
       const float mx = row_max();
@@ -494,7 +553,7 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   // so the result is the same either way.
   auto first = [&]() {
     qk(lds_k0);
-    if (no_mask(t_beg) && all_active(t_beg)) m_run = row_max();
+    if (!LOWP && no_mask(t_beg) && all_active(t_beg)) m_run = row_max();
   };
 
   // Step t with stage parity PAR: the stages of K_t (consumed; receives K_{t+2}), K_{t+1},
@@ -505,7 +564,7 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
     char* k_nxt = PAR ? lds_k0 : lds_k1;
     char* v_cur = PAR ? lds_v1 : lds_v0;
     char* v_nxt = PAR ? lds_v0 : lds_v1;
-    softmax(t);
+    softmax(t, par_tag);
     wait_dma();  // this group's halves of K_{t+1} and V_t (issued one MFMA cluster ago)
     barrier();
     // MFMA cluster: S of step t + 1 (past the last step it reads a stale or zero stage and
@@ -587,10 +646,19 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
     const float l_tot = la + lb;
     const float inv = 1.0f / l_tot;
     const float w0s = a0 * inv, w1s = a1 * inv;
+    // Input-dtype accumulation: the two halves (each rounded per tile) combined in fp32 and
+    // rounded to the input dtype, then rnd(acc rnd(1/l)) (flash_fwd.py:366-368).
+    const float ri = DTy::round(inv);
     auto merged = [&](int b, int g) {
       f32x4 o4;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o4[e] = o_acc[LO + b][4 * g + e] * w0s + x1[b][g][e] * w1s;
+      for (int e = 0; e < 4; ++e) {
+        if constexpr (LOWP) {
+          o4[e] = DTy::round(DTy::round(o_acc[LO + b][4 * g + e] * a0 + x1[b][g][e] * a1) * ri);
+        } else {
+          o4[e] = o_acc[LO + b][4 * g + e] * w0s + x1[b][g][e] * w1s;
+        }
+      }
       return o4;
     };
     if (SPLIT && slot >= 0) {
@@ -721,8 +789,16 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
         f32x4 o4;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          o4[e] = o_acc[u / 4][4 * (u % 4) + e] * w0 + (x[0][cc][e] * wn[0] + x[1][cc][e] * wn[1]) +
-                  x[2][cc][e] * wn[2];
+          if constexpr (LOWP) {
+            // the four slices (each rounded per tile) combined in fp32 and rounded to the
+            // input dtype, then rnd(acc rnd(1/l))
+            const float h = o_acc[u / 4][4 * (u % 4) + e] * a0 + (x[0][cc][e] * an[0] + x[1][cc][e] * an[1]) +
+                            x[2][cc][e] * an[2];
+            o4[e] = DTy::round(DTy::round(h) * DTy::round(inv));
+          } else {
+            o4[e] = o_acc[u / 4][4 * (u % 4) + e] * w0 + (x[0][cc][e] * wn[0] + x[1][cc][e] * wn[1]) +
+                    x[2][cc][e] * wn[2];
+          }
         }
         const int d = 32 * (u / 4) + 8 * (u % 4) + 4 * hl;
         if (d < d_real) *(u32x2*)(orow + d) = u32x2{DTy::pack(o4[0], o4[1]), DTy::pack(o4[2], o4[3])};
@@ -904,7 +980,7 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
 // heaviest first, so each CU takes the next tile when its current one ends and heavy
 // tiles pair with light ones.  Split items cover a chunk of key steps of a block and
 // leave a partial (slot >= 0) when the block has more than one chunk.
-template <int DT, int D, bool CAUSAL, bool TAIL, bool SPLIT, bool PAIR, int TMR = 128>
+template <int DT, int D, bool CAUSAL, bool TAIL, bool SPLIT, bool PAIR, int TMR = 128, bool LOWP = false>
 __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   constexpr int STAGE = pp_stage_bytes(D);
   // One array per (tensor, stage): the stage of every access is a compile-time constant
@@ -930,7 +1006,7 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
     const WorkItem wi = SPLIT ? split_item(blockIdx.x, p.n_bh, p.split_items, p.sched, CAUSAL,
                                            p.split_c, p.split_ns, p.split_slots, p.S)
                               : whole_item(blockIdx.x, p.n_bh, p.n_qblk, p.sched, CAUSAL);
-    attn_fwd_pp_block<DT, D, CAUSAL, TAIL, SPLIT, TMR>(p, wi, lds_k0, lds_k1, lds_v0, lds_v1);
+    attn_fwd_pp_block<DT, D, CAUSAL, TAIL, SPLIT, TMR, LOWP>(p, wi, lds_k0, lds_k1, lds_v0, lds_v1);
   }
 }
 
@@ -1028,6 +1104,27 @@ __device__ __forceinline__ void attn_merge_body(const FwdParams& p) {
   TA_PP64_DEFINE(DTN, DT, D, 1, 0)    \
   TA_PP64_DEFINE(DTN, DT, D, 1, 1)
 
+// Input-dtype accumulation (D = 64 and 128, whole rows): ta_fwd_ppl_<f16|bf16>_d<D>_c_t
+// (128-row blocks, tiles (128, 64) / (128, 128)) and ta_fwd_ppl64_<...> (64-row blocks,
+// tiles (64, 64) / (64, 128)).
+// One workgroup per CU (two waves per SIMD): at 128 VGPRs the exact max and the rounding of
+// O beside P spilled registers to scratch.
+#define TA_PPL_DEFINE(NAME, DTN, DT, D, C, T, TMR)                                          \
+  extern "C" __global__ void __launch_bounds__(512)                                       \
+      __attribute__((amdgpu_waves_per_eu(2, 2)))                                          \
+      ta_fwd_##NAME##_##DTN##_d##D##_c##C##_t##T(ta::FwdParams p) {                        \
+    ta::attn_fwd_pp_body<DT, D, (C != 0), (T != 0), false, false, TMR, true>(p);          \
+  }
+#define TA_PPL_DEFINE_CT(DTN, DT, D)            \
+  TA_PPL_DEFINE(ppl, DTN, DT, D, 0, 0, 128)     \
+  TA_PPL_DEFINE(ppl, DTN, DT, D, 0, 1, 128)     \
+  TA_PPL_DEFINE(ppl, DTN, DT, D, 1, 0, 128)     \
+  TA_PPL_DEFINE(ppl, DTN, DT, D, 1, 1, 128)     \
+  TA_PPL_DEFINE(ppl64, DTN, DT, D, 0, 0, 64)    \
+  TA_PPL_DEFINE(ppl64, DTN, DT, D, 0, 1, 64)    \
+  TA_PPL_DEFINE(ppl64, DTN, DT, D, 1, 0, 64)    \
+  TA_PPL_DEFINE(ppl64, DTN, DT, D, 1, 1, 64)
+
 // Merge kernels of the split path: ta_fwd_merge_<f16|bf16>_d<D>_c<0|1>, merge_threads(D)
 // threads.
 #define TA_MERGE_DEFINE(DTN, DT, D, C)                                                     \
@@ -1062,3 +1159,7 @@ TA_PP64_DEFINE_CT(f16, 0, 64)
 TA_PP64_DEFINE_CT(f16, 0, 128)
 TA_PP64_DEFINE_CT(bf16, 1, 64)
 TA_PP64_DEFINE_CT(bf16, 1, 128)
+TA_PPL_DEFINE_CT(f16, 0, 64)
+TA_PPL_DEFINE_CT(f16, 0, 128)
+TA_PPL_DEFINE_CT(bf16, 1, 64)
+TA_PPL_DEFINE_CT(bf16, 1, 128)

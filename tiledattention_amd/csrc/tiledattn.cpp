@@ -104,10 +104,18 @@ bool eight_wave64(int64_t tm, int64_t tn, int64_t accum, int64_t d) {
   return tm == 64 && (tn == 64 || tn == 128) && accum == TA_ACC_FP32 && (d == 64 || d == 128);
 }
 
-// Either form: direct-to-LDS staging of Q, K and V (in-place padding of narrower head dims
+// Input-dtype accumulation on the eight-wave kernels (ta_fwd_ppl_* for 128-row tiles,
+// ta_fwd_ppl64_* for 64-row ones) at D = 64 and 128: whole rows, no split or pairs.
+bool eight_wave_lowp(int64_t tm, int64_t tn, int64_t accum, int64_t d) {
+  return accum == TA_ACC_INPUT && (tm == 64 || tm == 128) && (tn == 64 || tn == 128) &&
+         (d == 64 || d == 128);
+}
+
+// Any of them: direct-to-LDS staging of Q, K and V (in-place padding of narrower head dims
 // through d_real; 128-key steps).
 bool eight_wave_family(int64_t tm, int64_t tn, int64_t accum, int64_t d) {
-  return eight_wave(tm, tn, accum, d) || eight_wave64(tm, tn, accum, d);
+  return eight_wave(tm, tn, accum, d) || eight_wave64(tm, tn, accum, d) ||
+         eight_wave_lowp(tm, tn, accum, d);
 }
 
 KernelId kernel_id(int dtype, int d, int tm, int tn, int causal, int tail, int accum) {
@@ -119,8 +127,9 @@ KernelId kernel_id(int dtype, int d, int tm, int tn, int causal, int tail, int a
     snprintf(buf, sizeof(buf), "ta_fwd_pp_%s_d%d_c%d_t%d", dt, d, causal ? 1 : 0, tail ? 1 : 0);
     return {"attn_fwd_pp.hsaco", buf, 512u};
   }
-  if (eight_wave64(tm, tn, accum, d)) {
-    snprintf(buf, sizeof(buf), "ta_fwd_pp64_%s_d%d_c%d_t%d", dt, d, causal ? 1 : 0, tail ? 1 : 0);
+  if (eight_wave64(tm, tn, accum, d) || eight_wave_lowp(tm, tn, accum, d)) {
+    const char* kind = eight_wave64(tm, tn, accum, d) ? "pp64" : tm == 128 ? "ppl" : "ppl64";
+    snprintf(buf, sizeof(buf), "ta_fwd_%s_%s_d%d_c%d_t%d", kind, dt, d, causal ? 1 : 0, tail ? 1 : 0);
     return {"attn_fwd_pp.hsaco", buf, 512u};
   }
   snprintf(buf, sizeof(buf), "ta_fwd_%s_d%d_m%d_n%d_c%d_t%d_a%d", dt, d, tm, tn, causal ? 1 : 0,
@@ -346,8 +355,9 @@ ta_status validate_args(const ta_fwd_args* a, int64_t* n_bh_out, int64_t* n_qblk
       return fail(TA_EINVAL, "d_real %d (0, or a multiple of 8 in [8, D])", a->d_real);
     if (!eight_wave_family(a->tile_m, a->tile_n, a->accum, a->D))
       return fail(TA_EUNSUPPORTED,
-                  "d_real needs fp32 accumulation and tile (128, 64) or (128, 128) with D <= 160, "
-                  "or tile (64, 64) or (64, 128) with D = 64 or 128");
+                  "d_real needs an eight-wave kernel: tile (128, 64) or (128, 128) with fp32 "
+                  "accumulation and D <= 160, or D = 64 or 128 with any tile and fp32 or "
+                  "input-dtype accumulation");
   }
   if (a->B < 0 || a->H < 0 || a->S < 0) return fail(TA_EINVAL, "negative shape");
   ta_status shape_st = check_shape(a->D, a->tile_m, a->tile_n);
