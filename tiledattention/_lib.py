@@ -144,11 +144,15 @@ _lib: ctypes.CDLL | None = None
 
 def lib_dir() -> Path:
     """Directory of ``libtiledattn.so`` and the code objects: ``TILEDATTN_LIB_DIR``, else
-    ``lib/`` of the ``tiledattention_amd`` package (found by its import spec, which does not
-    execute it)."""
+    ``lib/`` beside this package (a kernel package laid out by
+    ``tiledattention_amd.kernel_build`` carries its own), else ``lib/`` of the
+    ``tiledattention_amd`` package (found by its import spec, which does not execute it)."""
     env = os.getenv("TILEDATTN_LIB_DIR", "").strip()
     if env:
         return Path(env)
+    own = Path(__file__).resolve().parent / "lib"
+    if (own / "libtiledattn.so").exists():
+        return own
     spec = importlib.util.find_spec("tiledattention_amd")
     if spec is None or not spec.submodule_search_locations:
         raise DependencyError(
