@@ -277,9 +277,9 @@ def test_64_row_tiles_select_the_eight_wave_kernel():
     assert _lib.kernel_symbol(dtype=_lib.TA_FP16, head_dim=64, tile_m=64, tile_n=64, causal=False,
                               tail=True, accum=_lib.TA_ACC_FP32)[1] == "ta_fwd_pp64_f16_d64_c0_t1"
     assert _lib.kernel_symbol(dtype=_lib.TA_FP16, head_dim=64, tile_m=64, tile_n=64, causal=False,
-                              tail=True, accum=_lib.TA_ACC_INPUT)[1] == "ta_fwd_ppl64_f16_d64_c0_t1"
+                              tail=True, accum=_lib.TA_ACC_INPUT)[1] == "ta_fwd_ppl64_n64_f16_d64_c0_t1"
     assert _lib.kernel_symbol(dtype=_lib.TA_FP16, head_dim=128, tile_m=128, tile_n=128, causal=True,
-                              tail=False, accum=_lib.TA_ACC_INPUT)[1] == "ta_fwd_ppl_f16_d128_c1_t0"
+                              tail=False, accum=_lib.TA_ACC_INPUT)[1] == "ta_fwd_ppl_n128_f16_d128_c1_t0"
     assert _lib.kernel_symbol(dtype=_lib.TA_FP16, head_dim=160, tile_m=128, tile_n=64, causal=True,
                               tail=False, accum=_lib.TA_ACC_INPUT)[1].startswith("ta_fwd_f16_d160_m128_n64")
     assert _lib.kernel_symbol(dtype=_lib.TA_FP16, head_dim=160, tile_m=64, tile_n=64, causal=False,

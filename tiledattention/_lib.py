@@ -83,7 +83,9 @@ def kernel_symbol(*, dtype: int, head_dim: int, tile_m: int, tile_n: int, causal
         return "attn_fwd_pp.hsaco", f"ta_fwd_{kind}_{dt}_d{head_dim}_c{c}_t{t}"
     if (eight_wave_family(tile_m=tile_m, tile_n=tile_n, accum=accum, head_dim=head_dim)
             and not split and not pair):
-        kind = "pp64" if accum == TA_ACC_FP32 else ("ppl" if tile_m == 128 else "ppl64")
+        if accum == TA_ACC_FP32:
+            return "attn_fwd_pp.hsaco", f"ta_fwd_pp64_{dt}_d{head_dim}_c{c}_t{t}"
+        kind = f"{'ppl' if tile_m == 128 else 'ppl64'}_n{tile_n}"
         return "attn_fwd_pp.hsaco", f"ta_fwd_{kind}_{dt}_d{head_dim}_c{c}_t{t}"
     if split:
         raise ValueError("split key ranges exist for tiles (128, 64) and (128, 128), fp32 "

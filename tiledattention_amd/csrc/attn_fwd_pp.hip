@@ -63,11 +63,12 @@ constexpr int pp_stage_bytes(int d) { return kPPKeys * 2 * d; }
 // waves are two row blocks x two 32-key slots, so four waves share each row block).
 // LOWP: input-dtype accumulation (the reference's flash_fwd.py:301-372): every step of a
 // wave takes the exact running max, l sums the unrounded P in fp32, and O is rounded to the
-// input dtype once per 64 keys of the wave's slice, rnd((acc + P.V) rnd(alpha)), the P.V
-// products accumulated onto the rounded acc in fp32 by the MFMAs.  The
+// input dtype once per TILE_N keys of the wave's key slice (kLowpSteps steps),
+// rnd((acc + P.V) rnd(alpha)), the P.V products accumulated onto the rounded acc in fp32
+// by the MFMAs.  The
 // key slices of a row (each accumulated that way) are combined in fp32 at the end, rounded
 // to the input dtype, and multiplied by rnd(1/l) (one more rounding).
-template <int DT, int D, bool CAUSAL, bool TAIL, bool SPLIT, int TMR = 128, bool LOWP = false>
+template <int DT, int D, bool CAUSAL, bool TAIL, bool SPLIT, int TMR = 128, int LOWP_TN = 0>
 __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const WorkItem wi, char* lds_k0,
                                                   char* lds_k1, char* lds_v0, char* lds_v1) {
   constexpr int TM = TMR;            // query rows per workgroup
@@ -97,7 +98,12 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   static_assert(STAGE_A % (8 * 1024) == 0, "stage must split over the eight waves");
   static_assert(TK == kPPKeys && (TM == kPPRows || TM == 64), "steps of 128 keys, blocks of 128 or 64 rows");
   static_assert(TM == 128 || (!SPLIT && (D == 64 || D == 128)), "64-row blocks: whole rows, D 64 or 128");
+  constexpr bool LOWP = LOWP_TN != 0;
   static_assert(!LOWP || (!SPLIT && (D == 64 || D == 128)), "input-dtype accumulation: whole rows, D 64 or 128");
+  // Input-dtype accumulation: key steps between roundings of a wave's O, TILE_N keys of its
+  // key slice (64 keys a step with 128-row blocks, 32 with 64-row ones).
+  constexpr int kLowpSteps = LOWP ? LOWP_TN / (TMR == 128 ? 64 : 32) : 1;
+  static_assert(!LOWP || (kLowpSteps >= 1 && kLowpSteps <= 4), "TILE_N 64 or 128");
   // Raised MFMA-cluster priority only in the kernels built for two workgroups per CU (the
   // non-causal D = 64 whole-row ones, TA_PP_WAVES below).
   constexpr bool kPrioMfma = !SPLIT && D == 64 && !CAUSAL;
@@ -326,8 +332,8 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   // VALU cluster of step t: mask, row max, rescale, P = 2^(s*c - m*c) packed, l.  One
   // code path for every step (blocks without a needed key are masked whole), so the
   // rescale of O exists once and O keeps one register assignment through the loop.
-  auto softmax = [&](int t, auto par_tag) {
-    constexpr int PAR = decltype(par_tag)::value;  // t & 1 (whole rows start at step 0)
+  float lowp_alpha = 1.0f;  // input-dtype accumulation: this step's rescale of O
+  auto softmax = [&](int t) {
     // Blocks past the wave's last key are masked whole by the same test: all their keys
     // are past the wave's last query (causal) or past S.
     if (!(no_mask(t) && all_active(t))) {
@@ -418,30 +424,7 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
         }
       }
       l_part = l_part * alpha + ((l4[0] + l4[1]) + (l4[2] + l4[3]));
-      // The previous tile's accumulation (acc + P.V in fp32) rounded to the input dtype,
-      // rescaled first when some row's max moved: rnd((acc + P.V) rnd(alpha)).  A tile is 64
-      // keys of the wave's slice: with 64-row blocks (32 keys a step) every other step, the
-      // steps between only rescale.
-      const bool moved = __ballot(!(alpha == 1.0f)) != 0;
-      const float al = DTy::round(alpha);
-      constexpr bool kRoundHere = TM == 128 || PAR == 1;
-      if (kRoundHere || moved) {
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-#pragma unroll
-          for (int r = 0; r < 16; r += 2) {
-            if constexpr (kRoundHere) {
-              const uint32_t w = moved ? DTy::pack(o_acc[db][r] * al, o_acc[db][r + 1] * al)
-                                       : DTy::pack(o_acc[db][r], o_acc[db][r + 1]);
-              o_acc[db][r] = DTy::lo(w);
-              o_acc[db][r + 1] = DTy::hi(w);
-            } else {
-              o_acc[db][r] *= al;
-              o_acc[db][r + 1] *= al;
-            }
-          }
-        }
-      }
+      lowp_alpha = alpha;
 #pragma unroll
       for (int bk = 0; bk < KB; ++bk) {
 #pragma unroll
@@ -564,7 +547,32 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
     char* k_nxt = PAR ? lds_k0 : lds_k1;
     char* v_cur = PAR ? lds_v1 : lds_v0;
     char* v_nxt = PAR ? lds_v0 : lds_v1;
-    softmax(t, par_tag);
+    softmax(t);
+    if constexpr (LOWP) {
+      // The accumulation since the last rounding (acc + P.V in fp32) rounded to the input
+      // dtype once per kLowpSteps steps (TILE_N keys of the wave's key slice), rescaled
+      // first when some row's max moved: rnd((acc + P.V) rnd(alpha)); the steps between
+      // only rescale.
+      const bool moved = __ballot(!(lowp_alpha == 1.0f)) != 0;
+      const float al = DTy::round(lowp_alpha);
+      // t & 1 is PAR (whole rows start at step 0): known here unless kLowpSteps is 4.
+      const bool round_now = kLowpSteps == 1 || (kLowpSteps == 2 ? PAR == 1 : (PAR == 1 && (t & 2)));
+      if (round_now) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+#pragma unroll
+          for (int r = 0; r < 16; r += 2) {
+            const uint32_t w = moved ? DTy::pack(o_acc[db][r] * al, o_acc[db][r + 1] * al)
+                                     : DTy::pack(o_acc[db][r], o_acc[db][r + 1]);
+            o_acc[db][r] = DTy::lo(w);
+            o_acc[db][r + 1] = DTy::hi(w);
+          }
+        }
+      } else if (moved) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db) o_acc[db] *= al;
+      }
+    }
     wait_dma();  // this group's halves of K_{t+1} and V_t (issued one MFMA cluster ago)
     barrier();
     // MFMA cluster: S of step t + 1 (past the last step it reads a stale or zero stage and
@@ -980,7 +988,7 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
 // heaviest first, so each CU takes the next tile when its current one ends and heavy
 // tiles pair with light ones.  Split items cover a chunk of key steps of a block and
 // leave a partial (slot >= 0) when the block has more than one chunk.
-template <int DT, int D, bool CAUSAL, bool TAIL, bool SPLIT, bool PAIR, int TMR = 128, bool LOWP = false>
+template <int DT, int D, bool CAUSAL, bool TAIL, bool SPLIT, bool PAIR, int TMR = 128, int LOWP_TN = 0>
 __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   constexpr int STAGE = pp_stage_bytes(D);
   // One array per (tensor, stage): the stage of every access is a compile-time constant
@@ -1006,7 +1014,7 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
     const WorkItem wi = SPLIT ? split_item(blockIdx.x, p.n_bh, p.split_items, p.sched, CAUSAL,
                                            p.split_c, p.split_ns, p.split_slots, p.S)
                               : whole_item(blockIdx.x, p.n_bh, p.n_qblk, p.sched, CAUSAL);
-    attn_fwd_pp_block<DT, D, CAUSAL, TAIL, SPLIT, TMR, LOWP>(p, wi, lds_k0, lds_k1, lds_v0, lds_v1);
+    attn_fwd_pp_block<DT, D, CAUSAL, TAIL, SPLIT, TMR, LOWP_TN>(p, wi, lds_k0, lds_k1, lds_v0, lds_v1);
   }
 }
 
@@ -1104,26 +1112,27 @@ __device__ __forceinline__ void attn_merge_body(const FwdParams& p) {
   TA_PP64_DEFINE(DTN, DT, D, 1, 0)    \
   TA_PP64_DEFINE(DTN, DT, D, 1, 1)
 
-// Input-dtype accumulation (D = 64 and 128, whole rows): ta_fwd_ppl_<f16|bf16>_d<D>_c_t
-// (128-row blocks, tiles (128, 64) / (128, 128)) and ta_fwd_ppl64_<...> (64-row blocks,
-// tiles (64, 64) / (64, 128)).
+// Input-dtype accumulation (D = 64 and 128, whole rows), one kernel per TILE_N (the keys of
+// a wave's slice between roundings of O): ta_fwd_ppl_n<TN>_<f16|bf16>_d<D>_c_t (128-row
+// blocks, tiles (128, TN)) and ta_fwd_ppl64_n<TN>_<...> (64-row blocks, tiles (64, TN)).
 // One workgroup per CU (two waves per SIMD): at 128 VGPRs the exact max and the rounding of
 // O beside P spilled registers to scratch.
-#define TA_PPL_DEFINE(NAME, DTN, DT, D, C, T, TMR)                                          \
+#define TA_PPL_DEFINE(NAME, TN, DTN, DT, D, C, T, TMR)                                      \
   extern "C" __global__ void __launch_bounds__(512)                                       \
       __attribute__((amdgpu_waves_per_eu(2, 2)))                                          \
-      ta_fwd_##NAME##_##DTN##_d##D##_c##C##_t##T(ta::FwdParams p) {                        \
-    ta::attn_fwd_pp_body<DT, D, (C != 0), (T != 0), false, false, TMR, true>(p);          \
+      ta_fwd_##NAME##_n##TN##_##DTN##_d##D##_c##C##_t##T(ta::FwdParams p) {                \
+    ta::attn_fwd_pp_body<DT, D, (C != 0), (T != 0), false, false, TMR, TN>(p);            \
   }
-#define TA_PPL_DEFINE_CT(DTN, DT, D)            \
-  TA_PPL_DEFINE(ppl, DTN, DT, D, 0, 0, 128)     \
-  TA_PPL_DEFINE(ppl, DTN, DT, D, 0, 1, 128)     \
-  TA_PPL_DEFINE(ppl, DTN, DT, D, 1, 0, 128)     \
-  TA_PPL_DEFINE(ppl, DTN, DT, D, 1, 1, 128)     \
-  TA_PPL_DEFINE(ppl64, DTN, DT, D, 0, 0, 64)    \
-  TA_PPL_DEFINE(ppl64, DTN, DT, D, 0, 1, 64)    \
-  TA_PPL_DEFINE(ppl64, DTN, DT, D, 1, 0, 64)    \
-  TA_PPL_DEFINE(ppl64, DTN, DT, D, 1, 1, 64)
+#define TA_PPL_DEFINE_TCT(NAME, TN, DTN, DT, D, TMR) \
+  TA_PPL_DEFINE(NAME, TN, DTN, DT, D, 0, 0, TMR)     \
+  TA_PPL_DEFINE(NAME, TN, DTN, DT, D, 0, 1, TMR)     \
+  TA_PPL_DEFINE(NAME, TN, DTN, DT, D, 1, 0, TMR)     \
+  TA_PPL_DEFINE(NAME, TN, DTN, DT, D, 1, 1, TMR)
+#define TA_PPL_DEFINE_CT(DTN, DT, D)              \
+  TA_PPL_DEFINE_TCT(ppl, 64, DTN, DT, D, 128)     \
+  TA_PPL_DEFINE_TCT(ppl, 128, DTN, DT, D, 128)    \
+  TA_PPL_DEFINE_TCT(ppl64, 64, DTN, DT, D, 64)    \
+  TA_PPL_DEFINE_TCT(ppl64, 128, DTN, DT, D, 64)
 
 // Merge kernels of the split path: ta_fwd_merge_<f16|bf16>_d<D>_c<0|1>, merge_threads(D)
 // threads.

@@ -127,9 +127,14 @@ KernelId kernel_id(int dtype, int d, int tm, int tn, int causal, int tail, int a
     snprintf(buf, sizeof(buf), "ta_fwd_pp_%s_d%d_c%d_t%d", dt, d, causal ? 1 : 0, tail ? 1 : 0);
     return {"attn_fwd_pp.hsaco", buf, 512u};
   }
-  if (eight_wave64(tm, tn, accum, d) || eight_wave_lowp(tm, tn, accum, d)) {
-    const char* kind = eight_wave64(tm, tn, accum, d) ? "pp64" : tm == 128 ? "ppl" : "ppl64";
-    snprintf(buf, sizeof(buf), "ta_fwd_%s_%s_d%d_c%d_t%d", kind, dt, d, causal ? 1 : 0, tail ? 1 : 0);
+  if (eight_wave64(tm, tn, accum, d)) {
+    snprintf(buf, sizeof(buf), "ta_fwd_pp64_%s_d%d_c%d_t%d", dt, d, causal ? 1 : 0, tail ? 1 : 0);
+    return {"attn_fwd_pp.hsaco", buf, 512u};
+  }
+  if (eight_wave_lowp(tm, tn, accum, d)) {
+    // one kernel per tile_n: the keys of a wave's slice between roundings of O
+    snprintf(buf, sizeof(buf), "ta_fwd_%s_n%d_%s_d%d_c%d_t%d", tm == 128 ? "ppl" : "ppl64", tn, dt, d,
+             causal ? 1 : 0, tail ? 1 : 0);
     return {"attn_fwd_pp.hsaco", buf, 512u};
   }
   snprintf(buf, sizeof(buf), "ta_fwd_%s_d%d_m%d_n%d_c%d_t%d_a%d", dt, d, tm, tn, causal ? 1 : 0,
