@@ -332,8 +332,8 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   // VALU cluster of step t: mask, row max, rescale, P = 2^(s*c - m*c) packed, l.  One
   // code path for every step (blocks without a needed key are masked whole), so the
   // rescale of O exists once and O keeps one register assignment through the loop.
-  float lowp_alpha = 1.0f;  // input-dtype accumulation: this step's rescale of O
-  auto softmax = [&](int t) {
+  auto softmax = [&](int t, auto par_tag) {
+    constexpr int PAR = decltype(par_tag)::value;
     // Blocks past the wave's last key are masked whole by the same test: all their keys
     // are past the wave's last query (causal) or past S.
     if (!(no_mask(t) && all_active(t))) {
@@ -424,7 +424,29 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
         }
       }
       l_part = l_part * alpha + ((l4[0] + l4[1]) + (l4[2] + l4[3]));
-      lowp_alpha = alpha;
+      // The accumulation since the last rounding (acc + P.V in fp32) rounded to the input
+      // dtype once per kLowpSteps steps (TILE_N keys of the wave's key slice), rescaled
+      // first when some row's max moved: rnd((acc + P.V) rnd(alpha)); the steps between
+      // only rescale.  t & 1 is PAR (whole rows start at step 0): the cadence is known at
+      // compile time unless kLowpSteps is 4.
+      const bool moved = __ballot(!(alpha == 1.0f)) != 0;
+      const float al = DTy::round(alpha);
+      const bool round_now = kLowpSteps == 1 || (kLowpSteps == 2 ? PAR == 1 : (PAR == 1 && (t & 2)));
+      if (round_now) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+#pragma unroll
+          for (int r = 0; r < 16; r += 2) {
+            const uint32_t w = moved ? DTy::pack(o_acc[db][r] * al, o_acc[db][r + 1] * al)
+                                     : DTy::pack(o_acc[db][r], o_acc[db][r + 1]);
+            o_acc[db][r] = DTy::lo(w);
+            o_acc[db][r + 1] = DTy::hi(w);
+          }
+        }
+      } else if (moved) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db) o_acc[db] *= al;
+      }
 #pragma unroll
       for (int bk = 0; bk < KB; ++bk) {
 #pragma unroll
@@ -547,32 +569,7 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
     char* k_nxt = PAR ? lds_k0 : lds_k1;
     char* v_cur = PAR ? lds_v1 : lds_v0;
     char* v_nxt = PAR ? lds_v0 : lds_v1;
-    softmax(t);
-    if constexpr (LOWP) {
-      // The accumulation since the last rounding (acc + P.V in fp32) rounded to the input
-      // dtype once per kLowpSteps steps (TILE_N keys of the wave's key slice), rescaled
-      // first when some row's max moved: rnd((acc + P.V) rnd(alpha)); the steps between
-      // only rescale.
-      const bool moved = __ballot(!(lowp_alpha == 1.0f)) != 0;
-      const float al = DTy::round(lowp_alpha);
-      // t & 1 is PAR (whole rows start at step 0): known here unless kLowpSteps is 4.
-      const bool round_now = kLowpSteps == 1 || (kLowpSteps == 2 ? PAR == 1 : (PAR == 1 && (t & 2)));
-      if (round_now) {
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-#pragma unroll
-          for (int r = 0; r < 16; r += 2) {
-            const uint32_t w = moved ? DTy::pack(o_acc[db][r] * al, o_acc[db][r + 1] * al)
-                                     : DTy::pack(o_acc[db][r], o_acc[db][r + 1]);
-            o_acc[db][r] = DTy::lo(w);
-            o_acc[db][r + 1] = DTy::hi(w);
-          }
-        }
-      } else if (moved) {
-#pragma unroll
-        for (int db = 0; db < DB; ++db) o_acc[db] *= al;
-      }
-    }
+    softmax(t, par_tag);
     wait_dma();  // this group's halves of K_{t+1} and V_t (issued one MFMA cluster ago)
     barrier();
     // MFMA cluster: S of step t + 1 (past the last step it reads a stale or zero stage and
