@@ -106,6 +106,34 @@ def test_c4_noncausal_tile_sweep(gpu, dtype, d):
         check_close(as_f32(out, rows), ref, dtype, what=f"C4 {dtype} D={d} tiles={tm},{tn}")
 
 
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("d", [64, 128])
+def test_c4_input_dtype_accumulation(gpu, dtype, d):
+    """C4 with ACCUM_MODE=fp16 (flash_fwd.py:301-372) at every tile: 32-64 roundings of O
+    per key slice, sampled rows against the fp32 oracle at the input-dtype bound."""
+    q, k, v = inputs((4, 16, 4096, d), dtype, 2026, scale_inputs=0.5)
+    rows = sample_rows(4096, 64)
+    ref = oracle_f32(q, k, v, causal=False, rows=rows)
+    for tm, tn in TILES:
+        say(f"C4 {dtype} non-causal (4,16,4096,{d}) seed=2026 tiles=({tm},{tn}) accum fp16")
+        out = run_gpu(q, k, v, causal=False, tile_m=tm, tile_n=tn, accum_mode="fp16")
+        check_close(as_f32(out, rows), ref, dtype, tol=LOWP_TOL[dtype],
+                    what=f"C4 {dtype} D={d} tiles={tm},{tn} accum fp16")
+
+
+@pytest.mark.parametrize("tiles", [(None, None), (64, 128)])
+def test_c5_input_dtype_accumulation(gpu, tiles):
+    """C5 (S = 16384, fp16, causal) with ACCUM_MODE=fp16: up to 128 roundings of O per key
+    slice at TILE_N = 64, sampled rows (the last ones see every key) against the oracle."""
+    tm, tn = tiles
+    q, k, v = inputs((1, 8, 16384, 128), "float16", 1234)
+    rows = sample_rows(16384, 128)
+    ref = oracle_f32(q, k, v, causal=True, rows=rows)
+    say(f"C5 fp16 causal (1,8,16384,128) seed=1234 tiles=({tm},{tn}) accum fp16 rows={len(rows)}")
+    out = run_gpu(q, k, v, causal=True, tile_m=tm, tile_n=tn, accum_mode="fp16")
+    check_close(as_f32(out, rows), ref, "float16", tol=LOWP_TOL["float16"], what=f"C5 accum fp16 tiles={tm},{tn}")
+
+
 @pytest.mark.parametrize("outliers", [False, True])
 def test_c5_long_sequence_causal(gpu, outliers):
     """C5: B1 H8 S16384 D128 fp16 causal, seed 1234; C5b: 1% of k entries x20 (seed 1235)."""
