@@ -506,11 +506,20 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   // the compiler from moving memory accesses across the barrier.  Loads into LDS are
   // waited for explicitly (wait_dma) by the wave that issued them before the barrier that
   // publishes them.
+  // The barrier orders memory accesses only: the compiler issues the last few P.V MFMAs of
+  // a cluster (operands already in registers) after it, in the wave's softmax phase, where
+  // the MFMA pipe has room (3 of 32 at 128 rows; pinning all 32 in the cluster, or moving
+  // 5 or 8 out, measured 2-4 % slower).  The fp32 64-row kernels are pinned (sched_barrier):
+  // C3 S = 512 / 2048 -0.2 / -0.5 us against the one MFMA the compiler moves there (their
+  // input-dtype variants measured 2.4 % slower pinned and are not).
+  constexpr bool kPinPhases = TM == 64 && !LOWP;
   auto barrier = [&]() {
+    if constexpr (kPinPhases) __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(0xC07F);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    if constexpr (kPinPhases) __builtin_amdgcn_sched_barrier(0);
   };
 
   // ---- prologue and key loop ---------------------------------------------------------
