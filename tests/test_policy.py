@@ -268,6 +268,23 @@ def test_default_tile_prefers_64_rows_when_one_wave_of_blocks_fits(s, d, n_bh, a
                                                     accum_mode=accum) == expected
 
 
+@pytest.mark.parametrize("s,d,causal,n_bh,expected", [
+    (4096, 128, False, 64, (128, 128)),  # C4 D = 128: the reference's wider key tile
+    (2048, 128, False, 64, (128, 128)),
+    (2048, 128, False, 8, (64, 128)),    # 64-row blocks fit the CUs once
+    (2047, 128, False, 64, (128, 64)),   # S below 2048
+    (4096, 128, True, 64, (128, 64)),    # causal
+    (4096, 64, False, 64, (128, 64)),    # D = 64 (C4 D = 64)
+    (4096, 96, False, 64, (128, 64)),    # the caller's head dim, not the kernel's
+])
+def test_default_tile_n_follows_the_reference_rule(s, d, causal, n_bh, expected):
+    """TILE_N = 128 for non-causal D = 128 at S >= 2048, else 64 (flash_fwd.py:254-259): the
+    rounding cadence of input-dtype accumulation matches the reference's default."""
+    for accum in ("fp32", "fp16"):
+        assert ff._default_tile_config_for_shape_gfx950(seq_len=s, head_dim=d, causal=causal, n_bh=n_bh,
+                                                        accum_mode=accum) == expected
+
+
 def test_64_row_tiles_select_the_eight_wave_kernel():
     """Tiles (64, 64) / (64, 128) with fp32 accumulation at D = 64 / 128 run ta_fwd_pp64_*;
     the tail-masked variant whenever S is not a multiple of the 128-key step."""

@@ -224,12 +224,18 @@ def _default_tile_config_for_shape_gfx950(*, seq_len: int, head_dim: int, causal
     fixed cost of a workgroup again (B2 H16 S1024 causal: 16.4 -> 21.4 us), so 128 rows.
     The caller keeps 128 rows where the 128-row kernel would split key ranges
     (``_split_preferred``).
+
+    TILE_N follows the reference's rule (flash_fwd.py:254-259): 128 for non-causal
+    D = 128 at S >= 2048, else 64.  With fp32 accumulation both run the same kernels; with
+    input-dtype accumulation it is the rounding cadence of O (once per TILE_N keys), so
+    the default rounds as often as the reference's default does (C4 D = 128 bf16: 860 ->
+    979 TFLOP/s against TILE_N = 64).
     """
-    del causal
+    tile_n = 128 if (not causal and head_dim == 128 and seq_len >= 2048) else 64
     if (0 < head_dim <= 128 and n_bh > 0 and seq_len > 0
             and n_bh * ((seq_len + 63) // 64) <= _CU_COUNT):
-        return 64, 64
-    return 128, 64
+        return 64, tile_n
+    return 128, tile_n
 
 
 def _resolve_sync_mode() -> str:
@@ -496,7 +502,7 @@ def _build_plan(torch_mod, lib, q, k, v, causal: bool, tile: tuple[int, int] | N
             seq_len=seq_len, head_dim=head_dim, causal=causal, n_bh=bh, accum_mode=accum_mode
         )
         if tile_m == 64 and _split_preferred(lib, q, batch, heads, seq_len, head_dim, causal, torch_mod):
-            tile_m, tile_n = 128, 64
+            tile_m = 128
 
     chunk_plan = _resolve_chunk_plan(head_dim)
     kernel_head_dim, pad_dim = _resolve_kernel_head_dim_gfx950(head_dim)
