@@ -7,6 +7,8 @@ The names exported here match ``src/tiledattention/__init__.py:47-55`` of the re
 
 from __future__ import annotations
 
+import importlib as _importlib
+import sys as _sys
 from typing import TYPE_CHECKING
 
 from ._errors import (
@@ -31,9 +33,15 @@ def sdpa(
     scale: float | None = None,
 ) -> torch.Tensor:
     """Scaled dot-product attention forward; see ``tiledattention.sdpa.sdpa``."""
-    from .sdpa import sdpa as _sdpa
+    # The submodule's current ``sdpa`` on every call (as the reference's per-call import
+    # resolves it), found in sys.modules once it is imported.
+    mod = _sys.modules.get(_SDPA_MODULE)
+    if mod is None:
+        mod = _importlib.import_module(_SDPA_MODULE)
+    return mod.sdpa(q, k, v, causal=causal, scale=scale)
 
-    return _sdpa(q, k, v, causal=causal, scale=scale)
+
+_SDPA_MODULE = __name__ + ".sdpa"
 
 
 __all__ = [

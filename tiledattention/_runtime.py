@@ -83,6 +83,8 @@ def require_supported_runtime() -> None:
     """Raise unless torch sees a gfx950 GPU and the native library loads."""
     global _runtime_ready
 
+    if _runtime_ready:  # set only after every check below has passed
+        return
     with _runtime_lock:
         if _runtime_ready:
             return

@@ -458,7 +458,7 @@ def _knob_snapshot() -> tuple:
 class _LaunchPlan:
     """Everything a launch needs that does not depend on the tensors' addresses or the scale."""
 
-    __slots__ = ("generation", "empty", "out_shape", "head_dim", "pad_dim", "width",
+    __slots__ = ("generation", "empty", "out_shape", "out_like_q", "head_dim", "pad_dim", "width",
                  "copy", "args", "kernel", "chunk", "ws_bytes", "sync_mode", "device",
                  "device_index", "dtype")
 
@@ -530,6 +530,7 @@ def _build_plan(torch_mod, lib, q, k, v, causal: bool, tile: tuple[int, int] | N
     plan.pad_dim = 0 if pad_in_kernel else pad_dim
     plan.width = width
     plan.out_shape = (batch, heads, seq_len, width)
+    plan.out_like_q = width == head_dim
     plan.sync_mode = sync_mode
     plan.empty = bh == 0 or seq_len == 0
     if plan.empty:
@@ -633,7 +634,10 @@ def run_flash_fwd(
             _PLANS.clear()
         _PLANS[key] = plan
 
-    out = torch_mod.empty(plan.out_shape, dtype=plan.dtype, device=plan.device)
+    if plan.out_like_q and type(q) is torch_mod.Tensor:
+        out = torch_mod.empty_like(q, memory_format=torch_mod.contiguous_format)
+    else:
+        out = torch_mod.empty(plan.out_shape, dtype=plan.dtype, device=plan.device)
     if not plan.empty:
         wd, pad = plan.width, plan.pad_dim
         qk = _kernel_ready(torch_mod, q, wd, pad) if plan.copy[0] or q.data_ptr() % 16 else q

@@ -25,6 +25,16 @@ def _ensure_tensor(torch_mod: ModuleType, name: str, value: object) -> None:
 
 def validate_sdpa_inputs(torch_mod: ModuleType, q, k, v) -> None:
     """Check the SDPA input contract; raise the first violation found."""
+    tensor_type = torch_mod.Tensor
+    if type(q) is tensor_type and type(k) is tensor_type and type(v) is tensor_type:
+        # Every check below at once (plain tensors, 4-d, one shape, one CUDA device, one
+        # dtype in {fp16, bf16}); any failure takes the ordered checks for its message.
+        shape, dev, dt = q.shape, q.device, q.dtype
+        if (len(shape) == 4 and q.is_cuda and k.is_cuda and v.is_cuda and shape == k.shape
+                and shape == v.shape and dev == k.device and dev == v.device
+                and (dt is torch_mod.float16 or dt is torch_mod.bfloat16)
+                and dt == k.dtype and dt == v.dtype):
+            return
     _ensure_tensor(torch_mod, "q", q)
     _ensure_tensor(torch_mod, "k", k)
     _ensure_tensor(torch_mod, "v", v)
