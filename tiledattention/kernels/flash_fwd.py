@@ -304,8 +304,9 @@ class _Launcher:
         _raise_for_status(lib, st)
 
     def __call__(self, args: _lib.FwdArgs, stream: int) -> None:
-        st = self.lib.ta_sdpa_fwd(ctypes.byref(args), ctypes.c_void_p(stream))
-        _raise_for_status(self.lib, st)
+        st = self.lib.ta_sdpa_fwd(ctypes.byref(args), stream)  # c_void_p argtype takes the int
+        if st:
+            _raise_for_status(self.lib, st)
 
     def split(self, args: _lib.FwdArgs, chunk_steps: int, workspace: int, workspace_bytes: int,
               stream: int) -> None:
@@ -640,14 +641,16 @@ def run_flash_fwd(
         out = torch_mod.empty(plan.out_shape, dtype=plan.dtype, device=plan.device)
     if not plan.empty:
         wd, pad = plan.width, plan.pad_dim
-        qk = _kernel_ready(torch_mod, q, wd, pad) if plan.copy[0] or q.data_ptr() % 16 else q
-        kk = _kernel_ready(torch_mod, k, wd, pad) if plan.copy[1] or k.data_ptr() % 16 else k
-        vk = _kernel_ready(torch_mod, v, wd, pad) if plan.copy[2] or v.data_ptr() % 16 else v
+        qp, kp, vp = q.data_ptr(), k.data_ptr(), v.data_ptr()
         args = _lib.FwdArgs.from_buffer_copy(plan.args)
-        if qk is not q or kk is not k or vk is not v:
+        if plan.copy[0] or plan.copy[1] or plan.copy[2] or (qp | kp | vp) % 16:
+            qk = _kernel_ready(torch_mod, q, wd, pad) if plan.copy[0] or qp % 16 else q
+            kk = _kernel_ready(torch_mod, k, wd, pad) if plan.copy[1] or kp % 16 else k
+            vk = _kernel_ready(torch_mod, v, wd, pad) if plan.copy[2] or vp % 16 else v
             for name, t in (("q_stride", qk), ("k_stride", kk), ("v_stride", vk)):
                 getattr(args, name)[:] = tuple(t.stride())
-        args.q, args.k, args.v, args.o = qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), out.data_ptr()
+            qp, kp, vp = qk.data_ptr(), kk.data_ptr(), vk.data_ptr()
+        args.q, args.k, args.v, args.o = qp, kp, vp, out.data_ptr()
         args.scale = scale
         if plan.sync_mode == "strict":
             torch_mod.cuda.synchronize(plan.device)
