@@ -111,6 +111,11 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   // time there, since a phased softmax holds 32 exponent arguments beside the 32 scores.
   constexpr bool kPhasedP = !kPrioMfma;
   using DTy = DType<DT>;
+  // P.V MFMAs of a cluster issued after its closing barrier, in the wave's softmax phase
+  // (operands read in the cluster, held in registers): the 128-row input-dtype kernels, 3
+  // (C4 D = 128 -1.8 to -2.4 %, D = 64 -2 %, against the one the compiler moves there;
+  // 5 measured slower).  The other kernels leave it to the compiler (see barrier below).
+  constexpr int kLateMfma = TM == 128 && LOWP ? 3 : 0;
 
   static_assert(STAGE == pp_stage_bytes(D), "stage layout");
 
@@ -290,6 +295,7 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
 
   // O^T += V^T P^T of the step held in pk, from stage `vst`.  Every block: P is exactly 0
   // for masked keys.
+  u32x4 late_a[kLateMfma > 0 ? kLateMfma : 1];  // A operands of the late MFMAs
   auto pv = [&](const char* vst) {
 #pragma unroll
     for (int bk = 0; bk < KB; ++bk) {
@@ -307,6 +313,11 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
           u32x2 w0 = __builtin_bit_cast(u32x2, r0);
           u32x2 w1 = __builtin_bit_cast(u32x2, r1);
           const u32x4 a = {w0[0], w0[1], w1[0], w1[1]};
+          const int li = (bk * 2 + kc) * DB + db;  // issue order
+          if (li >= KB * 2 * DB - kLateMfma) {
+            late_a[li - (KB * 2 * DB - kLateMfma)] = a;
+            continue;
+          }
           o_acc[db] = DTy::mfma(a, bfrag, o_acc[db]);
         }
       }
@@ -485,10 +496,11 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
     constexpr int NQ = KB * DK;      // QK^T MFMAs
     constexpr int NP = KB * 2 * DB;  // P.V MFMAs
     constexpr int AHEAD = 4;
-    const int every = nv ? (NQ + NP) / nv : 0;
+    constexpr int NC = NQ + NP - kLateMfma;  // MFMAs in the cluster
+    const int every = nv ? NC / nv : 0;
     __builtin_amdgcn_sched_group_barrier(0x100, AHEAD, 0);
 #pragma unroll
-    for (int i = 0; i < NQ + NP; ++i) {
+    for (int i = 0; i < NC; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       const int j = i + AHEAD;  // MFMA whose operands are read now
       if (j < NQ) {
@@ -498,6 +510,9 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
       }
       if (every && i % every == 0) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
     }
+    // operand reads of late MFMAs not yet covered
+    constexpr int REM = NC + AHEAD < NQ + NP ? 2 * (NQ + NP - NC - AHEAD) : 0;
+    if constexpr (REM > 0) __builtin_amdgcn_sched_group_barrier(0x100, REM, 0);
   };
 
   // Workgroup barrier without a memory fence: a fence would also wait for this wave's
@@ -511,8 +526,9 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   // the MFMA pipe has room (3 of 32 at 128 rows; pinning all 32 in the cluster, or moving
   // 5 or 8 out, measured 2-4 % slower).  The fp32 64-row kernels are pinned (sched_barrier):
   // C3 S = 512 / 2048 -0.2 / -0.5 us against the one MFMA the compiler moves there (their
-  // input-dtype variants measured 2.4 % slower pinned and are not).
-  constexpr bool kPinPhases = TM == 64 && !LOWP;
+  // input-dtype variants measured 2.4 % slower pinned and are not).  Kernels with late
+  // MFMAs (kLateMfma) are pinned too, so that exactly those cross the barrier.
+  constexpr bool kPinPhases = (TM == 64 && !LOWP) || kLateMfma > 0;
   auto barrier = [&]() {
     if constexpr (kPinPhases) __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(0xC07F);
@@ -596,6 +612,15 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
     mfma_cluster_order(2 * NLDS);
     if constexpr (kPrioMfma) __builtin_amdgcn_s_setprio(0);
     barrier();
+    if constexpr (kLateMfma > 0) {
+#pragma unroll
+      for (int x = 0; x < kLateMfma; ++x) {
+        const int li = KB * 2 * DB - kLateMfma + x;
+        const int db = li % DB, bk = li / DB / 2, kc = li / DB % 2;
+        const u32x4 bfrag = {pk[bk][4 * kc + 0], pk[bk][4 * kc + 1], pk[bk][4 * kc + 2], pk[bk][4 * kc + 3]};
+        o_acc[db] = DTy::mfma(late_a[x], bfrag, o_acc[db]);
+      }
+    }
   };
   if (grp == 0) {
     first();
