@@ -75,6 +75,7 @@ def _call(lib, a):
     (dict(sched=4), _lib.TA_EINVAL, "sched"),
     (dict(S=-1), _lib.TA_EINVAL, "negative"),
     (dict(D=96), _lib.TA_EUNSUPPORTED, "head_dim"),
+    (dict(D=96, tile_m=128, accum=1), _lib.TA_EUNSUPPORTED, "head_dim 96 with tile (128, 64)"),
     (dict(D=160, tile_n=128), _lib.TA_EUNSUPPORTED, "tile_n 128 with head_dim 160"),
     (dict(D=512), _lib.TA_EUNSUPPORTED, "head_dim"),
     (dict(tile_m=32), _lib.TA_EUNSUPPORTED, "tile"),
@@ -199,7 +200,8 @@ def test_code_objects_built_for_gfx950():
 def test_kernel_symbol_names_exist_in_code_objects(tiles, accum):
     """The Python mirror of the C ABI's kernel choice names symbols the code objects hold."""
     for dtype in (_lib.TA_FP16, _lib.TA_BF16):
-        for d in (64, 128) + ((160, 256) if tiles[1] == 64 else ()):
+        for d in ((64, 128) + ((160, 256) if tiles[1] == 64 else ())
+                  + ((96,) if tiles[0] == 128 and accum == _lib.TA_ACC_FP32 else ())):
             for causal in (False, True):
                 for tail in (False, True):
                     f, sym = _lib.kernel_symbol(dtype=dtype, head_dim=d, tile_m=tiles[0],

@@ -18,6 +18,7 @@ from tests.parity_util import (
     as_f32,
     check_close,
     inputs,
+    knobs,
     oracle_f32,
     run_gpu,
     sample_rows,
@@ -256,6 +257,46 @@ def test_eight_wave_d160(gpu, d, dtype, causal, s):
     out = sdpa(*bshd, causal=causal)
     torch.cuda.synchronize()
     check_close(as_f32(out, rows), ref, dtype, what=f"eight-wave D={d} BSHD")
+
+
+@pytest.mark.parametrize("d,dtype,causal,s,tn", [
+    (96, "bfloat16", True, 2048, 64), (96, "float16", False, 1000, 128), (88, "bfloat16", False, 777, 64),
+    (72, "float16", True, 3000, 64), (80, "bfloat16", True, 128, 128), (96, "float16", True, 1, 64),
+])
+def test_eight_wave_d96(gpu, d, dtype, causal, s, tn):
+    """Kernel head dim 96 on the 128-row eight-wave kernel (tiles (128, 64) / (128, 128),
+    fp32 accumulation): stages split into a 64-column main part and a 32-column tail part,
+    three 32-wide d blocks of O (the odd-block merge); head dims 65-95 run in place with the
+    missing columns read as zero.  Ragged S, both dtypes, [B,S,H,D] views, split key ranges
+    (one-step chunks) and, causal, query-block pairs."""
+    import torch
+
+    from tiledattention import _lib, sdpa
+    from tiledattention.kernels import flash_fwd as ff
+
+    q, k, v = inputs((2, 3, s, d), dtype, 96 + d + s)
+    rows = None if s <= 2048 else sample_rows(s, 96)
+    ref = oracle_f32(q, k, v, causal=causal, rows=rows)
+    say(f"eight-wave D={d} -> 96 {dtype} (2,3,{s},{d}) causal={causal} tile (128,{tn})")
+    out = run_gpu(q, k, v, causal=causal, tile_m=128, tile_n=tn)
+    assert out.shape == (2, 3, s, d) and out.is_contiguous()
+    check_close(as_f32(out, rows), ref, dtype, what=f"eight-wave D={d} on the D=96 kernel")
+    assert any(pl.args is not None and _lib.FwdArgs.from_buffer_copy(pl.args).D == 96
+               for pl in ff._PLANS.values() if not pl.empty)
+    dev = torch.device("cuda:0")
+    bshd = [t.transpose(1, 2).contiguous().to(dev).transpose(1, 2) for t in (q, k, v)]
+    say(f"eight-wave D={d} -> 96 {dtype} (2,3,{s},{d}) causal={causal} [B,S,H,D] views")
+    with knobs(tile_m=128, tile_n=tn):
+        out = sdpa(*bshd, causal=causal)
+    torch.cuda.synchronize()
+    check_close(as_f32(out, rows), ref, dtype, what=f"eight-wave D={d} BSHD")
+    say(f"eight-wave D={d} -> 96 {dtype} (2,3,{s},{d}) causal={causal} split=1")
+    out = run_gpu(q, k, v, causal=causal, tile_m=128, tile_n=tn, split=1)
+    check_close(as_f32(out, rows), ref, dtype, what=f"eight-wave D={d} split")
+    if causal:
+        say(f"eight-wave D={d} -> 96 {dtype} (2,3,{s},{d}) causal pairs (sched 3)")
+        out = run_gpu(q, k, v, causal=True, tile_m=128, tile_n=tn, sched=3, split="off")
+        check_close(as_f32(out, rows), ref, dtype, what=f"eight-wave D={d} pairs")
 
 
 @pytest.mark.parametrize("tn", [64, 128])

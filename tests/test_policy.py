@@ -116,6 +116,21 @@ def test_gfx950_head_dim_padding(d, expected):
     assert ff._resolve_kernel_head_dim_gfx950(d) == expected
 
 
+@pytest.mark.parametrize("d,expected", [
+    (64, (64, 0)), (65, (96, 31)), (72, (96, 24)), (96, (96, 0)), (97, (128, 31)), (128, (128, 0)),
+    (160, (160, 0)),
+])
+def test_gfx950_native_96_head_dim(d, expected):
+    """128-row tiles with fp32 accumulation have a D = 96 kernel: head dims in (64, 96] run
+    on it (padding to 96, not 128); the other paths keep the D = 128 kernel."""
+    assert ff._resolve_kernel_head_dim_gfx950(d, native_96=True) == expected
+    if 64 < d <= 96:
+        assert ff._resolve_kernel_head_dim_gfx950(d) == (128, 128 - d)
+        sym = _lib.kernel_symbol(dtype=_lib.TA_BF16, head_dim=96, tile_m=128, tile_n=64, causal=True,
+                                 tail=False, accum=_lib.TA_ACC_FP32)
+        assert sym == ("attn_fwd_pp.hsaco", "ta_fwd_pp_bf16_d96_c1_t0")
+
+
 @pytest.mark.parametrize("d", [0, -1, 257, 512])
 def test_gfx950_head_dim_rejects(d):
     with pytest.raises(InvalidShapeError):

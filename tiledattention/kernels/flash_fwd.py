@@ -35,7 +35,8 @@ Environment knobs are re-read on every call, as in the reference:
 ``TILEDATTN_CHUNKED_HEAD_DIMS``
     Parsed as in flash_fwd.py:166-196.  A chunked plan computes the same attention as the
     unchunked one, so here it runs the kernel that serves the head dim unchunked (96 on the
-    D = 128 kernel with in-kernel padding, 160 on the native D = 160 kernel).
+    native D = 96 kernel with 128-row tiles and fp32 accumulation, else on the D = 128
+    kernel with in-kernel padding; 160 on the native D = 160 kernel).
 ``TILEDATTN_SCHED`` (this build only)
     Workgroup-to-tile order: ``0`` plain, ``1`` XCD-grouped (large causal grids on the
     eight-wave kernel run query blocks in pairs, see ``ta_fwd_args.sched``), ``2``
@@ -148,17 +149,21 @@ def _resolve_accum_mode(*, seq_len: int, head_dim: int, causal: bool) -> str:
     return mode
 
 
-def _resolve_kernel_head_dim_gfx950(head_dim: int) -> tuple[int, int]:
+def _resolve_kernel_head_dim_gfx950(head_dim: int, *, native_96: bool = False) -> tuple[int, int]:
     """Head dim of the gfx950 kernel that runs ``head_dim``, and the zero padding to add.
 
-    Kernels exist for D = 64, 128, 160 and 256.  Other head dims are zero-padded to the next
-    of them, which leaves Q K^T unchanged and only adds zero output columns that are sliced
-    off (the reference pads the same way, to a power of two, flash_fwd.py:149-163; its
-    160 = 128 + 32 chunk plan, :21-24, computes the same contraction as the native D = 160
-    kernel here).  Above 256 there is no kernel.
+    Kernels exist for D = 64, 128, 160 and 256, and D = 96 on the 128-row eight-wave kernel
+    with fp32 accumulation (``native_96``: tile (128, 64) or (128, 128), fp32).  Other head
+    dims are zero-padded to the next of them, which leaves Q K^T unchanged and only adds
+    zero output columns that are sliced off (the reference pads the same way, to a power of
+    two, flash_fwd.py:149-163; its 96 = 64 + 32 and 160 = 128 + 32 chunk plans, :21-24,
+    compute the same contractions as the native D = 96 and 160 kernels here).  Above 256
+    there is no kernel.
     """
     if head_dim <= 0:
         raise InvalidShapeError("head dimension D must be positive.")
+    if native_96 and 64 < head_dim <= 96:
+        return 96, 96 - head_dim
     for kd in _KERNEL_HEAD_DIMS:
         if head_dim <= kd:
             return kd, kd - head_dim
@@ -376,7 +381,7 @@ def _split_preferred(lib, q, batch: int, heads: int, seq_len: int, head_dim: int
         return False
     if raw not in ("", "auto"):
         return True
-    kernel_head_dim, _ = _resolve_kernel_head_dim_gfx950(head_dim)
+    kernel_head_dim, _ = _resolve_kernel_head_dim_gfx950(head_dim, native_96=True)
     args = _lib.FwdArgs()
     args.B, args.H, args.S, args.D = batch, heads, seq_len, kernel_head_dim
     args.causal = int(causal)
@@ -506,7 +511,8 @@ def _build_plan(torch_mod, lib, q, k, v, causal: bool, tile: tuple[int, int] | N
             tile_m = 128
 
     chunk_plan = _resolve_chunk_plan(head_dim)
-    kernel_head_dim, pad_dim = _resolve_kernel_head_dim_gfx950(head_dim)
+    kernel_head_dim, pad_dim = _resolve_kernel_head_dim_gfx950(
+        head_dim, native_96=tile_m == 128 and tile_n in (64, 128) and accum_mode == "fp32")
     if kernel_head_dim > 128 and tile_n != _WIDE_HEAD_DIM_TILE_N:
         if explicit_tile:
             raise ValueError(

@@ -76,12 +76,13 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   constexpr int NRB = TM / 32;       // 32-row blocks
   constexpr int NKS = 4 / NRB;       // key slots of a group's 64 keys (1 or 2)
   constexpr int KB = 2 / NKS;        // 32-key blocks per wave per step
-  // A stage holds 128 key rows: the first DA = min(D, 128) columns of each row in a main
-  // part (rows of 2 DA bytes), the rest (D = 160: 32 columns) in a tail part of 64-byte
-  // rows behind it, so both parts have power-of-two rows.
-  constexpr int DA = D > 128 ? 128 : D;
+  // A stage holds 128 key rows: the first DA columns of each row in a main part (rows of
+  // 2 DA bytes; DA = 128 at D = 160, 64 at D = 96, D otherwise), the rest (32 columns at
+  // D = 96 and 160) in a tail part of 64-byte rows behind it, so both parts have
+  // power-of-two rows.
+  constexpr int DA = D > 128 ? 128 : D == 96 ? 64 : D;
   constexpr int DT2 = D - DA;        // tail columns
-  static_assert(DT2 == 0 || DT2 == 32, "head dims 64, 128 and 160");
+  static_assert(DT2 == 0 || DT2 == 32, "head dims 64, 96, 128 and 160");
   constexpr int DK = D / 16;         // k-steps of the QK^T product
   constexpr int DKA = DA / 16;       // ... whose K operand is in the main part
   constexpr int DB = D / 32;         // 32-wide d blocks of O
@@ -1129,7 +1130,7 @@ __device__ __forceinline__ void attn_merge_body(const FwdParams& p) {
     ta::attn_fwd_pp_body<DT, D, (C != 0), (T != 0), true, false>(p);                      \
   }
 
-// Causal query-block pairs (whole rows, D = 64 and 128): ta_fwd_pp_pair_<f16|bf16>_d<D>_c1_t<0|1>.
+// Causal query-block pairs (whole rows, D = 64, 96 and 128): ta_fwd_pp_pair_<f16|bf16>_d<D>_c1_t<0|1>.
 #define TA_PP_PAIR_DEFINE(DTN, DT, D, T)                                                   \
   extern "C" __global__ void __launch_bounds__(512)                                       \
       __attribute__((amdgpu_waves_per_eu(2, 2)))                                          \
@@ -1190,17 +1191,23 @@ __device__ __forceinline__ void attn_merge_body(const FwdParams& p) {
   TA_MERGE_DEFINE(DTN, DT, D, 1)
 
 TA_PP_DEFINE_CT(f16, 0, 64)
+TA_PP_DEFINE_CT(f16, 0, 96)
 TA_PP_DEFINE_CT(f16, 0, 128)
 TA_PP_DEFINE_CT(f16, 0, 160)
 TA_PP_DEFINE_CT(bf16, 1, 64)
+TA_PP_DEFINE_CT(bf16, 1, 96)
 TA_PP_DEFINE_CT(bf16, 1, 128)
 TA_PP_DEFINE_CT(bf16, 1, 160)
 TA_PP_PAIR_DEFINE(f16, 0, 64, 0)
 TA_PP_PAIR_DEFINE(f16, 0, 64, 1)
+TA_PP_PAIR_DEFINE(f16, 0, 96, 0)
+TA_PP_PAIR_DEFINE(f16, 0, 96, 1)
 TA_PP_PAIR_DEFINE(f16, 0, 128, 0)
 TA_PP_PAIR_DEFINE(f16, 0, 128, 1)
 TA_PP_PAIR_DEFINE(bf16, 1, 64, 0)
 TA_PP_PAIR_DEFINE(bf16, 1, 64, 1)
+TA_PP_PAIR_DEFINE(bf16, 1, 96, 0)
+TA_PP_PAIR_DEFINE(bf16, 1, 96, 1)
 TA_PP_PAIR_DEFINE(bf16, 1, 128, 0)
 TA_PP_PAIR_DEFINE(bf16, 1, 128, 1)
 TA_PP64_DEFINE_CT(f16, 0, 64)

@@ -90,7 +90,7 @@ struct KernelId {
 };
 
 // The eight-wave kernel (attn_fwd_pp.hip) serves 128-row tiles with fp32 accumulation at
-// D = 64, 128 and 160: its workgroup step is 128 rows x 128 keys, 64 keys per wave group,
+// D = 64, 96, 128 and 160: its workgroup step is 128 rows x 128 keys, 64 keys per wave group,
 // so it stands for both TILE_N = 64 and TILE_N = 128 (the latter only up to D = 128,
 // check_shape).
 bool eight_wave(int64_t tm, int64_t tn, int64_t accum, int64_t d) {
@@ -154,15 +154,20 @@ KernelId pair_kernel_id(int dtype, int d, int tail) {
 
 bool valid_tile(int t) { return t == 64 || t == 128; }
 
-bool valid_head_dim(int64_t d) { return d == 64 || d == 128 || d == 160 || d == 256; }
+bool valid_head_dim(int64_t d) { return d == 64 || d == 96 || d == 128 || d == 160 || d == 256; }
 
-// Head dims above 128 exist only with 64-key tiles (two stages of wider rows fill the LDS).
-ta_status check_shape(int64_t d, int tile_m, int tile_n) {
+// Head dims above 128 exist only with 64-key tiles (two stages of wider rows fill the LDS);
+// D = 96 only on the 128-row eight-wave kernel (fp32 accumulation).
+ta_status check_shape(int64_t d, int tile_m, int tile_n, int accum) {
   if (!valid_head_dim(d))
-    return fail(TA_EUNSUPPORTED, "head_dim %lld (kernels exist for 64, 128, 160 and 256)",
+    return fail(TA_EUNSUPPORTED, "head_dim %lld (kernels exist for 64, 96, 128, 160 and 256)",
                 (long long)d);
   if (!valid_tile(tile_m) || !valid_tile(tile_n))
     return fail(TA_EUNSUPPORTED, "tile (%d, %d) (supported: 64 or 128 each)", tile_m, tile_n);
+  if (d == 96 && !eight_wave(tile_m, tile_n, accum, d))
+    return fail(TA_EUNSUPPORTED,
+                "head_dim 96 with tile (%d, %d) and accum %d (D = 96 kernels: tile (128, 64) or "
+                "(128, 128) with fp32 accumulation)", tile_m, tile_n, accum);
   if (d > 128 && tile_n != 64)
     return fail(TA_EUNSUPPORTED, "tile_n %d with head_dim %lld (head dims above 128 need tile_n 64)",
                 tile_n, (long long)d);
@@ -365,7 +370,7 @@ ta_status validate_args(const ta_fwd_args* a, int64_t* n_bh_out, int64_t* n_qblk
                   "input-dtype accumulation");
   }
   if (a->B < 0 || a->H < 0 || a->S < 0) return fail(TA_EINVAL, "negative shape");
-  ta_status shape_st = check_shape(a->D, a->tile_m, a->tile_n);
+  ta_status shape_st = check_shape(a->D, a->tile_m, a->tile_n, a->accum);
   if (shape_st != TA_OK) return shape_st;
   *n_bh_out = a->B * a->H;
   *n_qblk_out = 0;
@@ -511,9 +516,9 @@ ta_status ta_set_code_object_dir(const char* dir) {
 ta_status ta_prepare(int32_t device, int32_t dtype, int32_t head_dim, int32_t tile_m,
                      int32_t tile_n, int32_t causal, int32_t accum, int32_t aligned) {
   if (dtype != TA_FP16 && dtype != TA_BF16) return fail(TA_EINVAL, "dtype %d", dtype);
-  ta_status shape_st = check_shape(head_dim, tile_m, tile_n);
-  if (shape_st != TA_OK) return shape_st;
   if (accum != TA_ACC_FP32 && accum != TA_ACC_INPUT) return fail(TA_EINVAL, "accum %d", accum);
+  ta_status shape_st = check_shape(head_dim, tile_m, tile_n, accum);
+  if (shape_st != TA_OK) return shape_st;
   std::lock_guard<std::mutex> lock(g_mu);
   DeviceGuard guard(device);
   if (guard.err != hipSuccess)
