@@ -56,8 +56,8 @@ typedef struct ta_fwd_args {
   const void* v;
   void* o;
   int64_t B, H, S, D; /* D: 64, 96, 128, 160 or 256 (callers zero-pad other head dims,
-                         or set d_real); 160 and 256 need tile_n = 64, 96 tile (128, 64)
-                         or (128, 128) with fp32 accumulation */
+                         or set d_real); 160 and 256 need tile_n = 64, 96 fp32
+                         accumulation */
   int64_t q_stride[4]; /* element strides for (B,H,S,D); stride[3] must be 1, the others
                           non-negative multiples of 8; the row stride stride[2] at least
                           the row width (D, or d_real when set: rows must not overlap)

@@ -74,8 +74,9 @@ def _call(lib, a):
     (dict(causal=2), _lib.TA_EINVAL, "causal"),
     (dict(sched=4), _lib.TA_EINVAL, "sched"),
     (dict(S=-1), _lib.TA_EINVAL, "negative"),
-    (dict(D=96), _lib.TA_EUNSUPPORTED, "head_dim"),
+    (dict(D=96, accum=1), _lib.TA_EUNSUPPORTED, "head_dim 96 with tile (64, 64)"),
     (dict(D=96, tile_m=128, accum=1), _lib.TA_EUNSUPPORTED, "head_dim 96 with tile (128, 64)"),
+    (dict(D=80), _lib.TA_EUNSUPPORTED, "head_dim"),
     (dict(D=160, tile_n=128), _lib.TA_EUNSUPPORTED, "tile_n 128 with head_dim 160"),
     (dict(D=512), _lib.TA_EUNSUPPORTED, "head_dim"),
     (dict(tile_m=32), _lib.TA_EUNSUPPORTED, "tile"),
@@ -152,7 +153,8 @@ def test_zero_size_is_ok_without_launch(lib, kw):
 
 @pytest.mark.parametrize("args,status", [
     ((0, 3, 64, 64, 64, 0, 0, 1), _lib.TA_EINVAL),        # dtype
-    ((0, 0, 96, 64, 64, 0, 0, 1), _lib.TA_EUNSUPPORTED),  # head dim
+    ((0, 0, 80, 64, 64, 0, 0, 1), _lib.TA_EUNSUPPORTED),  # head dim
+    ((0, 0, 96, 64, 64, 0, 1, 1), _lib.TA_EUNSUPPORTED),  # D = 96 with input-dtype accumulation
     ((0, 0, 64, 48, 64, 0, 0, 1), _lib.TA_EUNSUPPORTED),  # tile
     ((0, 0, 64, 64, 64, 0, 9, 1), _lib.TA_EINVAL),        # accum
 ])
@@ -170,7 +172,7 @@ def test_cache_calls_and_code_object_dir(lib):
 def test_error_text_is_thread_local(lib):
     import threading
 
-    _call(lib, _args(D=96))
+    _call(lib, _args(D=80))
     seen = {}
 
     def other():
@@ -201,7 +203,7 @@ def test_kernel_symbol_names_exist_in_code_objects(tiles, accum):
     """The Python mirror of the C ABI's kernel choice names symbols the code objects hold."""
     for dtype in (_lib.TA_FP16, _lib.TA_BF16):
         for d in ((64, 128) + ((160, 256) if tiles[1] == 64 else ())
-                  + ((96,) if tiles[0] == 128 and accum == _lib.TA_ACC_FP32 else ())):
+                  + ((96,) if accum == _lib.TA_ACC_FP32 else ())):
             for causal in (False, True):
                 for tail in (False, True):
                     f, sym = _lib.kernel_symbol(dtype=dtype, head_dim=d, tile_m=tiles[0],

@@ -264,11 +264,12 @@ def test_eight_wave_d160(gpu, d, dtype, causal, s):
     (72, "float16", True, 3000, 64), (80, "bfloat16", True, 128, 128), (96, "float16", True, 1, 64),
 ])
 def test_eight_wave_d96(gpu, d, dtype, causal, s, tn):
-    """Kernel head dim 96 on the 128-row eight-wave kernel (tiles (128, 64) / (128, 128),
-    fp32 accumulation): stages split into a 64-column main part and a 32-column tail part,
-    three 32-wide d blocks of O (the odd-block merge); head dims 65-95 run in place with the
-    missing columns read as zero.  Ragged S, both dtypes, [B,S,H,D] views, split key ranges
-    (one-step chunks) and, causal, query-block pairs."""
+    """Kernel head dim 96 on the eight-wave kernels with fp32 accumulation: stages split
+    into a 64-column main part and a 32-column tail part, three 32-wide d blocks of O (the
+    odd-block merge at 128 rows, the four-way merge of three chunks a part at 64 rows); head
+    dims 65-95 run in place with the missing columns read as zero.  Ragged S, both dtypes,
+    both row counts, [B,S,H,D] views, split key ranges (one-step chunks) and, causal,
+    query-block pairs."""
     import torch
 
     from tiledattention import _lib, sdpa
@@ -290,6 +291,9 @@ def test_eight_wave_d96(gpu, d, dtype, causal, s, tn):
         out = sdpa(*bshd, causal=causal)
     torch.cuda.synchronize()
     check_close(as_f32(out, rows), ref, dtype, what=f"eight-wave D={d} BSHD")
+    say(f"64-row D={d} -> 96 {dtype} (2,3,{s},{d}) causal={causal} tile (64,{tn})")
+    out = run_gpu(q, k, v, causal=causal, tile_m=64, tile_n=tn)
+    check_close(as_f32(out, rows), ref, dtype, what=f"64-row D={d} on the D=96 kernel")
     say(f"eight-wave D={d} -> 96 {dtype} (2,3,{s},{d}) causal={causal} split=1")
     out = run_gpu(q, k, v, causal=causal, tile_m=128, tile_n=tn, split=1)
     check_close(as_f32(out, rows), ref, dtype, what=f"eight-wave D={d} split")

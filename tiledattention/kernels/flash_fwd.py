@@ -152,8 +152,8 @@ def _resolve_accum_mode(*, seq_len: int, head_dim: int, causal: bool) -> str:
 def _resolve_kernel_head_dim_gfx950(head_dim: int, *, native_96: bool = False) -> tuple[int, int]:
     """Head dim of the gfx950 kernel that runs ``head_dim``, and the zero padding to add.
 
-    Kernels exist for D = 64, 128, 160 and 256, and D = 96 on the 128-row eight-wave kernel
-    with fp32 accumulation (``native_96``: tile (128, 64) or (128, 128), fp32).  Other head
+    Kernels exist for D = 64, 128, 160 and 256, and D = 96 on the eight-wave kernels with
+    fp32 accumulation (``native_96``).  Other head
     dims are zero-padded to the next of them, which leaves Q K^T unchanged and only adds
     zero output columns that are sliced off (the reference pads the same way, to a power of
     two, flash_fwd.py:149-163; its 96 = 64 + 32 and 160 = 128 + 32 chunk plans, :21-24,
@@ -512,7 +512,7 @@ def _build_plan(torch_mod, lib, q, k, v, causal: bool, tile: tuple[int, int] | N
 
     chunk_plan = _resolve_chunk_plan(head_dim)
     kernel_head_dim, pad_dim = _resolve_kernel_head_dim_gfx950(
-        head_dim, native_96=tile_m == 128 and tile_n in (64, 128) and accum_mode == "fp32")
+        head_dim, native_96=tile_n in (64, 128) and accum_mode == "fp32")
     if kernel_head_dim > 128 and tile_n != _WIDE_HEAD_DIM_TILE_N:
         if explicit_tile:
             raise ValueError(

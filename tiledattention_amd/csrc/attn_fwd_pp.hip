@@ -98,7 +98,8 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   constexpr int NLDS = NLD + NLDT;   // loads per wave per tensor per step (own half)
   static_assert(STAGE_A % (8 * 1024) == 0, "stage must split over the eight waves");
   static_assert(TK == kPPKeys && (TM == kPPRows || TM == 64), "steps of 128 keys, blocks of 128 or 64 rows");
-  static_assert(TM == 128 || (!SPLIT && (D == 64 || D == 128)), "64-row blocks: whole rows, D 64 or 128");
+  static_assert(TM == 128 || (!SPLIT && (D == 64 || D == 96 || D == 128)),
+                "64-row blocks: whole rows, D 64, 96 or 128");
   constexpr bool LOWP = LOWP_TN != 0;
   static_assert(!LOWP || (!SPLIT && (D == 64 || D == 128)), "input-dtype accumulation: whole rows, D 64 or 128");
   // Input-dtype accumulation: key steps between roundings of a wave's O, TILE_N keys of its
@@ -1138,7 +1139,7 @@ __device__ __forceinline__ void attn_merge_body(const FwdParams& p) {
     ta::attn_fwd_pp_body<DT, D, true, (T != 0), false, true>(p);                          \
   }
 
-// 64-row blocks (tiles (64, 64) and (64, 128) with fp32 accumulation, D = 64 and 128):
+// 64-row blocks (tiles (64, 64) and (64, 128) with fp32 accumulation, D = 64, 96 and 128):
 // ta_fwd_pp64_<f16|bf16>_d<D>_c<0|1>_t<0|1>, the same residency as the 128-row kernels.
 #define TA_PP64_DEFINE(DTN, DT, D, C, T)                                                   \
   extern "C" __global__ void __launch_bounds__(512)                                       \
@@ -1211,8 +1212,10 @@ TA_PP_PAIR_DEFINE(bf16, 1, 96, 1)
 TA_PP_PAIR_DEFINE(bf16, 1, 128, 0)
 TA_PP_PAIR_DEFINE(bf16, 1, 128, 1)
 TA_PP64_DEFINE_CT(f16, 0, 64)
+TA_PP64_DEFINE_CT(f16, 0, 96)
 TA_PP64_DEFINE_CT(f16, 0, 128)
 TA_PP64_DEFINE_CT(bf16, 1, 64)
+TA_PP64_DEFINE_CT(bf16, 1, 96)
 TA_PP64_DEFINE_CT(bf16, 1, 128)
 TA_PPL_DEFINE_CT(f16, 0, 64)
 TA_PPL_DEFINE_CT(f16, 0, 128)

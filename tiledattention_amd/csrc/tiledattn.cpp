@@ -97,11 +97,11 @@ bool eight_wave(int64_t tm, int64_t tn, int64_t accum, int64_t d) {
   return tm == 128 && (tn == 64 || tn == 128) && accum == TA_ACC_FP32 && d <= 160;
 }
 
-// Its 64-row form (ta_fwd_pp64_*) serves the 64-row tiles with fp32 accumulation at D = 64
-// and 128: the same 128-key steps, each group's 64 keys split between two waves per row
+// Its 64-row form (ta_fwd_pp64_*) serves the 64-row tiles with fp32 accumulation at D = 64,
+// 96 and 128: the same 128-key steps, each group's 64 keys split between two waves per row
 // block, and no split key ranges or causal pairs.
 bool eight_wave64(int64_t tm, int64_t tn, int64_t accum, int64_t d) {
-  return tm == 64 && (tn == 64 || tn == 128) && accum == TA_ACC_FP32 && (d == 64 || d == 128);
+  return tm == 64 && (tn == 64 || tn == 128) && accum == TA_ACC_FP32 && (d == 64 || d == 96 || d == 128);
 }
 
 // Input-dtype accumulation on the eight-wave kernels (ta_fwd_ppl_* for 128-row tiles,
@@ -157,17 +157,17 @@ bool valid_tile(int t) { return t == 64 || t == 128; }
 bool valid_head_dim(int64_t d) { return d == 64 || d == 96 || d == 128 || d == 160 || d == 256; }
 
 // Head dims above 128 exist only with 64-key tiles (two stages of wider rows fill the LDS);
-// D = 96 only on the 128-row eight-wave kernel (fp32 accumulation).
+// D = 96 only on the eight-wave kernels with fp32 accumulation.
 ta_status check_shape(int64_t d, int tile_m, int tile_n, int accum) {
   if (!valid_head_dim(d))
     return fail(TA_EUNSUPPORTED, "head_dim %lld (kernels exist for 64, 96, 128, 160 and 256)",
                 (long long)d);
   if (!valid_tile(tile_m) || !valid_tile(tile_n))
     return fail(TA_EUNSUPPORTED, "tile (%d, %d) (supported: 64 or 128 each)", tile_m, tile_n);
-  if (d == 96 && !eight_wave(tile_m, tile_n, accum, d))
+  if (d == 96 && accum != TA_ACC_FP32)
     return fail(TA_EUNSUPPORTED,
-                "head_dim 96 with tile (%d, %d) and accum %d (D = 96 kernels: tile (128, 64) or "
-                "(128, 128) with fp32 accumulation)", tile_m, tile_n, accum);
+                "head_dim 96 with tile (%d, %d) and accum %d (D = 96 kernels: fp32 accumulation)",
+                tile_m, tile_n, accum);
   if (d > 128 && tile_n != 64)
     return fail(TA_EUNSUPPORTED, "tile_n %d with head_dim %lld (head dims above 128 need tile_n 64)",
                 tile_n, (long long)d);
