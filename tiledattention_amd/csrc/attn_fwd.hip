@@ -28,9 +28,9 @@
 // * Causal: tiles above the diagonal are never loaded by a wave that does not need them,
 //   32-key blocks above a wave's rows are skipped, and only the diagonal block is masked.
 // * fp32 accumulation rescales O lazily: the running max used for the exponent is only
-//   raised (and O rescaled) when a row's max grows by more than 2^8; final O = acc / l is
-//   independent of the reference point, and P stays below 256, well inside fp16/bf16
-//   range.  l is summed from the rounded P that feeds P.V (consistent normalisation).
+//   raised (and O rescaled) when a row's max grows by more than 2^kRescaleLog2 (2^15);
+//   final O = acc / l is independent of the reference point, and P stays at or below
+//   2^15, inside fp16/bf16 range.  l is summed from the rounded P that feeds P.V (consistent normalisation).
 //   Input-dtype accumulation rescales every tile and follows the reference's rounding
 //   sequence (acc = rnd(rnd(acc*rnd(alpha)) + rnd(P.V)), l from the unrounded P).
 #include <hip/hip_runtime.h>

@@ -25,7 +25,7 @@
 // * Operand layouts are those of the 128 x 64 kernel (attn_fwd.hip): scores transposed so
 //   a lane owns one query, row reductions in-lane plus v_permlane32_swap, P packed from the
 //   score registers straight into the B operand of the P.V MFMA, exp2 with scale*log2(e)
-//   folded into one FMA, lazy rescale of O with a 2^8 threshold, l summed from the rounded
+//   folded into one FMA, lazy rescale of O with a 2^15 threshold, l summed from the rounded
 //   P.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
