@@ -392,6 +392,30 @@ def test_chunked_head_dim_knob_matches_unchunked(gpu):
     assert bool((a == b).all())
 
 
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("causal", [False, True])
+def test_rising_logits_lazy_rescale(gpu, dtype, causal):
+    """Key logits rising along S (0 to 116 log2 units over the sequence, q constant): each
+    key slice's running max grows by about 14.5 log2 units a step, so P reaches ~2^14.5
+    against a stale reference point before the lazy rescale (threshold 2^15) moves it, and
+    moves it again a step later.  Checks that such P packs to the input dtype and the
+    rescales keep O/l exact, against the oracle."""
+    import torch
+
+    s, d = 1024, 64
+    q = torch.ones(1, 2, s, d, dtype=torch.float32)
+    beta = torch.linspace(0.0, 116.0 / (8.0 * 1.4426950408889634), s)  # scale 1/8: s*c = 11.54 beta
+    k = beta.view(1, 1, s, 1).expand(1, 2, s, d).clone()
+    g = torch.Generator().manual_seed(7)
+    v = torch.randn(1, 2, s, d, generator=g)
+    q, k, v = (t.to(getattr(torch, dtype)) for t in (q, k, v))
+    ref = oracle_f32(q, k, v, causal=causal)
+    say(f"rising logits {dtype} (1,2,{s},{d}) causal={causal}")
+    for tile in ((None, None), (128, 64), (64, 64)):
+        out = run_gpu(q, k, v, causal=causal, tile_m=tile[0], tile_n=tile[1])
+        check_close(as_f32(out), ref, dtype, what=f"rising logits tile={tile}")
+
+
 def test_custom_scale(gpu):
     q, k, v = inputs((1, 4, 300, 64), "float16", 11)
     for scale in (0.05, 1.0, 0.3):
