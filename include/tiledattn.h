@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define TA_ABI_VERSION 2
+#define TA_ABI_VERSION 3
 
 typedef enum ta_status {
   TA_OK = 0,
@@ -123,16 +123,24 @@ ta_status ta_sdpa_fwd(const ta_fwd_args* args, void* stream);
  * (128, 64) and (128, 128) with fp32 accumulation and D <= 160; the result matches ta_sdpa_fwd within
  * fp32 rounding of the merge. */
 
-/* Chunk length (key steps) this library would use for `args` on its device: 0 when the
- * unsplit grid is as fast (large grids, configurations without a split kernel).  Computed
+/* Chunk length of the paired split, for causal grids of at most one workgroup per compute
+ * unit: query blocks p and nq - 1 - p (nq blocks a head) share two workgroups, the second
+ * block's key range cut so that each workgroup runs about (nq + 1) / 2 key steps (the
+ * whole-row grid's longest runs nq); the cut blocks are merged as above.  The grid keeps
+ * the whole-row size.  A non-causal call with it is exactly ta_sdpa_fwd. */
+#define TA_SPLIT_PAIRS (-1)
+
+/* Chunk length (key steps, or TA_SPLIT_PAIRS) this library would use for `args` on its
+ * device: 0 when the unsplit grid is as fast (large grids, configurations without a split
+ * kernel).  Computed
  * from a model of the dispatch of the grid over the device's compute units; cached per
  * (S, B*H, causal, CU count).  Reads only the shape, dtype, tile, accum and device fields
  * (tensor pointers and strides may be unset). */
 ta_status ta_split_plan(const ta_fwd_args* args, int32_t* chunk_steps);
 
 /* The model behind ta_split_plan for a device with `compute_units` CUs, without touching
- * a device: chunk length for a 128-row-tile fp32-accumulation forward of sequence length
- * S over n_bh (b, h) slices, 0 for no split or invalid sizes. */
+ * a device: chunk length (or TA_SPLIT_PAIRS) for a 128-row-tile fp32-accumulation forward
+ * of sequence length S over n_bh (b, h) slices, 0 for no split or invalid sizes. */
 int32_t ta_split_plan_model(int64_t S, int64_t n_bh, int32_t causal, int32_t compute_units);
 
 /* Device workspace (bytes, 256-byte aligned base required) that ta_sdpa_fwd_split needs

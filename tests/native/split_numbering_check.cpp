@@ -4,7 +4,9 @@
 // exactly once, partial slots must be unique, in range and used exactly by the blocks of
 // more than one chunk, and the merge grid must name exactly those blocks with their
 // chunks' slots in key order; the pair grid must cover every query block exactly once with
-// nq + 1 key steps an item.  Prints "ok <cases>" or the first failure.
+// nq + 1 key steps an item; the paired split must cover every key step once, within
+// (nq + f + 3) / 2 steps a workgroup, and merge exactly its cut blocks.  Prints
+// "ok <cases>" or the first failure.
 #include <algorithm>
 #include <cstdio>
 #include <map>
@@ -133,6 +135,74 @@ static void check_pairs(int S, int n_bh, int sched) {
   CHECK((int)seen.size() == n_bh * nq, "S=%d n_bh=%d pairs cover %zu of %d", S, n_bh, seen.size(), n_bh * nq);
 }
 
+// Paired split (psplit_items) with cut offset f: every key step of every causal (b, h,
+// query block) exactly once, a workgroup's items of one head, at most (nq + f + 3) / 2
+// steps a workgroup, slots unique and in range, two chunks (slots 2p and 2p + 1 of the
+// head, in key order) exactly for the blocks the merge grid names, one chunk and no slot
+// for every other block; the layout agrees (nq items, 2 P slots, P merges).
+static void check_psplit(int S, int n_bh, int sched, int f) {
+  const int nq = (S + ta::kPPRows - 1) / ta::kPPRows;
+  ta::SplitLayout l;
+  const bool split = ta::split_layout(S, true, ta::kSplitPairs, &l, f);
+  const int P = ta::psplit_cut_pairs(nq, f);
+  CHECK(split == (P > 0), "S=%d f=%d layout %d P %d", S, f, split, P);
+  ta::SplitLayout lnc;
+  CHECK(!ta::split_layout(S, false, ta::kSplitPairs, &lnc, f), "non-causal paired layout");
+  if (split) CHECK(l.items == nq && l.slots == 2 * P && l.merge == P, "S=%d layout", S);
+  std::map<std::pair<int, int>, std::vector<std::tuple<int, int, int>>> chunks;
+  std::set<int> slots;
+  for (int blk = 0; blk < n_bh * nq; ++blk) {
+    ta::WorkItem it[2];
+    ta::psplit_items(blk, n_bh, nq, sched, f, &it[0], &it[1]);
+    int steps = 0;
+    for (int i = 0; i < 2; ++i) {
+      const ta::WorkItem& w = it[i];
+      if (i == 1 && w.qt < 0) break;
+      CHECK(w.bh >= 0 && w.bh < n_bh && w.qt >= 0 && w.qt < nq, "S=%d blk %d bh %d qt %d", S, blk, w.bh, w.qt);
+      if (!(w.bh >= 0 && w.bh < n_bh && w.qt >= 0 && w.qt < nq)) return;
+      CHECK(w.bh == it[0].bh, "one head a workgroup");
+      CHECK(w.t_beg >= 0 && w.t_beg < w.t_end && w.t_end <= w.qt + 1, "S=%d blk %d [%d,%d) qt %d", S,
+            blk, w.t_beg, w.t_end, w.qt);
+      steps += w.t_end - w.t_beg;
+      if (w.slot >= 0) {
+        CHECK(w.slot < n_bh * 2 * P, "slot %d of %d", w.slot, n_bh * 2 * P);
+        CHECK(slots.insert(w.slot).second, "slot %d reused", w.slot);
+      }
+      chunks[{w.bh, w.qt}].emplace_back(w.t_beg, w.t_end, w.slot);
+    }
+    CHECK(2 * steps <= nq + f + 3, "S=%d f=%d blk %d: %d steps of nq %d", S, f, blk, steps, nq);
+  }
+  CHECK((int)chunks.size() == n_bh * nq, "S=%d blocks %zu of %d", S, chunks.size(), n_bh * nq);
+  std::map<std::pair<int, int>, std::vector<int>> cut;
+  for (auto& kv : chunks) {
+    auto v = kv.second;
+    std::sort(v.begin(), v.end());
+    int at = 0;
+    for (auto& t : v) {
+      CHECK(std::get<0>(t) == at, "S=%d bh %d qt %d gap at %d", S, kv.first.first, kv.first.second, at);
+      at = std::get<1>(t);
+    }
+    CHECK(at == kv.first.second + 1, "S=%d qt %d ends at %d", S, kv.first.second, at);
+    if (v.size() == 1) {
+      CHECK(std::get<2>(v[0]) == -1, "whole block with slot %d", std::get<2>(v[0]));
+    } else {
+      CHECK(v.size() == 2, "paired split block in %zu chunks", v.size());
+      cut[kv.first] = {std::get<2>(v[0]), std::get<2>(v[1])};
+    }
+  }
+  std::set<std::pair<int, int>> merged;
+  for (int blk = 0; blk < n_bh * P; ++blk) {
+    const ta::MergeItem m = ta::psplit_merge_item(blk, nq, f);
+    auto itc = cut.find({m.bh, m.qt});
+    CHECK(itc != cut.end(), "merge blk %d names uncut block (%d, %d)", blk, m.bh, m.qt);
+    if (itc == cut.end()) continue;
+    CHECK(m.ns == 2 && itc->second[0] == m.slot0 && itc->second[1] == m.slot0 + 1,
+          "merge slots %d vs %d %d", m.slot0, itc->second[0], itc->second[1]);
+    CHECK(merged.insert({m.bh, m.qt}).second, "block merged twice");
+  }
+  CHECK(merged.size() == cut.size(), "S=%d f=%d merged %zu of %zu", S, f, merged.size(), cut.size());
+}
+
 int main() {
   int cases = 0;
   const int seqs[] = {1, 100, 128, 129, 255, 256, 300, 1000, 1024, 2048, 2100, 4096, 8192, 16384};
@@ -157,6 +227,19 @@ int main() {
     for (int nq = 2; nq <= 70; ++nq) {
       check_pairs(nq * 128 - 5, n_bh, 1);
       ++cases;
+    }
+  for (int S : seqs)
+    for (int n_bh : bhs)
+      for (int sched = 0; sched < 3; ++sched)
+        for (int f = 0; f <= 8; ++f) {
+          check_psplit(S, n_bh, sched, f);
+          ++cases;
+        }
+  for (int n_bh = 1; n_bh <= 12; ++n_bh)
+    for (int nq = 1; nq <= 70; ++nq) {
+      check_psplit(nq * 128 - 5, n_bh, 1, 4);
+      check_psplit(nq * 128, n_bh, 1, 0);
+      cases += 2;
     }
   if (fails) {
     printf("%d failures\n", fails);

@@ -169,3 +169,51 @@ def test_cabi_split_with_caller_workspace(gpu):
         torch.cuda.synchronize()
         check_close(as_f32(o), oracle_f32(q, k, v, causal=bool(causal)), "bfloat16",
                     what=f"C-ABI split {shape}")
+
+
+@pytest.mark.parametrize("shape,dtype", [
+    ((1, 8, 4096, 128), "bfloat16"),   # C3 S=4096: 16 pairs a head, 13 of them cut
+    ((1, 2, 1000, 64), "float16"),     # ragged last block
+    ((1, 3, 1300, 160), "bfloat16"),   # odd nq: the middle block alone
+    ((2, 2, 2100, 96), "float16"),     # native D = 96, odd nq, ragged
+    ((1, 4, 1000, 144), "bfloat16"),   # in-kernel padding to 160
+    ((1, 1, 129, 128), "float16"),     # two blocks: no pair is cut, whole rows
+])
+def test_paired_split_matches_oracle(gpu, shape, dtype):
+    """TILEDATTN_SPLIT=pairs (TA_SPLIT_PAIRS): causal blocks p and nq - 1 - p over two
+    workgroups, the heavy block's key range cut between them and merged."""
+    s = shape[2]
+    q, k, v = inputs(shape, dtype, 500 + s)
+    rows = None if s <= 2100 else sample_rows(s, 128)
+    ref = oracle_f32(q, k, v, causal=True, rows=rows)
+    say(f"paired split {dtype} {shape} causal")
+    out = run_gpu(q, k, v, causal=True, split="pairs", accum_mode="fp32")
+    check_close(as_f32(out, rows), ref, dtype, what=f"paired split {shape}")
+
+
+def test_paired_split_outliers_and_whole_rows_agree(gpu):
+    """C5b's fp16 outlier keys at S=4096 (running maxima differ strongly between the two
+    chunks of a cut block): the paired split meets the oracle and stays within one fp16
+    rounding of the whole-row result; a non-causal call with pairs is the whole-row
+    launch."""
+    import torch
+
+    shape = (1, 8, 4096, 128)
+    q, k, v = inputs(shape, "float16", 1234, outlier_frac=0.01, outlier_gain=20.0, outlier_seed=1235)
+    rows = sample_rows(4096, 128)
+    ref = oracle_f32(q, k, v, causal=True, rows=rows)
+    say("paired split fp16 outliers (1,8,4096,128) causal")
+    paired = run_gpu(q, k, v, causal=True, split="pairs", accum_mode="fp32")
+    say("whole rows fp16 outliers (1,8,4096,128) causal")
+    whole = run_gpu(q, k, v, causal=True, split="off", tile_m=128, tile_n=64, accum_mode="fp32")
+    a, w = as_f32(paired, rows), as_f32(whole, rows)
+    check_close(a, ref, "float16", what="paired split outliers")
+    check_close(w, ref, "float16", what="whole rows outliers")
+    # one fp16 rounding step apart at most (2^-10 per unit of |o|, twice for the margin)
+    diff = np.abs(a - w)
+    assert float(diff.max()) <= 2.0 ** -9 * max(1.0, float(np.abs(w).max())), float(diff.max())
+    say("paired split bf16 (1,2,640,128) non-causal = whole rows")
+    q, k, v = inputs((1, 2, 640, 128), "bfloat16", 9)
+    p_nc = run_gpu(q, k, v, causal=False, split="pairs")
+    w_nc = run_gpu(q, k, v, causal=False, split="off", tile_m=128, tile_n=64)
+    assert torch.equal(p_nc, w_nc)

@@ -83,7 +83,7 @@ def test_workspace_size_edge_cases(lib):
     out = ctypes.c_int64(-1)
     assert lib.ta_split_workspace_size(ctypes.byref(_args(S=4096)), 0, ctypes.byref(out)) == _lib.TA_OK
     assert out.value == 0
-    assert lib.ta_split_workspace_size(ctypes.byref(_args(S=4096)), -1, ctypes.byref(out)) == _lib.TA_EINVAL
+    assert lib.ta_split_workspace_size(ctypes.byref(_args(S=4096)), -2, ctypes.byref(out)) == _lib.TA_EINVAL
     # a chunk as long as the longest row splits nothing
     assert lib.ta_split_workspace_size(ctypes.byref(_args(S=4096)), 32, ctypes.byref(out)) == _lib.TA_OK
     assert out.value == 0
@@ -116,6 +116,43 @@ def test_split_launch_rejects_bad_workspace_before_any_device_call(lib):
     assert st == _lib.TA_EUNSUPPORTED
 
 
+def _cut_pairs(nq: int, f: int = 4) -> int:
+    """Pairs the paired split cuts: p with (nq - 2p - 1 - f) // 2 > 0 (the library's cut
+    offset f is 4 key steps)."""
+    return sum(1 for p in range(nq // 2) if (nq - 2 * p - 1 - f) // 2 > 0)
+
+
+@pytest.mark.parametrize("S,D", [(4096, 128), (1000, 64), (1300, 160), (2100, 96), (8192, 128),
+                                 (129, 128), (900, 128)])
+def test_paired_split_workspace_is_two_partials_per_cut_pair(lib, S, D):
+    a = _args(S=S, B=2, H=3, D=D, causal=1)
+    out = ctypes.c_int64(-1)
+    assert lib.ta_split_workspace_size(ctypes.byref(a), _lib.TA_SPLIT_PAIRS, ctypes.byref(out)) == _lib.TA_OK
+    rows = 6 * 2 * _cut_pairs(math.ceil(S / 128)) * 128
+    assert out.value == ((rows * D * 4 + 255) // 256 * 256 + rows * 4 if rows else 0)
+    # S = 4096: 32 blocks, pairs p = 0 .. 12 cut (k_p = 13 .. 1 steps)
+    if S == 4096:
+        assert rows == 6 * 2 * 13 * 128
+    # non-causal: the paired split is the whole-row grid (no workspace)
+    a.causal = 0
+    assert lib.ta_split_workspace_size(ctypes.byref(a), _lib.TA_SPLIT_PAIRS, ctypes.byref(out)) == _lib.TA_OK
+    assert out.value == 0
+
+
+def test_split_knob_pairs(monkeypatch, lib):
+    a = _args(S=4096)
+    monkeypatch.setenv("TILEDATTN_SPLIT", "pairs")
+    assert flash_fwd._resolve_split(lib, a, capable=True) == _lib.TA_SPLIT_PAIRS
+    with pytest.raises(ValueError, match="TILEDATTN_SPLIT needs"):
+        flash_fwd._resolve_split(lib, a, capable=False)
+    monkeypatch.setenv("TILEDATTN_SPLIT", "pair")
+    with pytest.raises(ValueError, match="'pairs'"):
+        flash_fwd._resolve_split(lib, a, capable=True)
+    assert _lib.kernel_symbol(dtype=_lib.TA_BF16, head_dim=128, tile_m=128, tile_n=64, causal=True,
+                              tail=False, accum=_lib.TA_ACC_FP32, split=True, pair=True) == (
+        "attn_fwd_pp.hsaco", "ta_fwd_pp_psplit_bf16_d128_c1_t0")
+
+
 def _plan(lib, S, n_bh, causal, cus=MI355X_CUS):
     return lib.ta_split_plan_model(S, n_bh, causal, cus)
 
@@ -132,8 +169,19 @@ def test_plan_model_splits_small_grids_and_leaves_large_ones(lib):
         a = _args(S=S, B=1, H=n_bh, causal=causal)
         assert lib.ta_split_workspace_size(ctypes.byref(a), c, ctypes.byref(out)) == _lib.TA_OK
         assert out.value > 0  # the chosen chunk splits something
-    for S in (1024, 2048, 4096, 8192, 16384):
+    for S in (1024, 2048, 8192, 16384):
         assert _plan(lib, S, 8, 1) == 0, S
+    # causal grids of more than half and at most one 128-row block per CU, 32 blocks a head
+    # or more: the paired split (B1 H8 S4096 45.0 -> 44.0 us, fp16 D = 64 33.0 -> 30.2; B1
+    # H4 S8192 70.8 with the best chunk, 70.6 paired)
+    for S, n_bh in ((4096, 8), (8192, 4), (4096, 6), (8000, 4), (16384, 2)):
+        assert _plan(lib, S, n_bh, 1) == _lib.TA_SPLIT_PAIRS, (S, n_bh)
+    # shorter rows: the whole-row grid (B1 H16 S2048 24.5 us, 28.5 paired)
+    assert _plan(lib, 2048, 16, 1) == 0
+    for S, n_bh in ((4096, 8), (8192, 4)):
+        assert _plan(lib, S, n_bh, 0) == 0, (S, n_bh)  # non-causal rows are all equal
+    # half a wave or less: chunks (B1 H2 S8192 47.2 us against 51.0 paired)
+    assert _plan(lib, 8192, 2, 1) > 0 and _plan(lib, 4096, 4, 1) != _lib.TA_SPLIT_PAIRS
     # grids of many waves balance by themselves
     assert _plan(lib, 4096, 64, 1) == 0
     assert _plan(lib, 4096, 64, 0) == 0
@@ -162,7 +210,7 @@ def test_split_knob(monkeypatch, raw, capable, expect):
 
 
 @pytest.mark.parametrize("raw,capable,msg", [
-    ("-1", True, ">= 0"), ("x", True, "'auto', 'off' or an integer"), ("1.5", True, "integer"),
+    ("-1", True, ">= 0"), ("x", True, "'auto', 'off', 'pairs' or an integer"), ("1.5", True, "integer"),
     ("4", False, "tile (128, 64)"),
 ])
 def test_split_knob_rejects(monkeypatch, raw, capable, msg):

@@ -17,7 +17,7 @@ from threading import Lock
 
 from ._errors import DependencyError
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 TA_OK = 0
 TA_EINVAL = 1
@@ -29,6 +29,7 @@ TA_FP16 = 0
 TA_BF16 = 1
 TA_ACC_FP32 = 0
 TA_ACC_INPUT = 1
+TA_SPLIT_PAIRS = -1  # chunk length of the paired split
 
 TILE_SHAPES = ((64, 64), (64, 128), (128, 64), (128, 128))
 STATIC_SCRATCH_BYTES = 64 << 20  # TA_STATIC_SCRATCH_BYTES
@@ -74,12 +75,12 @@ def kernel_symbol(*, dtype: int, head_dim: int, tile_m: int, tile_n: int, causal
     """(code object file, kernel symbol) the C ABI launches for a configuration; the same
     rule as kernel_id() in csrc/tiledattn.cpp (used to label measurements).  ``split``
     names the split-key-range kernel (its merge kernel is ta_fwd_merge_<dt>_d<D>_c<c>),
-    ``pair`` the causal pair kernel (``uses_pairs``).  ``tail`` is the variant the C ABI
-    picks (``tail_masked``)."""
+    ``pair`` the causal pair kernel (``uses_pairs``); both together the paired-split
+    kernel.  ``tail`` is the variant the C ABI picks (``tail_masked``)."""
     dt = "bf16" if dtype == TA_BF16 else "f16"
     c, t = int(bool(causal)), int(bool(tail))
     if tile_m == 128 and tile_n in (64, 128) and accum == TA_ACC_FP32 and head_dim <= 160:
-        kind = "pp_split" if split else ("pp_pair" if pair else "pp")
+        kind = ("pp_psplit" if pair else "pp_split") if split else ("pp_pair" if pair else "pp")
         return "attn_fwd_pp.hsaco", f"ta_fwd_{kind}_{dt}_d{head_dim}_c{c}_t{t}"
     if (eight_wave_family(tile_m=tile_m, tile_n=tile_n, accum=accum, head_dim=head_dim)
             and not split and not pair):

@@ -45,9 +45,11 @@ Environment knobs are re-read on every call, as in the reference:
 ``TILEDATTN_SPLIT`` (this build only)
     Split key ranges (``ta_sdpa_fwd_split``): ``auto`` (default) asks the library's
     dispatch model (``ta_split_plan``), ``0``/``off`` never splits, a positive integer
-    forces chunks of that many 128-key steps.  Splitting exists for tiles (128, 64) and
-    (128, 128) with fp32 accumulation and kernel head dims up to 160; forcing it elsewhere
-    raises ``ValueError``.
+    forces chunks of that many 128-key steps, ``pairs`` the paired split
+    (``TA_SPLIT_PAIRS``: causal blocks p and nq - 1 - p balanced over two workgroups;
+    non-causal calls run whole rows).  Splitting exists for tiles (128, 64) and (128, 128)
+    with fp32 accumulation and kernel head dims up to 160; forcing it elsewhere raises
+    ``ValueError``.
 """
 
 from __future__ import annotations
@@ -343,7 +345,8 @@ def _split_capable(*, tile_m: int, tile_n: int, accum_code: int, kernel_head_dim
 
 
 def _resolve_split(lib, args: _lib.FwdArgs, *, capable: bool) -> int:
-    """``TILEDATTN_SPLIT`` -> chunk length in 128-key steps (0 = whole rows)."""
+    """``TILEDATTN_SPLIT`` -> chunk length in 128-key steps (0 = whole rows,
+    ``_lib.TA_SPLIT_PAIRS`` = the paired split)."""
     raw = os.getenv("TILEDATTN_SPLIT", "").strip().lower()
     if raw in ("", "auto"):
         if not capable:
@@ -357,10 +360,18 @@ def _resolve_split(lib, args: _lib.FwdArgs, *, capable: bool) -> int:
         return chunk
     if raw in ("0", "off"):
         return 0
+    if raw == "pairs":
+        if not capable:
+            raise ValueError(
+                "TILEDATTN_SPLIT needs tile (128, 64) or (128, 128), fp32 accumulation and a head "
+                "dim of at most 160."
+            )
+        return _lib.TA_SPLIT_PAIRS
     try:
         chunk = int(raw)
     except ValueError as exc:
-        raise ValueError(f"TILEDATTN_SPLIT must be 'auto', 'off' or an integer, got {raw!r}.") from exc
+        raise ValueError(
+            f"TILEDATTN_SPLIT must be 'auto', 'off', 'pairs' or an integer, got {raw!r}.") from exc
     if chunk < 0:
         raise ValueError(f"TILEDATTN_SPLIT must be >= 0, got {chunk}.")
     if chunk and not capable:
@@ -389,7 +400,7 @@ def _split_preferred(lib, q, batch: int, heads: int, seq_len: int, head_dim: int
     args.tile_m, args.tile_n = 128, 64
     args.accum = _lib.TA_ACC_FP32
     args.device = q.device.index if q.device.index is not None else torch_mod.cuda.current_device()
-    return _resolve_split(lib, args, capable=True) > 0
+    return _resolve_split(lib, args, capable=True) != 0
 
 
 def _raise_for_status(lib, status: int) -> None:

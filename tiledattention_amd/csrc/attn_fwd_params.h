@@ -23,9 +23,10 @@ struct FwdParams {
   // Split key ranges (split kernels and the merge kernel only; see SplitLayout).
   float* part_o;       // [slots][128][D] fp32 partial outputs, each normalised by its own l
   float* part_lse;     // [slots][128] log2 of the partial's softmax denominator, m*c + log2(l)
-  int32_t split_c;     // key steps (of 128 keys) per chunk
+  int32_t split_c;     // key steps (of 128 keys) per chunk, or kSplitPairs (paired split)
   int32_t split_items; // work items per (b, h)
-  int32_t split_ns;    // chunks per query block (non-causal; causal derives it per block)
+  int32_t split_ns;    // chunks per query block (non-causal; causal derives it per block);
+                       // the cut offset f of the paired split
   int32_t split_slots; // partial slots per (b, h)
   int32_t d_real;      // head-dim columns present in q/k/v/o (eight-wave kernel; <= D,
                        // multiple of 8): columns d_real..D-1 read as zero, are not written

@@ -1023,7 +1023,9 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
 // A workgroup's work: one query block of the whole-row grid, one chunk of the split grid,
 // or (PAIR) the causal pair of query blocks nq - 1 - j and j of one head, one after the
 // other, so that every pair has nq + 1 key steps (balanced without relying on the order in
-// which the hardware hands out workgroups) and the grid is half as many workgroups.
+// which the hardware hands out workgroups) and the grid is half as many workgroups; with
+// SPLIT as well, the paired split (psplit_items): a light block whole and then the first
+// chunk of its partner, or the partner's remaining steps.
 // One workgroup per CU (LDS and registers).  The numbering (attn_fwd_split.h) regroups
 // block ids per XCD with sched >= 1 (one head's K/V in one L2) and issues causal tiles
 // heaviest first, so each CU takes the next tile when its current one ends and heavy
@@ -1040,9 +1042,12 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   __shared__ __attribute__((aligned(1024))) char lds_v0[STAGE];
   __shared__ __attribute__((aligned(1024))) char lds_v1[STAGE];
   if constexpr (PAIR) {
-    static_assert(CAUSAL && !SPLIT, "pairs of causal query blocks");
+    static_assert(CAUSAL, "pairs of causal query blocks");
     WorkItem a, b;
-    pair_items(blockIdx.x, p.n_bh, p.n_qblk, p.sched, &a, &b);
+    if constexpr (SPLIT)
+      psplit_items(blockIdx.x, p.n_bh, p.n_qblk, p.sched, p.split_ns, &a, &b);
+    else
+      pair_items(blockIdx.x, p.n_bh, p.n_qblk, p.sched, &a, &b);
     attn_fwd_pp_block<DT, D, CAUSAL, TAIL, SPLIT>(p, a, lds_k0, lds_k1, lds_v0, lds_v1);
     if (b.qt >= 0) {
       // Every wave is past its last LDS access of the first block before the second
@@ -1076,7 +1081,9 @@ __device__ __forceinline__ void attn_merge_body(const FwdParams& p) {
   static_assert(merge_threads(D) <= 256 && TM % RPW == 0, "workgroups must cover whole rows");
   using DTy = DType<DT>;
   const int blk = blockIdx.x / WPB;
-  const MergeItem mi = merge_item(blk, p.n_qblk, CAUSAL, p.split_c, p.split_ns, p.split_slots);
+  const MergeItem mi = CAUSAL && p.split_c == kSplitPairs
+                           ? psplit_merge_item(blk, p.n_qblk, p.split_ns)
+                           : merge_item(blk, p.n_qblk, CAUSAL, p.split_c, p.split_ns, p.split_slots);
   const int row = (blockIdx.x - blk * WPB) * RPW + threadIdx.x / CH;
   const int c8 = threadIdx.x % CH;
   const int q = mi.qt * TM + row;
@@ -1137,6 +1144,15 @@ __device__ __forceinline__ void attn_merge_body(const FwdParams& p) {
       __attribute__((amdgpu_waves_per_eu(2, 2)))                                          \
       ta_fwd_pp_pair_##DTN##_d##D##_c1_t##T(ta::FwdParams p) {                             \
     ta::attn_fwd_pp_body<DT, D, true, (T != 0), false, true>(p);                          \
+  }
+
+// Paired split (causal, D = 64, 96, 128 and 160): ta_fwd_pp_psplit_<f16|bf16>_d<D>_c1_t<0|1>,
+// merged by ta_fwd_merge_<...>_c1.
+#define TA_PP_PSPLIT_DEFINE(DTN, DT, D, T)                                                 \
+  extern "C" __global__ void __launch_bounds__(512)                                       \
+      __attribute__((amdgpu_waves_per_eu(2, 2)))                                          \
+      ta_fwd_pp_psplit_##DTN##_d##D##_c1_t##T(ta::FwdParams p) {                           \
+    ta::attn_fwd_pp_body<DT, D, true, (T != 0), true, true>(p);                           \
   }
 
 // 64-row blocks (tiles (64, 64) and (64, 128) with fp32 accumulation, D = 64, 96 and 128):
@@ -1211,6 +1227,22 @@ TA_PP_PAIR_DEFINE(bf16, 1, 96, 0)
 TA_PP_PAIR_DEFINE(bf16, 1, 96, 1)
 TA_PP_PAIR_DEFINE(bf16, 1, 128, 0)
 TA_PP_PAIR_DEFINE(bf16, 1, 128, 1)
+TA_PP_PSPLIT_DEFINE(f16, 0, 64, 0)
+TA_PP_PSPLIT_DEFINE(f16, 0, 64, 1)
+TA_PP_PSPLIT_DEFINE(f16, 0, 96, 0)
+TA_PP_PSPLIT_DEFINE(f16, 0, 96, 1)
+TA_PP_PSPLIT_DEFINE(f16, 0, 128, 0)
+TA_PP_PSPLIT_DEFINE(f16, 0, 128, 1)
+TA_PP_PSPLIT_DEFINE(f16, 0, 160, 0)
+TA_PP_PSPLIT_DEFINE(f16, 0, 160, 1)
+TA_PP_PSPLIT_DEFINE(bf16, 1, 64, 0)
+TA_PP_PSPLIT_DEFINE(bf16, 1, 64, 1)
+TA_PP_PSPLIT_DEFINE(bf16, 1, 96, 0)
+TA_PP_PSPLIT_DEFINE(bf16, 1, 96, 1)
+TA_PP_PSPLIT_DEFINE(bf16, 1, 128, 0)
+TA_PP_PSPLIT_DEFINE(bf16, 1, 128, 1)
+TA_PP_PSPLIT_DEFINE(bf16, 1, 160, 0)
+TA_PP_PSPLIT_DEFINE(bf16, 1, 160, 1)
 TA_PP64_DEFINE_CT(f16, 0, 64)
 TA_PP64_DEFINE_CT(f16, 0, 96)
 TA_PP64_DEFINE_CT(f16, 0, 128)

@@ -17,6 +17,22 @@ namespace ta {
 constexpr int kPPRows = 128;  // query rows per block
 constexpr int kPPKeys = 128;  // keys per step
 
+// Chunk length that selects the paired split (psplit_items below).
+constexpr int kSplitPairs = -1;
+
+TA_HD inline int psplit_cut(int nq, int p, int f) {
+  const int x = nq - 2 * p - 1 - f;
+  return x >= 2 ? x / 2 : 0;
+}
+
+// Pairs with a cut (k_p > 0), the pairs 0 .. P - 1.
+TA_HD inline int psplit_cut_pairs(int nq, int f) {
+  const int x = nq - 3 - f;
+  if (x < 0) return 0;
+  const int P = x / 2 + 1;
+  return P < (nq >> 1) ? P : (nq >> 1);
+}
+
 // Merge kernel workgroup: one thread per (row, 16-byte output chunk), the largest power of
 // two of rows whose D / 8 threads each fit 256 (32 rows at D = 64, 16 at D = 128, 8 at
 // D = 160 with 160 threads), so a workgroup covers whole rows and a block whole workgroups.
@@ -42,10 +58,22 @@ TA_HD inline int64_t split_causal_items(int64_t x, int64_t c) {
   return c * a * (a + 1) / 2 + b * (a + 1);
 }
 
-// False when chunks of c steps split nothing (every block fits in one chunk).
-TA_HD inline bool split_layout(int64_t S, bool causal, int64_t c, SplitLayout* out) {
+// False when chunks of c steps split nothing (every block fits in one chunk).  c =
+// kSplitPairs is the paired split (below; causal only) with cut offset f: items = nq
+// workgroups, slots = 2 P, merge = P for the P pairs it cuts.
+TA_HD inline bool split_layout(int64_t S, bool causal, int64_t c, SplitLayout* out, int f = 0) {
   const int64_t nq = (S + kPPRows - 1) / kPPRows;
   const int64_t len = (S + kPPKeys - 1) / kPPKeys;
+  if (c == kSplitPairs) {
+    if (!causal || nq > 0x7fffffffLL) return false;
+    const int P = psplit_cut_pairs((int)nq, f);
+    if (P == 0) return false;
+    out->items = nq;
+    out->ns = 0;
+    out->slots = 2 * (int64_t)P;
+    out->merge = P;
+    return true;
+  }
   if (c < 1) return false;
   if (causal) {
     if (nq <= c) return false;
@@ -185,12 +213,83 @@ TA_HD inline WorkItem split_item(int blk, int n_bh, int items, int sched, bool c
   return w;
 }
 
+// Paired split (chunk length kSplitPairs, causal only): the whole-row grid's nq workgroups
+// per (b, h), with the work balanced.  Query blocks p (p + 1 key steps) and nq - 1 - p
+// (nq - p steps) share workgroups 2p and 2p + 1: workgroup 2p runs block p whole and then
+// the first k_p steps of block nq - 1 - p, workgroup 2p + 1 the remaining steps of block
+// nq - 1 - p, so each takes about (nq + 1) / 2 steps where the whole-row grid's heaviest
+// workgroup takes nq.  k_p = (nq - 2p - 1 - f) / 2 when positive (f: the fixed cost of a
+// workgroup's second block, in key steps, given to the workgroup with one block), else
+// the pair is not cut.  A cut block leaves its two chunks in slots 2p and 2p + 1 of its
+// head (2 P slots a head for the P pairs that are cut); the middle block of an odd nq is
+// one workgroup of its own.
+//
+// Workgroup blk of the paired-split grid (nq per (b, h); sched >= 1 with 8 | total maps
+// block ids per XCD as xcd_order describes): its first item `a` and, on the light block's
+// workgroup of a cut pair, the heavy block's first chunk `b` (b->qt = -1 otherwise).
+// Every item carries its step range; slot -1 marks a whole block.
+TA_HD inline void psplit_items(int blk, int n_bh, int nq, int sched, int f, WorkItem* a,
+                               WorkItem* b) {
+  int bh, r;
+  if (sched >= 1 && ((nq * n_bh) & 7) == 0) {
+    xcd_order(blk, n_bh, nq, &bh, &r);
+  } else {
+    bh = blk / nq;
+    r = blk - bh * nq;
+  }
+  const int P = psplit_cut_pairs(nq, f);
+  a->bh = b->bh = bh;
+  b->qt = -1;
+  b->t_beg = b->t_end = 0;
+  b->slot = -1;
+  a->slot = -1;
+  const int np = nq >> 1;
+  if (r >= 2 * np) {  // the middle block of an odd nq
+    a->qt = np;
+    a->t_beg = 0;
+    a->t_end = np + 1;
+    return;
+  }
+  const int pr = r >> 1;
+  const int heavy = nq - 1 - pr;
+  const int k = psplit_cut(nq, pr, f);
+  if (r & 1) {
+    a->qt = heavy;
+    a->t_beg = k;
+    a->t_end = heavy + 1;
+    if (k > 0) a->slot = bh * 2 * P + 2 * pr + 1;
+  } else {
+    a->qt = pr;
+    a->t_beg = 0;
+    a->t_end = pr + 1;
+    if (k > 0) {
+      b->qt = heavy;
+      b->t_beg = 0;
+      b->t_end = k;
+      b->slot = bh * 2 * P + 2 * pr;
+    }
+  }
+}
+
 struct MergeItem {
   int bh;
   int qt;
   int ns;     // chunks
   int slot0;  // slot of chunk 0; chunk i is in slot0 + i
 };
+
+// Merge grid of the paired split: one block per (b, h, cut pair p), the heavy block
+// nq - 1 - p with its two chunks in slots 2p and 2p + 1 of the head.
+TA_HD inline MergeItem psplit_merge_item(int blk, int nq, int f) {
+  const int P = psplit_cut_pairs(nq, f);
+  MergeItem m;
+  m.bh = blk / P;
+  const int pr = blk - m.bh * P;
+  m.qt = nq - 1 - pr;
+  m.ns = 2;
+  m.slot0 = m.bh * 2 * P + 2 * pr;
+  return m;
+}
 
 // Merge grid: one block per (b, h, split query block): causal blocks qt >= C, or every
 // non-causal block.

@@ -260,6 +260,16 @@ using ta::SplitLayout;
 using ta::split_layout;
 constexpr int kSplitRows = ta::kPPRows;
 
+// Cut offset f of the paired split (attn_fwd_split.h psplit_items): the fixed cost of a
+// workgroup's second block, in key steps, moved to the workgroup that runs one block.
+constexpr int kPairCut = 4;
+static_assert(TA_SPLIT_PAIRS == ta::kSplitPairs, "header and numbering agree");
+
+// Layout of chunk length c (kSplitPairs: the paired split with offset kPairCut).
+bool layout_for(int64_t S, bool causal, int64_t c, SplitLayout* l) {
+  return split_layout(S, causal, c, l, kPairCut);
+}
+
 // Workspace: fp32 partial outputs [slots][128][D], then the log-sum-exps [slots][128].
 int64_t split_ws_bytes(int64_t n_bh, int64_t d, const SplitLayout& l) {
   const int64_t rows = n_bh * l.slots * kSplitRows;
@@ -281,7 +291,7 @@ double simulate_split(int64_t S, int64_t n_bh, bool causal, int64_t c, int ncu) 
   const int nq = (int)((S + ta::kPPRows - 1) / ta::kPPRows);
   const int len = (int)((S + ta::kPPKeys - 1) / ta::kPPKeys);
   SplitLayout l;
-  const bool split = split_layout(S, causal, c, &l);
+  const bool split = c > 0 && layout_for(S, causal, c, &l);
   const int64_t total = split ? n_bh * l.items : n_bh * nq;
   const int xcds = 8;
   const int per_xcd = std::max(1, ncu / xcds);
@@ -329,17 +339,29 @@ ta_status cu_count_locked(int device, int* out) {
 
 // Chunk length (key steps) with the earliest simulated finish, or 0 when no split beats
 // the whole-row grid by 20 % (the model's error on the fitted timings stays below that).
-// Grids of several waves of workgroups balance by themselves and are not split.
+// Grids of several waves of workgroups balance by themselves and are not split.  Causal
+// grids of more than half and at most one workgroup per CU, with 32 or more query blocks
+// a head, take the paired split instead, the fastest of the three there on the MI355X
+// (per call, bf16 unless noted, B1 H8 S4096: D = 128 45.0 us whole rows / 45.1 best
+// chunk / 44.0 paired, fp16 D = 64 33.0 / 33.0 / 30.2, D = 96 38.0 / 38.0 / 36.5, D = 160
+// 55.0 / 54.8 / 51.7; B1 H4 S8192 84.3 / 70.8 / 70.6).  With fewer workgroups chunks win
+// (B1 H2 S8192 47.2 against 51.0 paired, B1 H4 S4096 30.9 against 33.9), and with
+// shorter rows the second block's fixed cost outweighs the balance (B1 H16 S2048 24.5
+// whole rows, 28.5 paired).
 int32_t plan_split(int64_t S, int64_t n_bh, bool causal, int ncu) {
   const int64_t nq = (S + kSplitRows - 1) / kSplitRows;
   const int64_t len = (S + ta::kPPKeys - 1) / ta::kPPKeys;
   if (ncu < 8 || n_bh * nq > 4 * (int64_t)ncu) return 0;
+  if (causal && nq >= 32 && 2 * n_bh * nq > (int64_t)ncu && n_bh * nq <= (int64_t)ncu) {
+    SplitLayout l;
+    if (layout_for(S, causal, ta::kSplitPairs, &l)) return ta::kSplitPairs;
+  }
   const double base = simulate_split(S, n_bh, causal, 0, ncu);
   double best = base * 0.8;
   int32_t best_c = 0;
   for (int64_t c = 1; c < len; ++c) {
     SplitLayout l;
-    if (!split_layout(S, causal, c, &l)) continue;
+    if (!layout_for(S, causal, c, &l)) continue;
     if (l.items * n_bh > 8 * (int64_t)ncu) continue;  // more items than waves help
     const double t = simulate_split(S, n_bh, causal, c, ncu);
     if (t < best) {
@@ -606,25 +628,25 @@ int32_t ta_split_plan_model(int64_t S, int64_t n_bh, int32_t causal, int32_t com
 ta_status ta_split_workspace_size(const ta_fwd_args* a, int32_t chunk_steps, int64_t* bytes) {
   if (bytes == nullptr) return fail(TA_EINVAL, "bytes is NULL");
   *bytes = 0;
-  if (chunk_steps < 0) return fail(TA_EINVAL, "chunk_steps %d", chunk_steps);
+  if (chunk_steps < 0 && chunk_steps != TA_SPLIT_PAIRS) return fail(TA_EINVAL, "chunk_steps %d", chunk_steps);
   int64_t n_bh = 0, n_qblk = 0;
   ta_status vst = validate_args(a, &n_bh, &n_qblk, false);
   if (vst != TA_OK || n_qblk == 0 || chunk_steps == 0) return vst;
   if (!split_capable(a))
     return fail(TA_EUNSUPPORTED, "split key ranges need tile (128, 64) or (128, 128), fp32 accumulation, D <= 160");
   SplitLayout l;
-  if (split_layout(a->S, a->causal != 0, chunk_steps, &l)) *bytes = split_ws_bytes(n_bh, a->D, l);
+  if (layout_for(a->S, a->causal != 0, chunk_steps, &l)) *bytes = split_ws_bytes(n_bh, a->D, l);
   return TA_OK;
 }
 
 ta_status ta_sdpa_fwd_split(const ta_fwd_args* a, int32_t chunk_steps, void* workspace,
                             int64_t workspace_bytes, void* stream) {
-  if (chunk_steps < 0) return fail(TA_EINVAL, "chunk_steps %d", chunk_steps);
+  if (chunk_steps < 0 && chunk_steps != TA_SPLIT_PAIRS) return fail(TA_EINVAL, "chunk_steps %d", chunk_steps);
   int64_t n_bh = 0, n_qblk = 0;
   ta_status vst = validate_args(a, &n_bh, &n_qblk);
   if (vst != TA_OK || n_qblk == 0) return vst;
   SplitLayout l;
-  if (chunk_steps == 0 || !split_layout(a->S, a->causal != 0, chunk_steps, &l))
+  if (chunk_steps == 0 || !layout_for(a->S, a->causal != 0, chunk_steps, &l))
     return ta_sdpa_fwd(a, stream);
   if (!split_capable(a))
     return fail(TA_EUNSUPPORTED, "split key ranges need tile (128, 64) or (128, 128), fp32 accumulation, D <= 160");
@@ -648,8 +670,9 @@ ta_status ta_sdpa_fwd_split(const ta_fwd_args* a, int32_t chunk_steps, void* wor
   const bool aligned = unmasked_tail(a);
   const char* dt = a->dtype == TA_BF16 ? "bf16" : "f16";
   char name[96];
-  snprintf(name, sizeof(name), "ta_fwd_pp_split_%s_d%d_c%d_t%d", dt, (int)a->D, a->causal ? 1 : 0,
-           aligned ? 0 : 1);
+  const bool paired = chunk_steps == TA_SPLIT_PAIRS;
+  snprintf(name, sizeof(name), "ta_fwd_pp_%s_%s_d%d_c%d_t%d", paired ? "psplit" : "split", dt,
+           (int)a->D, a->causal ? 1 : 0, aligned ? 0 : 1);
   const KernelId sid{"attn_fwd_pp.hsaco", name, 512u};
   snprintf(name, sizeof(name), "ta_fwd_merge_%s_d%d_c%d", dt, (int)a->D, a->causal ? 1 : 0);
   const KernelId mid{"attn_fwd_pp.hsaco", name, 256u};
@@ -661,7 +684,7 @@ ta_status ta_sdpa_fwd_split(const ta_fwd_args* a, int32_t chunk_steps, void* wor
                                         (rows * a->D * 4 + 255) / 256 * 256);
   p.split_c = chunk_steps;
   p.split_items = static_cast<int32_t>(l.items);
-  p.split_ns = static_cast<int32_t>(l.ns);
+  p.split_ns = paired ? kPairCut : static_cast<int32_t>(l.ns);
   p.split_slots = static_cast<int32_t>(l.slots);
 
   // Resolve and launch under the cache lock, as ta_sdpa_fwd does.
