@@ -445,13 +445,24 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
       const bool moved = __ballot(!(alpha == 1.0f)) != 0;
       const float al = DTy::round(alpha);
       const bool round_now = kLowpSteps == 1 || (kLowpSteps == 2 ? PAR == 1 : (PAR == 1 && (t & 2)));
-      if (round_now) {
+      // `moved` is uniform: one branch per case (as a per-element select the compiler
+      // formed both packs, the products and a select for every value on every step).
+      if (round_now && moved) {
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
 #pragma unroll
           for (int r = 0; r < 16; r += 2) {
-            const uint32_t w = moved ? DTy::pack(o_acc[db][r] * al, o_acc[db][r + 1] * al)
-                                     : DTy::pack(o_acc[db][r], o_acc[db][r + 1]);
+            const uint32_t w = DTy::pack(o_acc[db][r] * al, o_acc[db][r + 1] * al);
+            o_acc[db][r] = DTy::lo(w);
+            o_acc[db][r + 1] = DTy::hi(w);
+          }
+        }
+      } else if (round_now) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+#pragma unroll
+          for (int r = 0; r < 16; r += 2) {
+            const uint32_t w = DTy::pack(o_acc[db][r], o_acc[db][r + 1]);
             o_acc[db][r] = DTy::lo(w);
             o_acc[db][r + 1] = DTy::hi(w);
           }
