@@ -148,7 +148,7 @@ def test_cabi_split_with_caller_workspace(gpu):
     ws = torch.full((64 << 20,), 0x7f, dtype=torch.uint8, device=dev)  # NaN-ish bytes
     stream = torch.cuda.current_stream(dev).cuda_stream
     for shape, causal, chunk in (((1, 4, 1536, 128), 1, 2), ((1, 2, 700, 64), 0, 1),
-                                 ((1, 2, 700, 160), 1, 2)):
+                                 ((1, 2, 700, 160), 1, 2), ((1, 2, 2100, 96), 1, _lib.TA_SPLIT_PAIRS)):
         q, k, v = inputs(shape, "bfloat16", 11 + shape[2])
         qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
         o = torch.empty_like(qd)

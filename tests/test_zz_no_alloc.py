@@ -2,8 +2,8 @@
 
 It must give exactly what ta_sdpa_fwd_split gives with a caller-owned workspace (the same
 kernels; only the workspace's address differs), on two calls in a row whose second is
-smaller (the static array keeps the first call's partials), and meet the north-star bound
-against the fp32 oracle.  Torch only allocates the tensors and provides the stream."""
+smaller (the static array keeps the first call's partials), for chunk lengths and the
+paired split, and meet the north-star bound against the fp32 oracle.  Torch only allocates the tensors and provides the stream."""
 
 from __future__ import annotations
 
@@ -37,7 +37,9 @@ def test_static_scratch_matches_caller_workspace(gpu, order):
     stream = torch.cuda.current_stream(dev).cuda_stream
     big = ((1, 4, 2048, 128), 1, "bfloat16", 3)
     small = ((1, 2, 700, 64), 0, "float16", 1)
-    cases = [big, small] if order == "large_then_small" else [small, big, small]
+    # the paired split (11 blocks a head, 3 pairs cut, the middle block alone)
+    pairs = ((1, 3, 1300, 128), 1, "bfloat16", _lib.TA_SPLIT_PAIRS)
+    cases = [big, pairs, small] if order == "large_then_small" else [small, big, pairs, small]
     for shape, causal, dtype, chunk in cases:
         dc = _lib.TA_BF16 if dtype == "bfloat16" else _lib.TA_FP16
         q, k, v = inputs(shape, dtype, 90 + shape[2])
