@@ -222,3 +222,20 @@ def test_paired_split_outliers_and_whole_rows_agree(gpu):
     p_nc = run_gpu(q, k, v, causal=False, split="pairs")
     w_nc = run_gpu(q, k, v, causal=False, split="off", tile_m=128, tile_n=64)
     assert torch.equal(p_nc, w_nc)
+
+
+def test_automatic_plan_runs_the_paired_split(gpu):
+    """B1 H6 S4096 bf16 causal: 192 query blocks of 128 rows for 256 CUs, 32 a head, so the
+    library's plan (TILEDATTN_SPLIT unset) is the paired split; sampled rows meet the oracle."""
+    from tiledattention import _lib
+    from tiledattention.kernels import flash_fwd
+
+    shape = (1, 6, 4096, 128)
+    q, k, v = inputs(shape, "bfloat16", 4096)
+    rows = sample_rows(4096, 96)
+    ref = oracle_f32(q, k, v, causal=True, rows=rows)
+    say("automatic plan bf16 (1,6,4096,128) causal")
+    out = run_gpu(q, k, v, causal=True, split=None)
+    assert any(key[0] == 4096 and key[1] == 6 and key[2] == 1 and c == _lib.TA_SPLIT_PAIRS
+               for key, c in flash_fwd._SPLIT_PLANS.items()), flash_fwd._SPLIT_PLANS
+    check_close(as_f32(out, rows), ref, "bfloat16", what="automatic paired split")
