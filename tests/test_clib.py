@@ -106,7 +106,7 @@ def _call(lib, a):
     (dict(d_real=-8), _lib.TA_EINVAL, "d_real"),
     (dict(d_real=36, D=128, tile_m=128), _lib.TA_EINVAL, "multiple of 8"),
     (dict(d_real=136, D=160, accum=1, tile_m=128), _lib.TA_EUNSUPPORTED, "d_real needs"),
-    (dict(d_real=136, D=160), _lib.TA_EUNSUPPORTED, "d_real needs"),  # 64-row tiles: D <= 128
+    (dict(d_real=200, D=256), _lib.TA_EUNSUPPORTED, "d_real needs"),  # 64-row tiles: D <= 160
     (dict(d_real=200, D=256, tile_m=128), _lib.TA_EUNSUPPORTED, "D <= 160"),
 ])
 def test_argument_validation(lib, kw, status, msg):

@@ -235,9 +235,10 @@ def test_wide_head_dims(gpu, dtype, d, tiles):
     (136, "float16", True, 3000),
 ])
 def test_eight_wave_d160(gpu, d, dtype, causal, s):
-    """Kernel head dim 160 on the eight-wave kernel (default tile (128, 64)): stages split
-    into a 128-column part and a 32-column tail part; head dims 129-159 run in place with
-    the missing tail columns read as zero.  Ragged S, both dtypes, [B,S,H,D] views."""
+    """Kernel head dim 160 on the 128-row eight-wave kernel (tile (128, 64); these grids'
+    default is 64 rows where their 64-row blocks fit the CUs once): stages split into a
+    128-column part and a 32-column tail part; head dims 129-159 run in place with the
+    missing tail columns read as zero.  Ragged S, both dtypes, [B,S,H,D] views."""
     import torch
 
     from tiledattention import _lib, sdpa
@@ -248,15 +249,50 @@ def test_eight_wave_d160(gpu, d, dtype, causal, s):
     rows = None if s <= 2048 else sample_rows(s, 96)
     ref = oracle_f32(q, k, v, causal=causal, rows=rows)
     say(f"eight-wave D={d} {dtype} (2,3,{s},{d}) causal={causal}")
-    out = run_gpu(q, k, v, causal=causal)
+    out = run_gpu(q, k, v, causal=causal, tile_m=128, tile_n=64)
     assert out.shape == (2, 3, s, d) and out.is_contiguous()
     check_close(as_f32(out, rows), ref, dtype, what=f"eight-wave D={d}")
     dev = torch.device("cuda:0")
     bshd = [t.transpose(1, 2).contiguous().to(dev).transpose(1, 2) for t in (q, k, v)]
     say(f"eight-wave D={d} {dtype} (2,3,{s},{d}) causal={causal} [B,S,H,D] views")
-    out = sdpa(*bshd, causal=causal)
+    with knobs(tile_m=128, tile_n=64):
+        out = sdpa(*bshd, causal=causal)
     torch.cuda.synchronize()
     check_close(as_f32(out, rows), ref, dtype, what=f"eight-wave D={d} BSHD")
+    say(f"default tile D={d} {dtype} (2,3,{s},{d}) causal={causal}")
+    out = run_gpu(q, k, v, causal=causal)
+    check_close(as_f32(out, rows), ref, dtype, what=f"default tile D={d}")
+
+
+@pytest.mark.parametrize("d,dtype,causal,s,tn", [
+    (160, "bfloat16", True, 2048, 64), (160, "float16", False, 1000, 64), (144, "bfloat16", True, 777, 64),
+    (136, "float16", False, 3000, 64), (160, "bfloat16", True, 1, 64), (160, "float16", True, 129, 64),
+])
+def test_64_row_d160(gpu, d, dtype, causal, s, tn):
+    """Kernel head dim 160 on the 64-row eight-wave kernel (tile (64, 64), the only TILE_N
+    above D = 128; fp32 accumulation): the 128 + 32 column stage split, five 32-wide d blocks of O and the
+    four-way merge of five chunks a part; head dims 129-159 in place.  Ragged S, both
+    dtypes, [B,S,H,D] views."""
+    import torch
+
+    from tiledattention import _lib, sdpa
+
+    assert _lib.kernel_symbol(dtype=_lib.TA_BF16, head_dim=160, tile_m=64, tile_n=tn, causal=causal,
+                              tail=True, accum=_lib.TA_ACC_FP32)[1].startswith("ta_fwd_pp64_")
+    q, k, v = inputs((2, 3, s, d), dtype, 640 + d + s)
+    rows = None if s <= 2048 else sample_rows(s, 96)
+    ref = oracle_f32(q, k, v, causal=causal, rows=rows)
+    say(f"64-row D={d} {dtype} (2,3,{s},{d}) causal={causal} tile (64,{tn})")
+    out = run_gpu(q, k, v, causal=causal, tile_m=64, tile_n=tn, accum_mode="fp32")
+    assert out.shape == (2, 3, s, d) and out.is_contiguous()
+    check_close(as_f32(out, rows), ref, dtype, what=f"64-row D={d}")
+    dev = torch.device("cuda:0")
+    bshd = [t.transpose(1, 2).contiguous().to(dev).transpose(1, 2) for t in (q, k, v)]
+    say(f"64-row D={d} {dtype} (2,3,{s},{d}) causal={causal} [B,S,H,D] views")
+    with knobs(tile_m=64, tile_n=tn, accum_mode="fp32"):
+        out = sdpa(*bshd, causal=causal)
+    torch.cuda.synchronize()
+    check_close(as_f32(out, rows), ref, dtype, what=f"64-row D={d} BSHD")
 
 
 @pytest.mark.parametrize("d,dtype,causal,s,tn", [

@@ -273,7 +273,10 @@ def test_sched_env(monkeypatch):
     (1024, 128, 32, "fp32", (128, 64)),  # B2 H16: 512 blocks of 64 rows
     (512, 64, 8, "fp32", (64, 64)),
     (512, 96, 8, "fp32", (64, 64)),      # kernel head dim 128 (in-place padding)
-    (512, 160, 8, "fp32", (128, 64)),    # no 64-row eight-wave kernel above D = 128
+    (512, 160, 8, "fp32", (64, 64)),     # the 64-row eight-wave kernel at D = 160
+    (2048, 144, 8, "fp32", (64, 64)),    # kernel head dim 160 (in-place padding)
+    (4096, 160, 8, "fp32", (128, 64)),   # 512 blocks of 64 rows
+    (512, 200, 8, "fp32", (128, 64)),    # kernel head dim 256: the four-wave kernel
     (512, 128, 8, "fp16", (64, 64)),     # input-dtype accumulation: its 64-row eight-wave kernel
     (512, 160, 8, "fp16", (128, 64)),    # D = 160: the four-wave kernels
     (512, 128, 0, "fp32", (128, 64)),    # no head count given
@@ -301,8 +304,8 @@ def test_default_tile_n_follows_the_reference_rule(s, d, causal, n_bh, expected)
 
 
 def test_64_row_tiles_select_the_eight_wave_kernel():
-    """Tiles (64, 64) / (64, 128) with fp32 accumulation at D = 64 / 128 run ta_fwd_pp64_*;
-    the tail-masked variant whenever S is not a multiple of the 128-key step."""
+    """Tiles (64, 64) / (64, 128) with fp32 accumulation at D = 64, 96, 128 and 160 run
+    ta_fwd_pp64_*; the tail-masked variant whenever S is not a multiple of the 128-key step."""
     f, sym = _lib.kernel_symbol(dtype=_lib.TA_BF16, head_dim=128, tile_m=64, tile_n=128, causal=True,
                                 tail=False, accum=_lib.TA_ACC_FP32)
     assert (f, sym) == ("attn_fwd_pp.hsaco", "ta_fwd_pp64_bf16_d128_c1_t0")
@@ -315,7 +318,9 @@ def test_64_row_tiles_select_the_eight_wave_kernel():
     assert _lib.kernel_symbol(dtype=_lib.TA_FP16, head_dim=160, tile_m=128, tile_n=64, causal=True,
                               tail=False, accum=_lib.TA_ACC_INPUT)[1].startswith("ta_fwd_f16_d160_m128_n64")
     assert _lib.kernel_symbol(dtype=_lib.TA_FP16, head_dim=160, tile_m=64, tile_n=64, causal=False,
-                              tail=True, accum=_lib.TA_ACC_FP32)[1].startswith("ta_fwd_f16_d160_m64_n64")
+                              tail=True, accum=_lib.TA_ACC_FP32)[1] == "ta_fwd_pp64_f16_d160_c0_t1"
+    assert _lib.kernel_symbol(dtype=_lib.TA_FP16, head_dim=160, tile_m=64, tile_n=64, causal=False,
+                              tail=True, accum=_lib.TA_ACC_INPUT)[1].startswith("ta_fwd_f16_d160_m64_n64")
     tm = dict(tile_m=64, tile_n=64, accum=_lib.TA_ACC_FP32, head_dim=128)
     assert not _lib.tail_masked(seq_len=512, **tm)
     assert _lib.tail_masked(seq_len=320, **tm)   # multiple of 64, not of the 128-key step

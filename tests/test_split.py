@@ -232,7 +232,8 @@ def test_split_capability_rule():
     # in-place padding (d_real) exists on both eight-wave forms
     ew = flash_fwd._eight_wave_kernel
     assert ew(**ok) and ew(**{**ok, "tile_m": 64}) and ew(**{**ok, "tile_m": 64, "tile_n": 128})
-    assert not ew(**{**ok, "tile_m": 64, "kernel_head_dim": 160})
+    assert ew(**{**ok, "tile_m": 64, "kernel_head_dim": 160})
+    assert not ew(**{**ok, "tile_m": 64, "kernel_head_dim": 256})
     with pytest.raises(ValueError, match="D <= 160"):
         _lib.kernel_symbol(dtype=_lib.TA_BF16, head_dim=256, tile_m=128, tile_n=64, causal=True,
                            tail=False, accum=_lib.TA_ACC_FP32, split=True)

@@ -50,14 +50,14 @@ def uses_pairs(*, causal: bool, head_dim: int, tile_m: int, tile_n: int, accum: 
 
 def eight_wave_family(*, tile_m: int, tile_n: int, accum: int, head_dim: int) -> bool:
     """The eight-wave kernels (attn_fwd_pp.hsaco): fp32 accumulation with tiles (128, 64) /
-    (128, 128) at D = 64, 96, 128 or 160, or tiles (64, 64) / (64, 128) at D = 64, 96 or 128; input-dtype
+    (128, 128) or (64, 64) / (64, 128) at D = 64, 96, 128 or 160; input-dtype
     accumulation with any tile at D = 64 or 128.  The same rule as eight_wave_family() in
     csrc/tiledattn.cpp."""
     if tile_n not in (64, 128) or tile_m not in (64, 128):
         return False
     if accum != TA_ACC_FP32:  # input-dtype accumulation: ta_fwd_ppl_* / ta_fwd_ppl64_*
         return head_dim in (64, 128)
-    return (tile_m == 128 and head_dim <= 160) or (tile_m == 64 and head_dim in (64, 96, 128))
+    return (tile_m == 128 and head_dim <= 160) or (tile_m == 64 and head_dim in (64, 96, 128, 160))
 
 
 def tail_masked(*, seq_len: int, tile_m: int, tile_n: int, accum: int, head_dim: int,

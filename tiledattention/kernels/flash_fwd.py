@@ -223,11 +223,13 @@ def _default_tile_config_for_shape_gfx950(*, seq_len: int, head_dim: int, causal
     128 query rows per workgroup: the eight-wave kernel (two waves per SIMD splitting every
     128-key step, one workgroup per CU; at kernel head dims above 128 with input-dtype
     accumulation the four-wave kernel with 64-key tiles).  When the 64-row blocks of all
-    ``n_bh`` heads fit the CUs in one wave (B*H*ceil(S/64) <= CUs; kernel head dim 64 or
-    128), 64 rows instead: the 64-row eight-wave kernel halves each block's key
-    loop and the grid is still one workgroup per CU (B1 H8 bf16: causal S=1024 15.0 -> 12.0
-    us, S=2048 23.5 -> 18.8; non-causal S=1024 14.4 -> 11.9, S=2048 23.3 -> 20.3; D=64 causal
-    S=2048 18.2 -> 13.5).  With more blocks than CUs, the second block of a CU pays the
+    ``n_bh`` heads fit the CUs in one wave (B*H*ceil(S/64) <= CUs; head dims up to 128, or up
+    to 160 with fp32 accumulation), 64 rows instead: the 64-row eight-wave kernel halves each
+    block's key loop and the grid is still one workgroup per CU (B1 H8 bf16: causal S=1024
+    15.0 -> 12.0 us, S=2048 23.5 -> 18.8; non-causal S=1024 14.4 -> 11.9, S=2048 23.3 ->
+    20.3; D=64 causal S=2048 18.2 -> 13.5; D=160 S=512 / 1024 / 2048 causal 12.2 -> 10.0 /
+    17.5 -> 13.1 / 28.3 -> 21.9, non-causal 12.3 -> 9.7 / 17.6 -> 13.0 / 28.3 -> 26.8).
+    With more blocks than CUs, the second block of a CU pays the
     fixed cost of a workgroup again (B2 H16 S1024 causal: 16.4 -> 21.4 us), so 128 rows.
     The caller keeps 128 rows where the 128-row kernel would split key ranges
     (``_split_preferred``).
@@ -239,7 +241,8 @@ def _default_tile_config_for_shape_gfx950(*, seq_len: int, head_dim: int, causal
     979 TFLOP/s against TILE_N = 64).
     """
     tile_n = 128 if (not causal and head_dim == 128 and seq_len >= 2048) else 64
-    if (0 < head_dim <= 128 and n_bh > 0 and seq_len > 0
+    max_d64 = 160 if accum_mode == "fp32" else 128  # 64-row eight-wave kernels
+    if (0 < head_dim <= max_d64 and n_bh > 0 and seq_len > 0
             and n_bh * ((seq_len + 63) // 64) <= _CU_COUNT):
         return 64, tile_n
     return 128, tile_n

@@ -98,8 +98,8 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   constexpr int NLDS = NLD + NLDT;   // loads per wave per tensor per step (own half)
   static_assert(STAGE_A % (8 * 1024) == 0, "stage must split over the eight waves");
   static_assert(TK == kPPKeys && (TM == kPPRows || TM == 64), "steps of 128 keys, blocks of 128 or 64 rows");
-  static_assert(TM == 128 || (!SPLIT && (D == 64 || D == 96 || D == 128)),
-                "64-row blocks: whole rows, D 64, 96 or 128");
+  static_assert(TM == 128 || (!SPLIT && (D == 64 || D == 96 || D == 128 || D == 160)),
+                "64-row blocks: whole rows, D 64, 96, 128 or 160");
   constexpr bool LOWP = LOWP_TN != 0;
   static_assert(!LOWP || (!SPLIT && (D == 64 || D == 128)), "input-dtype accumulation: whole rows, D 64 or 128");
   // Input-dtype accumulation: key steps between roundings of a wave's O, TILE_N keys of its
@@ -1257,9 +1257,11 @@ TA_PP_PSPLIT_DEFINE(bf16, 1, 160, 1)
 TA_PP64_DEFINE_CT(f16, 0, 64)
 TA_PP64_DEFINE_CT(f16, 0, 96)
 TA_PP64_DEFINE_CT(f16, 0, 128)
+TA_PP64_DEFINE_CT(f16, 0, 160)
 TA_PP64_DEFINE_CT(bf16, 1, 64)
 TA_PP64_DEFINE_CT(bf16, 1, 96)
 TA_PP64_DEFINE_CT(bf16, 1, 128)
+TA_PP64_DEFINE_CT(bf16, 1, 160)
 TA_PPL_DEFINE_CT(f16, 0, 64)
 TA_PPL_DEFINE_CT(f16, 0, 128)
 TA_PPL_DEFINE_CT(bf16, 1, 64)

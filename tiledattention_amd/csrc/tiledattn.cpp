@@ -98,10 +98,11 @@ bool eight_wave(int64_t tm, int64_t tn, int64_t accum, int64_t d) {
 }
 
 // Its 64-row form (ta_fwd_pp64_*) serves the 64-row tiles with fp32 accumulation at D = 64,
-// 96 and 128: the same 128-key steps, each group's 64 keys split between two waves per row
-// block, and no split key ranges or causal pairs.
+// 96, 128 and 160: the same 128-key steps, each group's 64 keys split between two waves per
+// row block, and no split key ranges or causal pairs.
 bool eight_wave64(int64_t tm, int64_t tn, int64_t accum, int64_t d) {
-  return tm == 64 && (tn == 64 || tn == 128) && accum == TA_ACC_FP32 && (d == 64 || d == 96 || d == 128);
+  return tm == 64 && (tn == 64 || tn == 128) && accum == TA_ACC_FP32 &&
+         (d == 64 || d == 96 || d == 128 || d == 160);
 }
 
 // Input-dtype accumulation on the eight-wave kernels (ta_fwd_ppl_* for 128-row tiles,
