@@ -64,7 +64,8 @@ typedef struct ta_fwd_args {
                           and below 2^23; S * stride[2] * 2 bytes below 2^31 for k and v
                           (and for q on the eight-wave kernels: fp32 accumulation with
                           tiles (128, 64) / (128, 128), D <= 160, or (64, 64) / (64, 128),
-                          D = 64 or 128), which are read with 32-bit buffer offsets */
+                          D = 64, 96 or 128, or (64, 64), D = 160), which are read with
+                          32-bit buffer offsets */
   int64_t k_stride[4];
   int64_t v_stride[4];
   int64_t o_stride[4];
@@ -85,7 +86,8 @@ typedef struct ta_fwd_args {
                       write them, so a narrower head dim needs no padded copies (the
                       reference pads on the host, flash_fwd.py:868-872).  The eight-wave
                       kernels only (fp32 accumulation; tiles (128, 64) and (128, 128) with
-                      D <= 160, tiles (64, 64) and (64, 128) with D = 64 or 128). */
+                      D <= 160, tiles (64, 64) and (64, 128) with D = 64, 96 or 128, tile
+                      (64, 64) with D = 160). */
   int32_t aligned; /* 1: the kernel variant without tail masking runs when S is a multiple
                       of tile_m and tile_n, and on the eight-wave kernels of their 128-key
                       step (the reference's aligned fast path,

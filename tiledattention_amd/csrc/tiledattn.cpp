@@ -388,9 +388,9 @@ ta_status validate_args(const ta_fwd_args* a, int64_t* n_bh_out, int64_t* n_qblk
       return fail(TA_EINVAL, "d_real %d (0, or a multiple of 8 in [8, D])", a->d_real);
     if (!eight_wave_family(a->tile_m, a->tile_n, a->accum, a->D))
       return fail(TA_EUNSUPPORTED,
-                  "d_real needs an eight-wave kernel: tile (128, 64) or (128, 128) with fp32 "
-                  "accumulation and D <= 160, or D = 64 or 128 with any tile and fp32 or "
-                  "input-dtype accumulation");
+                  "d_real needs an eight-wave kernel: fp32 accumulation with D <= 160 (tile "
+                  "(128, 64) or (128, 128), or (64, 64) / (64, 128) up to D = 128 and (64, 64) "
+                  "at D = 160), or D = 64 or 128 with any tile and input-dtype accumulation");
   }
   if (a->B < 0 || a->H < 0 || a->S < 0) return fail(TA_EINVAL, "negative shape");
   ta_status shape_st = check_shape(a->D, a->tile_m, a->tile_n, a->accum);
