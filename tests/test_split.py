@@ -277,3 +277,18 @@ def test_knob_snapshot_follows_the_environment(monkeypatch):
 
     read = set(re.findall(r'"(TILEDATTN_[A-Z_]+)"', src))
     assert read == set(flash_fwd._KNOBS)
+
+
+def test_plan_model_paired_split_boundaries(lib):
+    """The paired split's rule: causal, more than CUs / 2 and at most CUs query blocks of 128
+    rows, 32 or more a head; the edges of each condition, on 256 and 304 CUs."""
+    P = _lib.TA_SPLIT_PAIRS
+    assert _plan(lib, 4096, 8, 1) == P            # 256 blocks = CUs
+    assert _plan(lib, 4096, 5, 1) == P            # 160 > 128
+    assert _plan(lib, 4096, 4, 1) != P            # 128: not more than half
+    assert _plan(lib, 4096, 9, 1) != P            # 288 > 256
+    assert _plan(lib, 3968, 8, 1) != P            # 31 blocks a head
+    assert _plan(lib, 3969, 8, 1) == P            # 32 blocks (ragged last one)
+    assert _plan(lib, 4096, 9, 1, cus=304) == P   # 288 <= 304
+    assert _plan(lib, 4096, 4, 1, cus=304) != P   # 128 <= 152
+    assert _plan(lib, 8192, 3, 0) != P            # non-causal
