@@ -241,6 +241,30 @@ def test_pair_kernel_symbols_exist(dtype):
             assert f == "attn_fwd_pp.hsaco" and sym.encode() + b"\x00" in data, sym
 
 
+@pytest.mark.parametrize("dtype", [_lib.TA_FP16, _lib.TA_BF16])
+def test_rows256_kernel_symbols_exist(dtype):
+    """The 256-row rule (non-causal, fp32, D = 64 / 128, two or more 256-row blocks a CU)
+    names symbols of the eight-wave object; C4 takes it, smaller or causal grids do not."""
+    data = (_lib.lib_dir() / "attn_fwd_pp.hsaco").read_bytes()
+    c4 = dict(causal=False, tile_m=128, tile_n=64, accum=_lib.TA_ACC_FP32, n_bh=64, seq_len=4096,
+              compute_units=256)
+    for d in (64, 128):
+        assert _lib.uses_rows256(head_dim=d, **c4)
+        for tail in (False, True):
+            f, sym = _lib.kernel_symbol(dtype=dtype, head_dim=d, tile_m=128, tile_n=64, causal=False,
+                                        tail=tail, accum=_lib.TA_ACC_FP32, rows256=True)
+            assert f == "attn_fwd_pp.hsaco" and sym.encode() + b"\x00" in data, sym
+    assert not _lib.uses_rows256(head_dim=128, **{**c4, "causal": True})
+    assert not _lib.uses_rows256(head_dim=160, **c4)
+    assert not _lib.uses_rows256(head_dim=128, **{**c4, "n_bh": 31})   # 496 < 512 blocks
+    assert _lib.uses_rows256(head_dim=128, **{**c4, "n_bh": 32})       # 512
+    assert not _lib.uses_rows256(head_dim=128, **{**c4, "accum": _lib.TA_ACC_INPUT})
+    assert not _lib.uses_rows256(head_dim=128, **{**c4, "tile_m": 64})
+    with pytest.raises(ValueError, match="256-row"):
+        _lib.kernel_symbol(dtype=dtype, head_dim=128, tile_m=128, tile_n=64, causal=True, tail=False,
+                           accum=_lib.TA_ACC_FP32, rows256=True)
+
+
 @pytest.mark.parametrize("kw,expected", [
     (dict(), True),                                   # C3 S=8192: 512 blocks on 256 CUs
     (dict(n_qblk=32), False),                          # one wave of workgroups

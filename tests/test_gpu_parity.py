@@ -609,3 +609,34 @@ def test_golden_fixture_c1(gpu):
     say("golden c1")
     out = run_gpu(fx["q"], fx["k"], fx["v"], causal=bool(fx["causal"]))
     check_close(as_f32(out), fx["out_f32"], str(fx["dtype"]), what="golden c1")
+
+
+@pytest.mark.parametrize("shape,dtype,tiles", [
+    ((4, 16, 2048, 128), "bfloat16", (128, 64)),
+    ((4, 16, 2100, 64), "float16", (128, 64)),     # ragged: the tail-masked variant
+    ((2, 32, 2304, 120), "bfloat16", (128, 128)),  # kernel head dim 128, columns 120.. zero
+    ((8, 8, 2000, 128), "float16", (128, 64)),
+])
+def test_rows256_noncausal(gpu, shape, dtype, tiles):
+    """Non-causal grids of two or more 256-row blocks per CU run ta_fwd_pp256_* (the two wave
+    groups on different rows, every key of a step each): sampled rows against the oracle,
+    contiguous and [B,S,H,D] views."""
+    import torch
+
+    from tiledattention import sdpa
+
+    b, h, s, d = shape
+    assert b * h * -(-s // 256) >= 512
+    q, k, v = inputs(shape, dtype, 256 + s + d)
+    rows = sample_rows(s, 64)
+    ref = oracle_f32(q, k, v, causal=False, rows=rows)
+    say(f"256-row blocks {dtype} {shape} non-causal tiles={tiles}")
+    out = run_gpu(q, k, v, causal=False, tile_m=tiles[0], tile_n=tiles[1], accum_mode="fp32")
+    check_close(as_f32(out, rows), ref, dtype, what=f"256-row {shape}")
+    dev = torch.device("cuda:0")
+    bshd = [t.transpose(1, 2).contiguous().to(dev).transpose(1, 2) for t in (q, k, v)]
+    say(f"256-row blocks {dtype} {shape} non-causal [B,S,H,D] views")
+    with knobs(tile_m=tiles[0], tile_n=tiles[1], accum_mode="fp32"):
+        out = sdpa(*bshd, causal=False)
+    torch.cuda.synchronize()
+    check_close(as_f32(out, rows), ref, dtype, what=f"256-row {shape} BSHD")

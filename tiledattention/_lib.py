@@ -70,15 +70,30 @@ def tail_masked(*, seq_len: int, tile_m: int, tile_n: int, accum: int, head_dim:
     return not (aligned and seq_len % tile_m == 0 and seq_len % tile_n == 0 and steps)
 
 
+def uses_rows256(*, causal: bool, head_dim: int, tile_m: int, tile_n: int, accum: int, n_bh: int,
+                 seq_len: int, compute_units: int) -> bool:
+    """Whether a whole-row launch runs 256-row blocks (ta_fwd_pp256_*); the same rule as
+    use_rows256() in csrc/tiledattn.cpp."""
+    return (not causal and tile_m == 128 and tile_n in (64, 128) and accum == TA_ACC_FP32
+            and head_dim in (64, 128) and n_bh * -(-seq_len // 256) >= 2 * compute_units)
+
+
 def kernel_symbol(*, dtype: int, head_dim: int, tile_m: int, tile_n: int, causal: bool,
-                  tail: bool, accum: int, split: bool = False, pair: bool = False) -> tuple[str, str]:
+                  tail: bool, accum: int, split: bool = False, pair: bool = False,
+                  rows256: bool = False) -> tuple[str, str]:
     """(code object file, kernel symbol) the C ABI launches for a configuration; the same
     rule as kernel_id() in csrc/tiledattn.cpp (used to label measurements).  ``split``
     names the split-key-range kernel (its merge kernel is ta_fwd_merge_<dt>_d<D>_c<c>),
     ``pair`` the causal pair kernel (``uses_pairs``); both together the paired-split
-    kernel.  ``tail`` is the variant the C ABI picks (``tail_masked``)."""
+    kernel; ``rows256`` the 256-row kernel (``uses_rows256``; its tail variant also runs
+    when S is not a multiple of 256).  ``tail`` is the variant the C ABI picks
+    (``tail_masked``)."""
     dt = "bf16" if dtype == TA_BF16 else "f16"
     c, t = int(bool(causal)), int(bool(tail))
+    if rows256:
+        if causal or head_dim not in (64, 128) or accum != TA_ACC_FP32 or tile_m != 128:
+            raise ValueError("256-row blocks exist for non-causal fp32 D = 64 / 128 at 128-row tiles")
+        return "attn_fwd_pp.hsaco", f"ta_fwd_pp256_{dt}_d{head_dim}_c0_t{t}"
     if tile_m == 128 and tile_n in (64, 128) and accum == TA_ACC_FP32 and head_dim <= 160:
         kind = ("pp_psplit" if pair else "pp_split") if split else ("pp_pair" if pair else "pp")
         return "attn_fwd_pp.hsaco", f"ta_fwd_{kind}_{dt}_d{head_dim}_c{c}_t{t}"

@@ -73,9 +73,12 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
                                                   char* lds_k1, char* lds_v0, char* lds_v1) {
   constexpr int TM = TMR;            // query rows per workgroup
   constexpr int TK = 128;            // keys per workgroup step (64 per wave group)
-  constexpr int NRB = TM / 32;       // 32-row blocks
-  constexpr int NKS = 4 / NRB;       // key slots of a group's 64 keys (1 or 2)
-  constexpr int KB = 2 / NKS;        // 32-key blocks per wave per step
+  // 256 rows (non-causal whole rows): the two groups own different rows, 128 each, and every
+  // wave takes all 128 keys of a step (64 MFMAs a cluster, 64 scores a lane).
+  constexpr bool R256 = TMR == 256;
+  constexpr int NRB = R256 ? 4 : TM / 32;   // 32-row blocks of a group
+  constexpr int NKS = R256 ? 1 : 4 / NRB;   // key slots of a group's 64 keys (1 or 2)
+  constexpr int KB = R256 ? 4 : 2 / NKS;    // 32-key blocks per wave per step
   // A stage holds 128 key rows: the first DA columns of each row in a main part (rows of
   // 2 DA bytes; DA = 128 at D = 160, 64 at D = 96, D otherwise), the rest (32 columns at
   // D = 96 and 160) in a tail part of 64-byte rows behind it, so both parts have
@@ -97,8 +100,11 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   constexpr int NLDT = DT2 ? 1 : 0;  // tail loads (a group's 64 tail rows are 4 KiB)
   constexpr int NLDS = NLD + NLDT;   // loads per wave per tensor per step (own half)
   static_assert(STAGE_A % (8 * 1024) == 0, "stage must split over the eight waves");
-  static_assert(TK == kPPKeys && (TM == kPPRows || TM == 64), "steps of 128 keys, blocks of 128 or 64 rows");
-  static_assert(TM == 128 || (!SPLIT && (D == 64 || D == 96 || D == 128 || D == 160)),
+  static_assert(TK == kPPKeys && (TM == kPPRows || TM == 64 || R256),
+                "steps of 128 keys, blocks of 64, 128 or 256 rows");
+  static_assert(!R256 || (!CAUSAL && !SPLIT && LOWP_TN == 0 && (D == 64 || D == 128)),
+                "256-row blocks: non-causal whole rows, fp32 accumulation, D 64 or 128");
+  static_assert(TM != 64 || (!SPLIT && (D == 64 || D == 96 || D == 128 || D == 160)),
                 "64-row blocks: whole rows, D 64, 96, 128 or 160");
   constexpr bool LOWP = LOWP_TN != 0;
   static_assert(!LOWP || (!SPLIT && (D == 64 || D == 128)), "input-dtype accumulation: whole rows, D 64 or 128");
@@ -108,10 +114,10 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   static_assert(!LOWP || (kLowpSteps >= 1 && kLowpSteps <= 4), "TILE_N 64 or 128");
   // Raised MFMA-cluster priority only in the kernels built for two workgroups per CU (the
   // non-causal D = 64 whole-row ones, TA_PP_WAVES below).
-  constexpr bool kPrioMfma = !SPLIT && D == 64 && !CAUSAL;
+  constexpr bool kPrioMfma = !SPLIT && D == 64 && !CAUSAL && !R256;
   // Those kernels have 128 VGPRs a lane (four waves per SIMD): P is formed two scores at a
   // time there, since a phased softmax holds 32 exponent arguments beside the 32 scores.
-  constexpr bool kPhasedP = !kPrioMfma;
+  constexpr bool kPhasedP = !kPrioMfma && !R256;  // R256: 64 scores a lane, no room for 64 more
   using DTy = DType<DT>;
   // P.V MFMAs of a cluster issued after its closing barrier, in the wave's softmax phase
   // (operands read in the cluster, held in registers): the 128-row input-dtype kernels, 3
@@ -148,7 +154,7 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   const int v_rb = (int)p.v_ss * 2;
 
   const int q0 = qt * TM;
-  const int wq0 = q0 + rb * 32;  // first query row of this wave
+  const int wq0 = R256 ? q0 + 128 * grp + 32 * wr : q0 + rb * 32;  // first query row of this wave
   const int my_q = wq0 + l32;    // this lane's query row
 
   // ---- Q fragment: B operand of S^T = K Q^T, kept for the whole key loop ------------
@@ -163,7 +169,7 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   const int t_end = SPLIT ? wi.t_end : ((CAUSAL ? min(S, q0 + TM) : S) + TK - 1) / TK;
   const int wave_kv_end = CAUSAL ? min(S, wq0 + 32) : S;
   const int gkoff = 64 * grp;              // the group's keys in a step: [TK t + gkoff, + 64)
-  const int koff = gkoff + 32 * KB * ks;   // this wave's: [TK t + koff, + 32 KB)
+  const int koff = R256 ? 0 : gkoff + 32 * KB * ks;   // this wave's: [TK t + koff, + 32 KB)
 
   // ---- staging: HBM -> LDS directly -------------------------------------------------
   // A stage is 1 KiB chunks g; lane l of the wave instruction that fills chunk g writes
@@ -175,7 +181,10 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   // load of a tensor.  One buffer resource per step starts at the step's first key; rows
   // past S are outside it and read as zero, and a step past the last gets an empty
   // resource (its loads write zeros into a stage half nobody reads any more).
-  const int ld_g0 = gkoff / RPL + wr;  // first chunk this wave fills
+  // R256: both groups read whole stages, so the eight waves fill every chunk, wave w the
+  // chunks w + 8 i (g & 3 and g & 1 stay fixed per wave, so one per-lane offset still serves).
+  constexpr int LS = R256 ? 8 : 4;     // chunk stride of a wave's loads
+  const int ld_g0 = R256 ? wave : gkoff / RPL + wr;  // first chunk this wave fills
   const int ld_row = ld_g0 * RPL + lane / CPR;
   const int ld_pc = lane % CPR;
   // A logical chunk at or past d_real gets an offset of 2^31 or more: every buffer resource
@@ -208,8 +217,8 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          r, (__attribute__((address_space(3))) void*)(stage + (ld_g0 + 4 * i) * 1024), 16,
-          vo + i * 4 * RPL * rb, 0, 0, 0);
+          r, (__attribute__((address_space(3))) void*)(stage + (ld_g0 + LS * i) * 1024), 16,
+          vo + i * LS * RPL * rb, 0, 0, 0);
     }
     if constexpr (NLDT != 0) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -571,14 +580,28 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
   // softmax cluster, like the loads of every MFMA cluster.
   static_assert(2 * NLDS < 16, "vmcnt field");
   dma(kp, p.k_ss, k_rb, kvo, tkvo, t_beg, lds_k0);
-  if (TM == 128 || grp == 0) dma_q(lds_v1);  // 64-row blocks: group 0's chunks hold every row
+  if constexpr (R256) {
+    // Q straight into the B-operand registers: lane l holds row wq0 + l % 32, columns
+    // 16 kk + 8 (l / 32) .. + 8 (the layout the LDS read below produces); rows past S and
+    // columns past d_real are zero.  Counted by vmcnt before K_1 and V_0.
+    const uint16_t* qrow = qp + (int64_t)(my_q < S ? my_q : 0) * p.q_ss;
+#pragma unroll
+    for (int kk = 0; kk < DK; ++kk) {
+      const int d0 = 16 * kk + 8 * hl;
+      qf[kk] = my_q < S && d0 < d_real ? *(const u32x4*)(qrow + d0) : u32x4{0u, 0u, 0u, 0u};
+    }
+  } else if (TM == 128 || grp == 0) {
+    dma_q(lds_v1);  // 64-row blocks: group 0's chunks hold every row
+  }
   dma(kp, p.k_ss, k_rb, kvo, tkvo, t_beg + 1, lds_k1);
   dma(vp, p.v_ss, v_rb, vvo, tvvo, t_beg, lds_v0);
-  __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * NLDS));
+  // R256: every prologue load, since the first MFMA cluster of each group reads K_1 and
+  // V_0 shares loaded by the other group's waves.
+  __builtin_amdgcn_s_waitcnt(R256 ? 0x0F70 : 0x0F70 | (2 * NLDS));
   barrier();
   // Q fragment from lds_v1 (rows 32 wr + l32, read like a K operand); lds_v1 receives V_1
   // only in the first MFMA cluster, at least two barriers later.
-  {
+  if constexpr (!R256) {
     const int qr = 32 * rb + l32;
 #pragma unroll
     for (int kk = 0; kk < DK; ++kk) {
@@ -601,14 +624,23 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
 
   // Step t with stage parity PAR: the stages of K_t (consumed; receives K_{t+2}), K_{t+1},
   // V_t and V_{t-1} (consumed; receives V_{t+1}).
-  auto iter = [&](int t, auto par_tag) {
+  auto iter = [&](int t, auto par_tag, auto g1_tag) {
     constexpr int PAR = decltype(par_tag)::value;
     char* k_cur = PAR ? lds_k1 : lds_k0;
     char* k_nxt = PAR ? lds_k0 : lds_k1;
     char* v_cur = PAR ? lds_v1 : lds_v0;
     char* v_nxt = PAR ? lds_v0 : lds_v1;
+    // R256: group 1 issues its share of K_{t+2} and V_{t+1} at the start of its softmax
+    // (the phase of group 0's MFMA cluster, which loads the rest; both stages are free:
+    // their last readers were the two MFMA clusters of step t - 1) and waits for it at the
+    // end of its MFMA cluster, so both shares have landed before group 0 reads the stages.
+    constexpr bool loads_in_softmax = R256 && decltype(g1_tag)::value;
+    if constexpr (loads_in_softmax) {
+      dma(kp, p.k_ss, k_rb, kvo, tkvo, t + 2, k_cur);
+      dma(vp, p.v_ss, v_rb, vvo, tvvo, t + 1, v_nxt);
+    }
     softmax(t, par_tag);
-    wait_dma();  // this group's halves of K_{t+1} and V_t (issued one MFMA cluster ago)
+    if constexpr (!loads_in_softmax) wait_dma();  // this wave's K_{t+1} and V_t loads (one cluster ago)
     barrier();
     // MFMA cluster: S of step t + 1 (past the last step it reads a stale or zero stage and
     // is never used) and P.V of step t, one straight-line block whose LDS reads run AHEAD
@@ -620,9 +652,14 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
     if constexpr (kPrioMfma) __builtin_amdgcn_s_setprio(1);
     qk(k_nxt);
     pv(v_cur);
-    dma(kp, p.k_ss, k_rb, kvo, tkvo, t + 2, k_cur);
-    dma(vp, p.v_ss, v_rb, vvo, tvvo, t + 1, v_nxt);
-    mfma_cluster_order(2 * NLDS);
+    if constexpr (loads_in_softmax) {
+      mfma_cluster_order(0);
+      wait_dma();
+    } else {
+      dma(kp, p.k_ss, k_rb, kvo, tkvo, t + 2, k_cur);
+      dma(vp, p.v_ss, v_rb, vvo, tvvo, t + 1, v_nxt);
+      mfma_cluster_order(2 * NLDS);
+    }
     if constexpr (kPrioMfma) __builtin_amdgcn_s_setprio(0);
     barrier();
     if constexpr (kLateMfma > 0) {
@@ -635,12 +672,14 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
       }
     }
   };
+  using G0 = std::false_type;
+  using G1 = std::integral_constant<bool, R256>;  // group 1's own load schedule (R256 only)
   if (grp == 0) {
     first();
     barrier();
     for (int t = t_beg; t < t_end; t += 2) {
-      iter(t, std::integral_constant<int, 0>{});
-      if (t + 1 < t_end) iter(t + 1, std::integral_constant<int, 1>{});
+      iter(t, std::integral_constant<int, 0>{}, G0{});
+      if (t + 1 < t_end) iter(t + 1, std::integral_constant<int, 1>{}, G0{});
     }
     barrier();  // phase 2 n_steps + 1: group 1's last MFMA cluster
   } else {
@@ -648,12 +687,33 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
     first();
     barrier();
     for (int t = t_beg; t < t_end; t += 2) {
-      iter(t, std::integral_constant<int, 0>{});
-      if (t + 1 < t_end) iter(t + 1, std::integral_constant<int, 1>{});
+      iter(t, std::integral_constant<int, 0>{}, G1{});
+      if (t + 1 < t_end) iter(t + 1, std::integral_constant<int, 1>{}, G1{});
     }
   }
   wait_dma();  // the zero-filling loads of the last two steps, before the merge reuses LDS
   barrier();
+
+  // R256: every wave holds all keys of its 32 rows: O / l straight to the output (the lane
+  // pair l, l + 32 shares a row and holds half of its l each).
+  if constexpr (R256) {
+    float la, lb;
+    swap32(l_part, la, lb);
+    const float inv = 1.0f / (la + lb);
+    if (TAIL && my_q >= S) return;
+    uint16_t* orow = op + (int64_t)my_q * p.o_ss;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = 32 * db + 8 * g + 4 * hl;
+        if (d < d_real)
+          *(u32x2*)(orow + d) = u32x2{DTy::pack(o_acc[db][4 * g] * inv, o_acc[db][4 * g + 1] * inv),
+                                      DTy::pack(o_acc[db][4 * g + 2] * inv, o_acc[db][4 * g + 3] * inv)};
+      }
+    }
+    return;
+  }
 
   // Merge of d blocks [LO, LO + DB/2) of this wave's row block with the partner wave's
   // (same rows, the other key half).  Exchange regions: group 0's waves send from lds_k0,
@@ -1166,7 +1226,16 @@ __device__ __forceinline__ void attn_merge_body(const FwdParams& p) {
     ta::attn_fwd_pp_body<DT, D, true, (T != 0), true, true>(p);                           \
   }
 
-// 64-row blocks (tiles (64, 64) and (64, 128) with fp32 accumulation, D = 64, 96 and 128):
+// 256-row blocks (non-causal whole rows, fp32 accumulation, D = 64 and 128; the C ABI picks
+// them for grids of two or more blocks per CU): ta_fwd_pp256_<f16|bf16>_d<D>_c0_t<0|1>.
+#define TA_PP256_DEFINE(DTN, DT, D, T)                                                     \
+  extern "C" __global__ void __launch_bounds__(512)                                       \
+      __attribute__((amdgpu_waves_per_eu(2, 2)))                                          \
+      ta_fwd_pp256_##DTN##_d##D##_c0_t##T(ta::FwdParams p) {                               \
+    ta::attn_fwd_pp_body<DT, D, false, (T != 0), false, false, 256>(p);                   \
+  }
+
+// 64-row blocks (tiles (64, 64) and (64, 128) with fp32 accumulation, D = 64, 96, 128 and 160):
 // ta_fwd_pp64_<f16|bf16>_d<D>_c<0|1>_t<0|1>, the same residency as the 128-row kernels.
 #define TA_PP64_DEFINE(DTN, DT, D, C, T)                                                   \
   extern "C" __global__ void __launch_bounds__(512)                                       \
@@ -1254,6 +1323,14 @@ TA_PP_PSPLIT_DEFINE(bf16, 1, 128, 0)
 TA_PP_PSPLIT_DEFINE(bf16, 1, 128, 1)
 TA_PP_PSPLIT_DEFINE(bf16, 1, 160, 0)
 TA_PP_PSPLIT_DEFINE(bf16, 1, 160, 1)
+TA_PP256_DEFINE(f16, 0, 64, 0)
+TA_PP256_DEFINE(f16, 0, 64, 1)
+TA_PP256_DEFINE(f16, 0, 128, 0)
+TA_PP256_DEFINE(f16, 0, 128, 1)
+TA_PP256_DEFINE(bf16, 1, 64, 0)
+TA_PP256_DEFINE(bf16, 1, 64, 1)
+TA_PP256_DEFINE(bf16, 1, 128, 0)
+TA_PP256_DEFINE(bf16, 1, 128, 1)
 TA_PP64_DEFINE_CT(f16, 0, 64)
 TA_PP64_DEFINE_CT(f16, 0, 96)
 TA_PP64_DEFINE_CT(f16, 0, 128)

@@ -488,6 +488,16 @@ bool use_pairs(const ta_fwd_args* a, int64_t n_bh, int64_t n_qblk, int ncu) {
   return a->sched == 1 && n_bh * n_qblk >= 2 * (int64_t)ncu;
 }
 
+// Whether a whole-row launch runs 256-row blocks (ta_fwd_pp256_*: the two wave groups own
+// different rows and each takes every key of a step, 64 MFMAs a cluster): non-causal, the
+// eight-wave kernel at D = 64 or 128 with fp32 accumulation, a grid of two or more such
+// blocks per CU (fewer leave CUs idle or unbalanced).
+bool use_rows256(const ta_fwd_args* a, int64_t n_bh, int ncu) {
+  if (a->causal || !eight_wave(a->tile_m, a->tile_n, a->accum, a->D) || (a->D != 64 && a->D != 128))
+    return false;
+  return n_bh * ((a->S + 255) / 256) >= 2 * (int64_t)ncu;
+}
+
 // Whether the split path exists for this configuration (the eight-wave kernel).
 bool split_capable(const ta_fwd_args* a) {
   return eight_wave(a->tile_m, a->tile_n, a->accum, a->D);
@@ -571,13 +581,21 @@ ta_status ta_sdpa_fwd(const ta_fwd_args* a, void* stream) {
   if (guard.err != hipSuccess)
     return fail(TA_EHIP, "set device %d: %s", a->device, hipGetErrorString(guard.err));
   int64_t blocks = n_bh * n_qblk;
-  if (a->causal && eight_wave(a->tile_m, a->tile_n, a->accum, a->D)) {
+  if (eight_wave(a->tile_m, a->tile_n, a->accum, a->D)) {
     int ncu = 0;
     ta_status cst = cu_count_locked(a->device, &ncu);
     if (cst != TA_OK) return cst;
-    if (use_pairs(a, n_bh, n_qblk, ncu)) {
+    if (a->causal && use_pairs(a, n_bh, n_qblk, ncu)) {
       id = pair_kernel_id(a->dtype, (int)a->D, !aligned);
       blocks = n_bh * ((n_qblk + 1) / 2);
+    } else if (use_rows256(a, n_bh, ncu)) {
+      const int64_t nq256 = (a->S + 255) / 256;
+      char name[64];
+      snprintf(name, sizeof(name), "ta_fwd_pp256_%s_d%d_c0_t%d", a->dtype == TA_BF16 ? "bf16" : "f16",
+               (int)a->D, aligned && a->S % 256 == 0 ? 0 : 1);
+      id = KernelId{"attn_fwd_pp.hsaco", name, 512u};
+      p.n_qblk = static_cast<int32_t>(nq256);
+      blocks = n_bh * nq256;
     }
   }
   hipFunction_t fn = nullptr;
