@@ -16,14 +16,20 @@ The JSON line also carries:
   (oracle/eager.py, run_study.py:304-335) on a bounded sample of the same workload;
 * ``sweep``: the C3 sequence sweep S in {512..8192} (bf16), as before;
 * ``blocks``: every other BASELINE.json configuration, each timed the same way (TFLOP/s,
-  share of peak, algorithmic HBM GB/s, mean and p95 per call): C2, the C3 sweep in fp16, the
-  C4 tile x accumulation sweep (fp16/bf16, D 64/128), C5 and its outlier variant C5b.
+  share of peak, algorithmic HBM GB/s, mean and p95 per call, the kernel the library
+  launches): C2, the C4 tile x accumulation sweep (fp16/bf16, D 64/128), C5 and its outlier
+  variant C5b; ``grid``, the metric's curves: B1 H8, S in {512..8192}, fp16 and bf16, causal
+  and not, D 64 and 128, each point beside the reference's own GB10 number
+  (benchmark-gb10/results/benchmark_results.csv, line cited per point); ``ceiling``, what
+  bounds the headline on the same box in the same run: hipBLASLt's bf16 GEMM (torch.matmul,
+  8192^3) and the headline workload on inputs whose mantissas are cleared (same
+  instructions and memory traffic, least multiplier activity).
 
 Inputs are generated on the CPU from a seeded ``torch.Generator`` (q, k, v drawn in that
 order, as run_study.py:526-529 does) and copied to the GPU before any timing.
 
 Usage: ``python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-[--no-sweep] [--no-blocks]``.
+[--no-sweep] [--no-blocks] [--only-block NAME]``.
 """
 
 from __future__ import annotations
@@ -44,6 +50,32 @@ if str(ROOT) not in sys.path:
 PEAK_TFLOPS = 2516.6  # dense fp16/bf16 MFMA, MI355X: 256 CU * 4096 FLOP/clk * 2.4 GHz
 REFERENCE_GB10_C3_S8192 = 60.87  # benchmark-gb10/results/benchmark_results.csv:548, TFLOP/s
 C4_TILES = ((64, 64), (64, 128), (128, 64), (128, 128))
+GRID_S = (512, 1024, 2048, 4096, 8192)
+
+# The reference's TFLOP/s on GB10 for its B1 H8 grid (method "tiledattention"), keyed by
+# (dtype, causal, S, D): (line of benchmark-gb10/results/benchmark_results.csv, TFLOP/s).
+REFERENCE_GB10_GRID = {
+    ("float16", False, 512, 64): (2, 15.197), ("float16", False, 512, 128): (16, 24.123),
+    ("float16", False, 1024, 64): (30, 34.222), ("float16", False, 1024, 128): (44, 46.929),
+    ("float16", False, 2048, 64): (58, 48.115), ("float16", False, 2048, 128): (72, 60.241),
+    ("float16", False, 4096, 64): (86, 58.803), ("float16", False, 4096, 128): (100, 70.232),
+    ("float16", False, 8192, 64): (114, 61.928), ("float16", False, 8192, 128): (128, 71.119),
+    ("bfloat16", False, 512, 64): (142, 15.636), ("bfloat16", False, 512, 128): (156, 23.334),
+    ("bfloat16", False, 1024, 64): (170, 35.209), ("bfloat16", False, 1024, 128): (184, 44.311),
+    ("bfloat16", False, 2048, 64): (198, 48.586), ("bfloat16", False, 2048, 128): (212, 57.796),
+    ("bfloat16", False, 4096, 64): (226, 59.020), ("bfloat16", False, 4096, 128): (240, 67.056),
+    ("bfloat16", False, 8192, 64): (254, 61.970), ("bfloat16", False, 8192, 128): (268, 68.317),
+    ("float16", True, 512, 64): (282, 8.904), ("float16", True, 512, 128): (296, 15.240),
+    ("float16", True, 1024, 64): (310, 21.641), ("float16", True, 1024, 128): (324, 32.420),
+    ("float16", True, 2048, 64): (338, 37.218), ("float16", True, 2048, 128): (352, 50.012),
+    ("float16", True, 4096, 64): (366, 48.166), ("float16", True, 4096, 128): (380, 61.523),
+    ("float16", True, 8192, 64): (394, 53.977), ("float16", True, 8192, 128): (408, 63.994),
+    ("bfloat16", True, 512, 64): (422, 8.894), ("bfloat16", True, 512, 128): (436, 15.158),
+    ("bfloat16", True, 1024, 64): (450, 21.097), ("bfloat16", True, 1024, 128): (464, 31.186),
+    ("bfloat16", True, 2048, 64): (478, 36.040), ("bfloat16", True, 2048, 128): (492, 47.805),
+    ("bfloat16", True, 4096, 64): (506, 47.052), ("bfloat16", True, 4096, 128): (520, 58.014),
+    ("bfloat16", True, 8192, 64): (534, 52.394), ("bfloat16", True, 8192, 128): (548, 60.875),
+}
 
 
 def _args():
@@ -199,6 +231,24 @@ class _Env:
                 os.environ[k] = v
 
 
+def _kernel_of(q, k, v, causal: bool) -> str:
+    """The attention kernel the library launches for this call (``ta_describe_launch``)."""
+    from tiledattention.kernels import flash_fwd
+
+    return flash_fwd.describe_call(q, k, v, causal=causal).get("kernel", "")
+
+
+def clear_mantissa(t, keep_bits: int = 0):
+    """``t`` (fp16/bf16) with all but the top ``keep_bits`` mantissa bits cleared: the same
+    exponents and signs, so the same softmax ranges, with less multiplier activity."""
+    import torch
+
+    man = 7 if t.dtype == torch.bfloat16 else 10
+    mask = (0xFFFF << (man - keep_bits)) & 0xFFFF
+    bits = t.view(torch.int16).to(torch.int32) & mask
+    return bits.to(torch.int16).view(t.dtype)
+
+
 def run_blocks(dev, only: str = "") -> dict:
     """Every BASELINE.json configuration beside the headline, timed like the sweep."""
     import torch
@@ -210,17 +260,19 @@ def run_blocks(dev, only: str = "") -> dict:
     def want(name):
         return name.startswith(only) if only else True
 
-    def one(name, shape, dtype, causal, seed, env=None, **input_kw):
+    def one(name, shape, dtype, causal, seed, env=None, quiet=False, **input_kw):
         b, h, s, d = shape
         q, k, v = (t.to(dev) for t in make_inputs(shape, dtype, seed, **input_kw))
         with _Env(**(env or {})):
             fn = lambda: sdpa(q, k, v, causal=causal)  # noqa: E731
             rec = measure(fn, flops=flops_of(b, h, s, d, causal), nbytes=alg_bytes(b, h, s, d))
+            rec["kernel"] = _kernel_of(q, k, v, causal)
         rec.update({"B": b, "H": h, "S": s, "D": d, "dtype": dtype, "causal": causal, "seed": seed})
         if env:
             rec["knobs"] = {("TILEDATTN_" + k.upper()): v for k, v in env.items()}
-        _log(f"block {name}: {rec['tflops']} TFLOP/s ({rec['frac_peak']:.1%}), "
-             f"{rec['hbm_gbps_alg']} GB/s alg, p95 {rec['p95_ms']} ms")
+        if not quiet:
+            _log(f"block {name}: {rec['tflops']} TFLOP/s ({rec['frac_peak']:.1%}), "
+                 f"{rec['hbm_gbps_alg']} GB/s alg, p95 {rec['p95_ms']} ms, {rec['kernel']}")
         del q, k, v
         torch.cuda.empty_cache()
         return rec
@@ -229,9 +281,27 @@ def run_blocks(dev, only: str = "") -> dict:
         # C2: B1 H8 S1024 D64 fp16 non-causal, tile 64x64, fp32 accumulation (aligned fast path)
         blocks["C2"] = one("C2", (1, 8, 1024, 64), "float16", False, 2026,
                            env={"tile_m": 64, "tile_n": 64, "accum_mode": "fp32"})
-    if want("C3_fp16"):
-        blocks["C3_fp16"] = {str(s): one(f"C3_fp16 S={s}", (1, 8, s, 128), "float16", True, 1234)
-                             for s in (512, 1024, 2048, 4096, 8192)}
+    if want("grid"):
+        # The metric's curves (TFLOP/s vs S for fp16/bf16, D 64/128, causal and not) at the
+        # reference's B1 H8 grid, seed 1234, default knobs, each beside the reference's point.
+        grid = {}
+        for dtype in ("float16", "bfloat16"):
+            for causal in (False, True):
+                for d in (64, 128):
+                    curve = {}
+                    for s_ in GRID_S:
+                        rec = one("grid", (1, 8, s_, d), dtype, causal, 1234, quiet=True)
+                        line_no, ref = REFERENCE_GB10_GRID[(dtype, causal, s_, d)]
+                        rec["reference_gb10_tflops"] = ref
+                        rec["reference_csv_line"] = line_no
+                        rec["vs_reference"] = round(rec["tflops"] / ref, 2)
+                        curve[str(s_)] = rec
+                    key = f"{'fp16' if dtype == 'float16' else 'bf16'}_{'causal' if causal else 'noncausal'}_d{d}"
+                    grid[key] = curve
+                    _log(f"block grid {key}: " + ", ".join(
+                        f"S={s_} {curve[str(s_)]['tflops']} ({curve[str(s_)]['frac_peak']:.1%}; ref "
+                        f"{curve[str(s_)]['reference_gb10_tflops']})" for s_ in GRID_S))
+        blocks["grid"] = grid
     if want("C4"):
         # C4: B4 H16 S4096 non-causal, inputs N(0,1)*0.5 seed 2026; every tile, both
         # accumulation modes; plus the default configuration (no knobs).
@@ -250,17 +320,66 @@ def run_blocks(dev, only: str = "") -> dict:
                             fn = lambda: sdpa(q, k, v, causal=False)  # noqa: E731
                             rec = measure(fn, flops=flops_of(*shape, False), nbytes=alg_bytes(*shape),
                                           hot_s=0.1, regions=3, per_region=10, calls=20)
+                            rec["kernel"] = _kernel_of(q, k, v, False)
                         rec.update({"knobs": {("TILEDATTN_" + k_.upper()): v_ for k_, v_ in env.items()}})
                         c4[key] = rec
-                        _log(f"block C4 {key}: {rec['tflops']} TFLOP/s ({rec['frac_peak']:.1%})")
+                        _log(f"block C4 {key}: {rec['tflops']} TFLOP/s ({rec['frac_peak']:.1%}) {rec['kernel']}")
                 del q, k, v
                 torch.cuda.empty_cache()
+        for key, rec in c4.items():
+            if not key.endswith("default"):
+                rec["vs_default"] = round(rec["tflops"] / c4[key.rsplit("_", 2)[0] + "_default"]["tflops"], 3)
         blocks["C4"] = c4
     if want("C5"):
         blocks["C5"] = one("C5", (1, 8, 16384, 128), "float16", True, 1234)
         blocks["C5b"] = one("C5b", (1, 8, 16384, 128), "float16", True, 1234,
                             outlier_frac=0.01, outlier_gain=20.0, outlier_seed=1235)
+    if want("ceiling"):
+        blocks["ceiling"] = run_ceiling(dev)
     return blocks
+
+
+def run_ceiling(dev) -> dict:
+    """The headline kernel beside what bounds it, on the same box in the same run.
+
+    * hipBLASLt's bf16 GEMM through torch.matmul, M = N = K = 8192 (and 16384): dense MFMA
+      work with no softmax, the library's best rate on this part at this moment;
+    * the headline workload (C3 S=8192 bf16 causal) on its own inputs, and on the same
+      inputs with every mantissa bit cleared (and with 3 of bf16's 7 kept): the same
+      kernel, instructions and memory traffic, only the operands' bit activity differs, so
+      a rate that rises as bits are cleared is set by power (the clock the part holds),
+      not by the schedule."""
+    import torch
+
+    from tiledattention import sdpa
+
+    out: dict = {}
+    for n in (8192, 16384):
+        g = torch.Generator(device="cpu").manual_seed(7)
+        a = torch.randn((n, n), generator=g, dtype=torch.float32).to(torch.bfloat16).to(dev)
+        b_ = torch.randn((n, n), generator=g, dtype=torch.float32).to(torch.bfloat16).to(dev)
+        c = torch.empty((n, n), dtype=torch.bfloat16, device=dev)
+        fn = lambda: torch.matmul(a, b_, out=c)  # noqa: E731
+        rec = measure(fn, flops=2.0 * n ** 3, nbytes=3.0 * n * n * 2, hot_s=0.5, regions=5,
+                      per_region=5 if n == 8192 else 2, calls=10)
+        out[f"gemm_bf16_{n}"] = rec
+        _log(f"ceiling gemm bf16 {n}^3: {rec['tflops']} TFLOP/s ({rec['frac_peak']:.1%})")
+        del a, b_, c
+        torch.cuda.empty_cache()
+    shape, causal = (1, 8, 8192, 128), True
+    q, k, v = (t.to(dev) for t in make_inputs(shape, "bfloat16", 1234))
+    flops = flops_of(*shape, causal)
+    for label, keep in (("attention_c3_s8192", None), ("attention_c3_s8192_mantissa3", 3),
+                        ("attention_c3_s8192_mantissa0", 0)):
+        qi, ki, vi = (q, k, v) if keep is None else (clear_mantissa(t, keep) for t in (q, k, v))
+        fn = lambda: sdpa(qi, ki, vi, causal=causal)  # noqa: E731
+        rec = measure(fn, flops=flops, nbytes=alg_bytes(*shape), hot_s=0.5)
+        rec["kernel"] = _kernel_of(qi, ki, vi, causal)
+        out[label] = rec
+        _log(f"ceiling {label}: {rec['tflops']} TFLOP/s ({rec['frac_peak']:.1%}) {rec['kernel']}")
+    out["attention_vs_gemm_8192"] = round(out["attention_c3_s8192"]["tflops"] / out["gemm_bf16_8192"]["tflops"], 4)
+    out["attention_vs_gemm_16384"] = round(out["attention_c3_s8192"]["tflops"] / out["gemm_bf16_16384"]["tflops"], 4)
+    return out
 
 
 def _cpu_model() -> str:
@@ -326,7 +445,7 @@ def main() -> int:
 
     import torch
 
-    from tiledattention import _lib, sdpa
+    from tiledattention import sdpa
     from tiledattention.kernels import flash_fwd
 
     dev = torch.device("cuda:0")
@@ -352,19 +471,11 @@ def main() -> int:
     _log(f"ms/step {ms_step:.4f}  kernel mean {kern_ms:.4f} ms  "
          f"{value:.1f} TFLOP/s  kernel {achieved:.1f} TFLOP/s ({achieved / PEAK_TFLOPS:.1%} of peak)")
 
-    # The kernel this configuration launches (the C ABI's choice, mirrored in _lib); the
-    # committed HBM-traffic figure is used only if it was measured on that kernel.
-    tm, tn = flash_fwd._default_tile_config_for_shape_gfx950(seq_len=s, head_dim=d, causal=causal,
-                                                             n_bh=b * h)
-    n_qblk = (s + tm - 1) // tm
-    sched = flash_fwd._resolve_sched(n_blocks=b * h * n_qblk, causal=causal, tile_m=tm, tile_n=tn,
-                                     head_dim=d)
-    pair = _lib.uses_pairs(causal=causal, head_dim=d, tile_m=tm, tile_n=tn, accum=_lib.TA_ACC_FP32,
-                           n_bh=b * h, n_qblk=n_qblk, sched=sched,
-                           compute_units=torch.cuda.get_device_properties(dev).multi_processor_count)
-    tail = _lib.tail_masked(seq_len=s, tile_m=tm, tile_n=tn, accum=_lib.TA_ACC_FP32, head_dim=d)
-    _, kernel = _lib.kernel_symbol(dtype=_lib.TA_BF16, head_dim=d, tile_m=tm, tile_n=tn,
-                                   causal=causal, tail=tail, accum=_lib.TA_ACC_FP32, pair=pair)
+    # The kernel this configuration launches, as the library reports it; the committed
+    # HBM-traffic figure is used only if it was measured on that kernel.
+    desc = flash_fwd.describe_call(q, k, v, causal=causal)
+    kernel = desc["kernel"]
+    _log(f"headline kernel {kernel}: grid {desc['grid']} x {desc['block']}, layout {desc['layout']}")
     traffic = None
     tp = Path(args.traffic_json)
     if tp.exists():
@@ -381,6 +492,7 @@ def main() -> int:
             qs, ks, vs = (t.to(dev) for t in make_inputs((1, 8, ss, 128), dtype, seed))
             fn_s = lambda: sdpa(qs, ks, vs, causal=True)  # noqa: E731
             sweep[str(ss)] = measure(fn_s, flops=flops_of(1, 8, ss, 128, True), nbytes=alg_bytes(1, 8, ss, 128))
+            sweep[str(ss)]["kernel"] = _kernel_of(qs, ks, vs, True)
             _log(f"sweep S={ss}: {sweep[str(ss)]}")
             del qs, ks, vs
 
@@ -402,7 +514,7 @@ def main() -> int:
         "config": {
             "workload": f"C3: sdpa fwd B={b} H={h} S={s} D={d} bf16 causal, seed {seed}",
             "B": b, "H": h, "S": s, "D": d, "causal": causal,
-            "tile_m": tm, "tile_n": tn, "accum": "fp32", "kernel": kernel,
+            "accum": "fp32", "kernel": kernel, "launch": desc,
             "flops_per_step": flops,
             "reference_value_gb10": REFERENCE_GB10_C3_S8192 if s == 8192 else None,
         },

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define TA_ABI_VERSION 3
+#define TA_ABI_VERSION 4
 
 typedef enum ta_status {
   TA_OK = 0,
@@ -166,10 +166,61 @@ ta_status ta_sdpa_fwd_split(const ta_fwd_args* args, int32_t chunk_steps, void* 
  * hipMalloc (code under HIP graph capture, tight serving loops, harnesses that forbid
  * allocation).  Same arguments, kernels and result as ta_sdpa_fwd_split; a chunk length
  * whose workspace (ta_split_workspace_size) exceeds TA_STATIC_SCRATCH_BYTES is rejected
- * with TA_EINVAL.  Every call on one GPU shares that GPU's array: calls whose work overlaps
- * on the same GPU (other streams, other threads) race on it and must be serialized by the
- * caller. */
+ * with TA_EINVAL, and a chunk length that splits nothing runs ta_sdpa_fwd (no scratch).
+ * Every call on one GPU shares that GPU's array: calls whose work overlaps on the same GPU
+ * (other streams, other threads) race on it and must be serialized by the caller.  The
+ * first call on a device resolves the array's address there (hipGetSymbolAddress, which
+ * loads the library's device code on that device) and loads the code object of its
+ * kernels: make one call on each device before capturing a graph or entering code that must
+ * not allocate; later calls allocate nothing. */
 ta_status ta_sdpa_fwd_split_static(const ta_fwd_args* args, int32_t chunk_steps, void* stream);
+
+/* How a forward's work is laid out over workgroups (ta_launch_desc.layout). */
+typedef enum ta_layout {
+  TA_LAYOUT_WHOLE_ROWS = 0,   /* one workgroup per query block of `rows` rows */
+  TA_LAYOUT_PAIRS = 1,        /* causal query blocks nq - 1 - j and j on one workgroup */
+  TA_LAYOUT_ROWS256 = 2,      /* non-causal 256-row blocks (the two wave groups own
+                                 different rows) */
+  TA_LAYOUT_SPLIT = 3,        /* chunks of key steps, merged by a second kernel */
+  TA_LAYOUT_PAIRED_SPLIT = 4  /* the paired split (TA_SPLIT_PAIRS), merged likewise */
+} ta_layout;
+
+/* What one forward enqueues: the kernels, their grids and code object, and the decisions
+ * behind them.  Filled by ta_describe_launch from the same planning step the launch entry
+ * points run, so a description and the launch it describes cannot differ. */
+typedef struct ta_launch_desc {
+  char code_object[64];   /* file of the kernels ("" when nothing is launched) */
+  char kernel[96];        /* the attention kernel's symbol */
+  int64_t grid;           /* its workgroups (0: zero-size problem, nothing launched) */
+  int32_t block;          /* its threads per workgroup */
+  int32_t rows;           /* query rows per query block it processes (64, 128 or 256) */
+  int32_t tail;           /* 1: the tail-masked variant */
+  int32_t layout;         /* ta_layout */
+  int32_t chunk_steps;    /* the split that runs: 0 whole rows, > 0 chunk length, or
+                             TA_SPLIT_PAIRS */
+  int32_t compute_units;  /* compute units the decision was made for */
+  char merge_kernel[96];  /* the merge kernel of a split ("" when none) */
+  int64_t merge_grid;
+  int32_t merge_block;
+  int32_t in_place_pad;   /* 1: the kernel family reads d_real < D in place (eight-wave) */
+  int32_t split_capable;  /* 1: split kernels exist for this configuration */
+  int32_t reserved;
+  int64_t workspace_bytes; /* workspace ta_sdpa_fwd_split needs for chunk_steps (0 if none) */
+} ta_launch_desc;
+
+/* Describe what ta_sdpa_fwd (chunk_steps = 0) or ta_sdpa_fwd_split (chunk_steps != 0)
+ * would enqueue for `args` on its device, without launching anything.  No counterpart in
+ * the reference, whose single kernel is fixed by its tile knobs (flash_fwd.py:895-952):
+ * here the pairs, 256-row and split layouts are chosen from the grid size and the
+ * device's compute units, and callers that label or model launches (benchmarks,
+ * profilers, schedulers) read the choice from the library instead of restating its rules.
+ * Reads the shape, dtype, tile, accum, causal, sched, aligned, d_real and device fields
+ * (tensor pointers and strides may be unset). */
+ta_status ta_describe_launch(const ta_fwd_args* args, int32_t chunk_steps, ta_launch_desc* out);
+
+/* ta_describe_launch for a device with `compute_units` CUs, without touching a device. */
+ta_status ta_describe_launch_model(const ta_fwd_args* args, int32_t chunk_steps,
+                                   int32_t compute_units, ta_launch_desc* out);
 
 /* Unload every cached module on every device (compile_cache.reset_cache_for_tests). */
 ta_status ta_cache_reset(void);

@@ -73,8 +73,16 @@ def oracle_f32(q, k, v, *, causal, scale=None, rows=None):
 
 
 def as_f32(out, rows=None):
+    """The output as fp32 numpy, optionally only the query rows `rows`.
+
+    With `rows`, every element of the whole output is first checked for finiteness on its
+    own device, so a NaN or inf outside the sampled rows still fails the test (the values
+    of unsampled rows are not compared with the oracle, their finiteness is)."""
     import torch
 
+    if rows is not None:
+        bad = int((~torch.isfinite(out.detach())).sum())
+        assert bad == 0, f"{bad} non-finite output elements (the whole output is checked)"
     o = out.detach().to("cpu", torch.float32)
     if rows is not None:
         o = o[:, :, torch.as_tensor(rows, dtype=torch.long), :]

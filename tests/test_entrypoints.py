@@ -48,3 +48,48 @@ def test_bench_workload_inputs_and_counts_match_the_oracle_helpers():
     vals = [0.1 * i for i in range(1, 60)]
     assert bench.p95(vals) == O.p95(vals)
     assert bench.flops_of(1, 8, 8192, 128, True) == 137438953472.0  # 2*B*H*S^2*D
+
+
+def test_bench_mantissa_clearing_keeps_sign_and_exponent():
+    """The ceiling block's operands: every value keeps its sign and exponent and only the
+    top ``keep_bits`` mantissa bits; bf16 with none kept is +-2^e exactly (truncation
+    toward zero, |x'| <= |x| < 2|x'|)."""
+    import torch
+
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(4096, generator=g)
+    for dtype, man in ((torch.bfloat16, 7), (torch.float16, 10)):
+        t = x.to(dtype)
+        for keep in (0, 3):
+            y = bench.clear_mantissa(t, keep)
+            assert y.dtype == dtype
+            tb = t.view(torch.int16).to(torch.int32) & 0xFFFF
+            yb = y.view(torch.int16).to(torch.int32) & 0xFFFF
+            low = (1 << (man - keep)) - 1
+            assert torch.equal(yb & low, torch.zeros_like(yb))
+            assert torch.equal(yb, tb & (0xFFFF ^ low))
+            tf, yf = t.float().abs(), y.float().abs()
+            nz = tf > 0
+            assert (yf <= tf).all() and (tf[nz] < 2 * yf[nz]).all()
+            assert torch.equal(torch.sign(t.float()), torch.sign(y.float()))
+        y0 = bench.clear_mantissa(t, 0).float().abs()
+        nz = y0 > 0
+        assert torch.equal(torch.exp2(torch.log2(y0[nz]).round()), y0[nz])  # powers of two
+
+
+def test_bench_reference_grid_covers_the_metric():
+    """The grid block's reference points: every (dtype, causal, S, D) of the metric at the
+    reference's B1 H8 grid, the headline point equal to the line the bench compares with."""
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    keys = {(dt, c, s, d) for dt in ("float16", "bfloat16") for c in (False, True)
+            for s in bench.GRID_S for d in (64, 128)}
+    assert set(bench.REFERENCE_GB10_GRID) == keys
+    line_no, ref = bench.REFERENCE_GB10_GRID[("bfloat16", True, 8192, 128)]
+    assert line_no == 548 and abs(ref - bench.REFERENCE_GB10_C3_S8192) < 0.01
+    lines = [v[0] for v in bench.REFERENCE_GB10_GRID.values()]
+    assert len(set(lines)) == len(lines)

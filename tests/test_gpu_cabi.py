@@ -74,3 +74,28 @@ def test_cabi_bad_device_is_a_hip_error(gpu):
     x = torch.ones(4, device="cuda") * 2
     torch.cuda.synchronize()
     assert float(x.sum()) == 8.0
+
+
+def test_describe_launch_on_the_device(gpu):
+    """ta_describe_launch on the device equals the model at the device's CU count, and the
+    Python layer's description of a call names the same kernel (the headline workload:
+    causal pairs at 256 CUs)."""
+    import torch
+
+    from tiledattention.kernels import flash_fwd
+
+    lib = _lib.load()
+    cu = torch.cuda.get_device_properties(0).multi_processor_count
+    say(f"C-ABI ta_describe_launch on device 0 ({cu} CUs)")
+    for kw in (dict(B=1, H=8, S=8192, D=128, causal=True, sched=1),
+               dict(B=4, H=16, S=4096, D=128, causal=False, sched=1),
+               dict(B=1, H=8, S=512, D=128, causal=True, tile_m=64)):
+        args = _lib.shape_args(**kw)
+        on_dev = _lib.describe(lib, args).as_dict()
+        model = _lib.describe(lib, args, compute_units=cu).as_dict()
+        assert on_dev == model and on_dev["compute_units"] == cu
+    q, k, v = inputs((1, 8, 8192, 128), "bfloat16", 1234)
+    qd, kd, vd = (t.cuda() for t in (q, k, v))
+    desc = flash_fwd.describe_call(qd, kd, vd, causal=True)
+    expect = "ta_fwd_pp_pair_bf16_d128_c1_t0" if cu <= 256 else "ta_fwd_pp_bf16_d128_c1_t0"
+    assert desc["kernel"] == expect and desc["code_object"] == "attn_fwd_pp.hsaco"

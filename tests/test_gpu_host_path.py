@@ -44,7 +44,8 @@ def test_knob_changes_between_calls_take_effect(gpu):
     # this grid (2 x 6 blocks of 64 rows, fewer than the CUs) is (64,64) too
     assert seen == [1, 2, 2, 2], seen
     from tiledattention.kernels import flash_fwd as ff
-    assert ff._default_tile_config_for_shape_gfx950(seq_len=384, head_dim=64, causal=True, n_bh=2) == (64, 64)
+    assert ff._default_tile_config_for_shape_gfx950(seq_len=384, head_dim=64, causal=True, n_bh=2,
+                                                    compute_units=256) == (64, 64)
     say("host path: invalid sync mode raises on every call")
     for _ in range(2):
         with knobs(sync_mode="sometimes"), pytest.raises(ValueError, match="TILEDATTN_SYNC_MODE"):

@@ -94,6 +94,26 @@ def test_c3_bf16_causal_d128(gpu, s):
             check_close(as_f32(out), ref, "bfloat16", what=f"C3 S={s} tiles={tm},{tn}")
 
 
+@pytest.mark.parametrize("dtype,causal,d,s", [
+    ("float16", False, 128, 8192),   # the reference's headline curve (benchmark_results.csv:128)
+    ("float16", False, 128, 2048),
+    ("bfloat16", False, 128, 8192),
+    ("float16", False, 64, 8192), ("bfloat16", False, 64, 8192),
+    ("float16", True, 64, 8192), ("bfloat16", True, 64, 8192),
+    ("float16", False, 64, 1024), ("bfloat16", True, 64, 2048),
+])
+def test_metric_grid_b1_h8(gpu, dtype, causal, d, s):
+    """The bench's grid workloads (B1 H8, seed 1234, default knobs): the metric's other
+    curves, non-causal D = 128 and D = 64 both ways, against the oracle (sampled rows for
+    S >= 4096, with every output element checked for finiteness)."""
+    q, k, v = inputs((1, 8, s, d), dtype, 1234)
+    rows = None if s <= 2048 else sample_rows(s, 128)
+    ref = oracle_f32(q, k, v, causal=causal, rows=rows)
+    say(f"grid {dtype} causal={causal} (1,8,{s},{d}) seed=1234 rows={'all' if rows is None else len(rows)}")
+    out = run_gpu(q, k, v, causal=causal)
+    check_close(as_f32(out, rows), ref, dtype, what=f"grid {dtype} causal={causal} S={s} D={d}")
+
+
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 @pytest.mark.parametrize("d", [64, 128])
 def test_c4_noncausal_tile_sweep(gpu, dtype, d):

@@ -126,9 +126,8 @@ def test_gfx950_native_96_head_dim(d, expected):
     assert ff._resolve_kernel_head_dim_gfx950(d, native_96=True) == expected
     if 64 < d <= 96:
         assert ff._resolve_kernel_head_dim_gfx950(d) == (128, 128 - d)
-        sym = _lib.kernel_symbol(dtype=_lib.TA_BF16, head_dim=96, tile_m=128, tile_n=64, causal=True,
-                                 tail=False, accum=_lib.TA_ACC_FP32)
-        assert sym == ("attn_fwd_pp.hsaco", "ta_fwd_pp_bf16_d96_c1_t0")
+        desc = _lib.describe(_lib.load(), _lib.shape_args(S=512, D=96, causal=True), 0, compute_units=256)
+        assert (desc.code_object, desc.kernel) == (b"attn_fwd_pp.hsaco", b"ta_fwd_pp_bf16_d96_c1_t0")
 
 
 @pytest.mark.parametrize("d", [0, -1, 257, 512])
@@ -249,18 +248,18 @@ def test_sched_default(n, causal, tiles, accum, d, expected):
                                      head_dim=d, causal=False) == (2 if tiles == (128, 64) and d <= 64 else 1)
     code = _lib.TA_ACC_FP32 if accum == "fp32" else _lib.TA_ACC_INPUT
     assert ff._resolve_sched(n_blocks=n, causal=causal, tile_m=tiles[0], tile_n=tiles[1],
-                             accum_code=code, head_dim=d) == expected
+                             accum_code=code, head_dim=d, compute_units=256) == expected
 
 
 def test_sched_env(monkeypatch):
     monkeypatch.setenv("TILEDATTN_SCHED", "0")
-    assert ff._resolve_sched(n_blocks=512, causal=True, tile_m=128, tile_n=64) == 0
+    assert ff._resolve_sched(n_blocks=512, causal=True, tile_m=128, tile_n=64, compute_units=256) == 0
     monkeypatch.setenv("TILEDATTN_SCHED", "3")
-    assert ff._resolve_sched(n_blocks=512, causal=True, tile_m=128, tile_n=64) == 3
+    assert ff._resolve_sched(n_blocks=512, causal=True, tile_m=128, tile_n=64, compute_units=256) == 3
     for bad in ("4", "-1", "x"):
         monkeypatch.setenv("TILEDATTN_SCHED", bad)
         with pytest.raises(ValueError, match="TILEDATTN_SCHED"):
-            ff._resolve_sched(n_blocks=512, causal=True, tile_m=128, tile_n=64)
+            ff._resolve_sched(n_blocks=512, causal=True, tile_m=128, tile_n=64, compute_units=256)
 
 
 # ---------------------------------------------------------------- default tile on gfx950
@@ -283,7 +282,7 @@ def test_sched_env(monkeypatch):
 ])
 def test_default_tile_prefers_64_rows_when_one_wave_of_blocks_fits(s, d, n_bh, accum, expected):
     assert ff._default_tile_config_for_shape_gfx950(seq_len=s, head_dim=d, causal=True, n_bh=n_bh,
-                                                    accum_mode=accum) == expected
+                                                    accum_mode=accum, compute_units=256) == expected
 
 
 @pytest.mark.parametrize("s,d,causal,n_bh,expected", [
@@ -300,30 +299,20 @@ def test_default_tile_n_follows_the_reference_rule(s, d, causal, n_bh, expected)
     rounding cadence of input-dtype accumulation matches the reference's default."""
     for accum in ("fp32", "fp16"):
         assert ff._default_tile_config_for_shape_gfx950(seq_len=s, head_dim=d, causal=causal, n_bh=n_bh,
-                                                        accum_mode=accum) == expected
+                                                        accum_mode=accum, compute_units=256) == expected
 
 
-def test_64_row_tiles_select_the_eight_wave_kernel():
-    """Tiles (64, 64) / (64, 128) with fp32 accumulation at D = 64, 96, 128 and 160 run
-    ta_fwd_pp64_*; the tail-masked variant whenever S is not a multiple of the 128-key step."""
-    f, sym = _lib.kernel_symbol(dtype=_lib.TA_BF16, head_dim=128, tile_m=64, tile_n=128, causal=True,
-                                tail=False, accum=_lib.TA_ACC_FP32)
-    assert (f, sym) == ("attn_fwd_pp.hsaco", "ta_fwd_pp64_bf16_d128_c1_t0")
-    assert _lib.kernel_symbol(dtype=_lib.TA_FP16, head_dim=64, tile_m=64, tile_n=64, causal=False,
-                              tail=True, accum=_lib.TA_ACC_FP32)[1] == "ta_fwd_pp64_f16_d64_c0_t1"
-    assert _lib.kernel_symbol(dtype=_lib.TA_FP16, head_dim=64, tile_m=64, tile_n=64, causal=False,
-                              tail=True, accum=_lib.TA_ACC_INPUT)[1] == "ta_fwd_ppl64_n64_f16_d64_c0_t1"
-    assert _lib.kernel_symbol(dtype=_lib.TA_FP16, head_dim=128, tile_m=128, tile_n=128, causal=True,
-                              tail=False, accum=_lib.TA_ACC_INPUT)[1] == "ta_fwd_ppl_n128_f16_d128_c1_t0"
-    assert _lib.kernel_symbol(dtype=_lib.TA_FP16, head_dim=160, tile_m=128, tile_n=64, causal=True,
-                              tail=False, accum=_lib.TA_ACC_INPUT)[1].startswith("ta_fwd_f16_d160_m128_n64")
-    assert _lib.kernel_symbol(dtype=_lib.TA_FP16, head_dim=160, tile_m=64, tile_n=64, causal=False,
-                              tail=True, accum=_lib.TA_ACC_FP32)[1] == "ta_fwd_pp64_f16_d160_c0_t1"
-    assert _lib.kernel_symbol(dtype=_lib.TA_FP16, head_dim=160, tile_m=64, tile_n=64, causal=False,
-                              tail=True, accum=_lib.TA_ACC_INPUT)[1].startswith("ta_fwd_f16_d160_m64_n64")
-    tm = dict(tile_m=64, tile_n=64, accum=_lib.TA_ACC_FP32, head_dim=128)
-    assert not _lib.tail_masked(seq_len=512, **tm)
-    assert _lib.tail_masked(seq_len=320, **tm)   # multiple of 64, not of the 128-key step
-    assert _lib.tail_masked(seq_len=512, aligned=False, **tm)
-    four = dict(tile_m=64, tile_n=64, accum=_lib.TA_ACC_INPUT, head_dim=160)
-    assert not _lib.tail_masked(seq_len=320, **four)  # four-wave kernels step by the tile
+
+
+# ---------------------------------------------------------------- split preference and accumulation
+def test_split_preference_needs_fp32_accumulation(monkeypatch):
+    """Split kernels exist for fp32 accumulation only: a long, narrow causal grid that the
+    fp32 planner splits (B1 H1 S16384 D128) keeps the 64-row default under input-dtype
+    accumulation instead of moving to 128 rows it could not split."""
+    lib = _lib.load()
+    assert lib.ta_split_plan_model(16384, 1, 1, 256) != 0
+    monkeypatch.delenv("TILEDATTN_SPLIT", raising=False)
+    assert ff._split_preferred(lib, None, 1, 1, 16384, 128, True, None, "fp16") is False
+    monkeypatch.setenv("TILEDATTN_SPLIT", "4")  # forced: fp32 prefers the split tile
+    assert ff._split_preferred(lib, None, 1, 1, 16384, 128, True, None, "fp32") is True
+    assert ff._split_preferred(lib, None, 1, 1, 16384, 128, True, None, "fp16") is False

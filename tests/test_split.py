@@ -148,9 +148,9 @@ def test_split_knob_pairs(monkeypatch, lib):
     monkeypatch.setenv("TILEDATTN_SPLIT", "pair")
     with pytest.raises(ValueError, match="'pairs'"):
         flash_fwd._resolve_split(lib, a, capable=True)
-    assert _lib.kernel_symbol(dtype=_lib.TA_BF16, head_dim=128, tile_m=128, tile_n=64, causal=True,
-                              tail=False, accum=_lib.TA_ACC_FP32, split=True, pair=True) == (
-        "attn_fwd_pp.hsaco", "ta_fwd_pp_psplit_bf16_d128_c1_t0")
+    desc = _lib.describe(lib, _lib.shape_args(S=4096, H=8, causal=True), _lib.TA_SPLIT_PAIRS,
+                         compute_units=MI355X_CUS)
+    assert (desc.code_object, desc.kernel) == (b"attn_fwd_pp.hsaco", b"ta_fwd_pp_psplit_bf16_d128_c1_t0")
 
 
 def _plan(lib, S, n_bh, causal, cus=MI355X_CUS):
@@ -234,26 +234,6 @@ def test_split_capability_rule():
     assert ew(**ok) and ew(**{**ok, "tile_m": 64}) and ew(**{**ok, "tile_m": 64, "tile_n": 128})
     assert ew(**{**ok, "tile_m": 64, "kernel_head_dim": 160})
     assert not ew(**{**ok, "tile_m": 64, "kernel_head_dim": 256})
-    with pytest.raises(ValueError, match="D <= 160"):
-        _lib.kernel_symbol(dtype=_lib.TA_BF16, head_dim=256, tile_m=128, tile_n=64, causal=True,
-                           tail=False, accum=_lib.TA_ACC_FP32, split=True)
-
-
-def test_split_kernel_symbols_exist_in_code_object():
-    data = (_lib.lib_dir() / "attn_fwd_pp.hsaco").read_bytes()
-    for dtype, dt in ((_lib.TA_FP16, "f16"), (_lib.TA_BF16, "bf16")):
-        for d in (64, 128, 160):
-            for causal in (0, 1):
-                for tail in (0, 1):
-                    f, sym = _lib.kernel_symbol(dtype=dtype, head_dim=d, tile_m=128, tile_n=64,
-                                                causal=bool(causal), tail=bool(tail),
-                                                accum=_lib.TA_ACC_FP32, split=True)
-                    assert f == "attn_fwd_pp.hsaco"
-                    assert sym.encode() + b"\x00" in data, sym
-                assert f"ta_fwd_merge_{dt}_d{d}_c{causal}".encode() + b"\x00" in data
-    with pytest.raises(ValueError):
-        _lib.kernel_symbol(dtype=0, head_dim=128, tile_m=64, tile_n=64, causal=True, tail=False,
-                           accum=_lib.TA_ACC_FP32, split=True)
 
 
 # ---------------------------------------------------------------- launch-plan cache keys

@@ -59,6 +59,12 @@ def test_static_scratch_matches_caller_workspace(gpu, order):
         st = lib.ta_sdpa_fwd_split_static(ctypes.byref(b), chunk, ctypes.c_void_p(stream))
         assert st == _lib.TA_OK, _lib.last_error(lib)
         torch.cuda.synchronize()
+        # once warm, a call allocates no device memory: the free bytes do not move
+        free0 = torch.cuda.mem_get_info(dev)[0]
+        st = lib.ta_sdpa_fwd_split_static(ctypes.byref(b), chunk, ctypes.c_void_p(stream))
+        assert st == _lib.TA_OK, _lib.last_error(lib)
+        torch.cuda.synchronize()
+        assert torch.cuda.mem_get_info(dev)[0] == free0
         assert torch.equal(o_ws, o_st), float((o_ws.float() - o_st.float()).abs().max())
         check_close(as_f32(o_st), oracle_f32(q, k, v, causal=bool(causal)), dtype,
                     what=f"static scratch {shape}")
@@ -83,8 +89,11 @@ def test_static_scratch_whole_rows_and_oversize(gpu):
     torch.cuda.synchronize()
     assert torch.equal(o0, o1)
     check_close(as_f32(o1), oracle_f32(q, k, v, causal=True), "float16", what="static whole rows")
-    # B1 H64 S=16384 D=128, chunks of one step: ~4 GiB of partials, far above the array
+    # B1 H64 S=16384 D=128, chunks of one step: ~4 GiB of partials, far above the array.
+    # Null tensor pointers: were the size check ever skipped, validation would still reject
+    # the call before any launch.
     a = _args(qd, kd, vd, o1, causal=1, dtype_code=_lib.TA_FP16)
+    a.q = a.k = a.v = a.o = None
     a.H, a.S = 64, 16384
     for name in ("q_stride", "k_stride", "v_stride", "o_stride"):
         getattr(a, name)[:] = (64 * 16384 * 128, 16384 * 128, 128, 1)

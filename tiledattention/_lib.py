@@ -17,7 +17,7 @@ from threading import Lock
 
 from ._errors import DependencyError
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 TA_OK = 0
 TA_EINVAL = 1
@@ -35,79 +35,12 @@ TILE_SHAPES = ((64, 64), (64, 128), (128, 64), (128, 128))
 STATIC_SCRATCH_BYTES = 64 << 20  # TA_STATIC_SCRATCH_BYTES
 
 
-def uses_pairs(*, causal: bool, head_dim: int, tile_m: int, tile_n: int, accum: int, n_bh: int,
-               n_qblk: int, sched: int, compute_units: int) -> bool:
-    """Whether a whole-row launch runs causal query blocks in pairs; the same rule as
-    use_pairs() in csrc/tiledattn.cpp."""
-    if not causal or n_qblk < 2 or head_dim > 128:
-        return False
-    if not (tile_m == 128 and tile_n in (64, 128) and accum == TA_ACC_FP32):
-        return False
-    if sched == 3:
-        return True
-    return sched == 1 and n_bh * n_qblk >= 2 * compute_units
+TA_LAYOUT_WHOLE_ROWS = 0
+TA_LAYOUT_PAIRS = 1
+TA_LAYOUT_ROWS256 = 2
+TA_LAYOUT_SPLIT = 3
+TA_LAYOUT_PAIRED_SPLIT = 4
 
-
-def eight_wave_family(*, tile_m: int, tile_n: int, accum: int, head_dim: int) -> bool:
-    """The eight-wave kernels (attn_fwd_pp.hsaco): fp32 accumulation with tiles (128, 64) /
-    (128, 128) or (64, 64) / (64, 128) at D = 64, 96, 128 or 160; input-dtype
-    accumulation with any tile at D = 64 or 128.  The same rule as eight_wave_family() in
-    csrc/tiledattn.cpp."""
-    if tile_n not in (64, 128) or tile_m not in (64, 128):
-        return False
-    if accum != TA_ACC_FP32:  # input-dtype accumulation: ta_fwd_ppl_* / ta_fwd_ppl64_*
-        return head_dim in (64, 128)
-    return (tile_m == 128 and head_dim <= 160) or (tile_m == 64 and head_dim in (64, 96, 128, 160))
-
-
-def tail_masked(*, seq_len: int, tile_m: int, tile_n: int, accum: int, head_dim: int,
-                aligned: bool = True) -> bool:
-    """Whether the C ABI launches the tail-masked variant; unmasked_tail() in
-    csrc/tiledattn.cpp: S a multiple of both tiles (and of the 128-key step on the
-    eight-wave kernels) and the aligned fast path allowed."""
-    steps = not eight_wave_family(tile_m=tile_m, tile_n=tile_n, accum=accum, head_dim=head_dim) \
-        or seq_len % 128 == 0
-    return not (aligned and seq_len % tile_m == 0 and seq_len % tile_n == 0 and steps)
-
-
-def uses_rows256(*, causal: bool, head_dim: int, tile_m: int, tile_n: int, accum: int, n_bh: int,
-                 seq_len: int, compute_units: int) -> bool:
-    """Whether a whole-row launch runs 256-row blocks (ta_fwd_pp256_*); the same rule as
-    use_rows256() in csrc/tiledattn.cpp."""
-    return (not causal and tile_m == 128 and tile_n in (64, 128) and accum == TA_ACC_FP32
-            and head_dim in (64, 128) and n_bh * -(-seq_len // 256) >= 2 * compute_units)
-
-
-def kernel_symbol(*, dtype: int, head_dim: int, tile_m: int, tile_n: int, causal: bool,
-                  tail: bool, accum: int, split: bool = False, pair: bool = False,
-                  rows256: bool = False) -> tuple[str, str]:
-    """(code object file, kernel symbol) the C ABI launches for a configuration; the same
-    rule as kernel_id() in csrc/tiledattn.cpp (used to label measurements).  ``split``
-    names the split-key-range kernel (its merge kernel is ta_fwd_merge_<dt>_d<D>_c<c>),
-    ``pair`` the causal pair kernel (``uses_pairs``); both together the paired-split
-    kernel; ``rows256`` the 256-row kernel (``uses_rows256``; its tail variant also runs
-    when S is not a multiple of 256).  ``tail`` is the variant the C ABI picks
-    (``tail_masked``)."""
-    dt = "bf16" if dtype == TA_BF16 else "f16"
-    c, t = int(bool(causal)), int(bool(tail))
-    if rows256:
-        if causal or head_dim not in (64, 128) or accum != TA_ACC_FP32 or tile_m != 128:
-            raise ValueError("256-row blocks exist for non-causal fp32 D = 64 / 128 at 128-row tiles")
-        return "attn_fwd_pp.hsaco", f"ta_fwd_pp256_{dt}_d{head_dim}_c0_t{t}"
-    if tile_m == 128 and tile_n in (64, 128) and accum == TA_ACC_FP32 and head_dim <= 160:
-        kind = ("pp_psplit" if pair else "pp_split") if split else ("pp_pair" if pair else "pp")
-        return "attn_fwd_pp.hsaco", f"ta_fwd_{kind}_{dt}_d{head_dim}_c{c}_t{t}"
-    if (eight_wave_family(tile_m=tile_m, tile_n=tile_n, accum=accum, head_dim=head_dim)
-            and not split and not pair):
-        if accum == TA_ACC_FP32:
-            return "attn_fwd_pp.hsaco", f"ta_fwd_pp64_{dt}_d{head_dim}_c{c}_t{t}"
-        kind = f"{'ppl' if tile_m == 128 else 'ppl64'}_n{tile_n}"
-        return "attn_fwd_pp.hsaco", f"ta_fwd_{kind}_{dt}_d{head_dim}_c{c}_t{t}"
-    if split:
-        raise ValueError("split key ranges exist for tiles (128, 64) and (128, 128), fp32 "
-                         "accumulation, D <= 160")
-    return (f"attn_fwd_m{tile_m}_n{tile_n}.hsaco",
-            f"ta_fwd_{dt}_d{head_dim}_m{tile_m}_n{tile_n}_c{c}_t{t}_a{int(accum != TA_ACC_FP32)}")
 
 # Every symbol the header declares; tests check the built library exports all of them.
 EXPORTED_SYMBOLS = (
@@ -120,6 +53,8 @@ EXPORTED_SYMBOLS = (
     "ta_split_workspace_size",
     "ta_sdpa_fwd_split",
     "ta_sdpa_fwd_split_static",
+    "ta_describe_launch",
+    "ta_describe_launch_model",
     "ta_cache_reset",
     "ta_cache_size",
     "ta_last_error",
@@ -154,6 +89,66 @@ class FwdArgs(ctypes.Structure):
         ("d_real", ctypes.c_int32),
         ("aligned", ctypes.c_int32),
     ]
+
+
+class LaunchDesc(ctypes.Structure):
+    """Mirror of ``ta_launch_desc``: what one forward enqueues (filled by the library)."""
+
+    _fields_ = [
+        ("code_object", ctypes.c_char * 64),
+        ("kernel", ctypes.c_char * 96),
+        ("grid", ctypes.c_int64),
+        ("block", ctypes.c_int32),
+        ("rows", ctypes.c_int32),
+        ("tail", ctypes.c_int32),
+        ("layout", ctypes.c_int32),
+        ("chunk_steps", ctypes.c_int32),
+        ("compute_units", ctypes.c_int32),
+        ("merge_kernel", ctypes.c_char * 96),
+        ("merge_grid", ctypes.c_int64),
+        ("merge_block", ctypes.c_int32),
+        ("in_place_pad", ctypes.c_int32),
+        ("split_capable", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("workspace_bytes", ctypes.c_int64),
+    ]
+
+    def as_dict(self) -> dict:
+        out = {}
+        for name, _ in self._fields_:
+            if name == "reserved":
+                continue
+            val = getattr(self, name)
+            out[name] = val.decode() if isinstance(val, bytes) else int(val)
+        return out
+
+
+def shape_args(*, B: int = 1, H: int = 1, S: int = 128, D: int = 128, causal: bool = False,
+               dtype: int = TA_BF16, tile_m: int = 128, tile_n: int = 64, accum: int = TA_ACC_FP32,
+               sched: int = 0, aligned: int = 1, d_real: int = 0, device: int = 0) -> "FwdArgs":
+    """A ``FwdArgs`` carrying only the fields the planning queries read (no tensors)."""
+    a = FwdArgs()
+    a.B, a.H, a.S, a.D = B, H, S, D
+    a.causal, a.dtype, a.tile_m, a.tile_n, a.accum = int(causal), dtype, tile_m, tile_n, accum
+    a.sched, a.aligned, a.d_real, a.device = sched, aligned, d_real, device
+    return a
+
+
+def describe(lib: ctypes.CDLL, args: "FwdArgs", chunk_steps: int = 0,
+             compute_units: int | None = None) -> LaunchDesc:
+    """What ``ta_sdpa_fwd`` (chunk 0) or ``ta_sdpa_fwd_split`` would launch for ``args``:
+    on ``args.device`` (``ta_describe_launch``), or for a device of ``compute_units`` CUs
+    without touching one (``ta_describe_launch_model``).  Raises ``ValueError`` with the
+    library's message on a non-OK status."""
+    out = LaunchDesc()
+    if compute_units is None:
+        st = lib.ta_describe_launch(ctypes.byref(args), int(chunk_steps), ctypes.byref(out))
+    else:
+        st = lib.ta_describe_launch_model(ctypes.byref(args), int(chunk_steps), int(compute_units),
+                                          ctypes.byref(out))
+    if st != TA_OK:
+        raise ValueError(f"{status_name(lib, st)}: {last_error(lib)}")
+    return out
 
 
 _lock = Lock()
@@ -209,6 +204,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ta_sdpa_fwd_split.restype = i32
     lib.ta_sdpa_fwd_split_static.argtypes = [ctypes.POINTER(FwdArgs), i32, ctypes.c_void_p]
     lib.ta_sdpa_fwd_split_static.restype = i32
+    lib.ta_describe_launch.argtypes = [ctypes.POINTER(FwdArgs), i32, ctypes.POINTER(LaunchDesc)]
+    lib.ta_describe_launch.restype = i32
+    lib.ta_describe_launch_model.argtypes = [ctypes.POINTER(FwdArgs), i32, i32, ctypes.POINTER(LaunchDesc)]
+    lib.ta_describe_launch_model.restype = i32
     lib.ta_cache_reset.argtypes = []
     lib.ta_cache_reset.restype = i32
     lib.ta_cache_size.argtypes = []

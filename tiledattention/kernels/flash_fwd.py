@@ -217,14 +217,15 @@ def _use_unmasked_tail_kernel(*, seq_len: int, tile_m: int, tile_n: int) -> bool
 
 
 def _default_tile_config_for_shape_gfx950(*, seq_len: int, head_dim: int, causal: bool,
-                                         n_bh: int = 0, accum_mode: str = "fp32") -> tuple[int, int]:
+                                         n_bh: int = 0, accum_mode: str = "fp32",
+                                         compute_units: int) -> tuple[int, int]:
     """Default (TILE_M, TILE_N) on gfx950 when neither env knob is set.
 
     128 query rows per workgroup: the eight-wave kernel (two waves per SIMD splitting every
     128-key step, one workgroup per CU; at kernel head dims above 128 with input-dtype
     accumulation the four-wave kernel with 64-key tiles).  When the 64-row blocks of all
     ``n_bh`` heads fit the CUs in one wave (B*H*ceil(S/64) <= CUs; head dims up to 128, or up
-    to 160 with fp32 accumulation), 64 rows instead: the 64-row eight-wave kernel halves each
+    to 160 with fp32 accumulation; ``compute_units`` is the device's CU count), 64 rows instead: the 64-row eight-wave kernel halves each
     block's key loop and the grid is still one workgroup per CU (B1 H8 bf16: causal S=1024
     15.0 -> 12.0 us, S=2048 23.5 -> 18.8; non-causal S=1024 14.4 -> 11.9, S=2048 23.3 ->
     20.3; D=64 causal S=2048 18.2 -> 13.5; D=160 S=512 / 1024 / 2048 causal 12.2 -> 10.0 /
@@ -243,7 +244,7 @@ def _default_tile_config_for_shape_gfx950(*, seq_len: int, head_dim: int, causal
     tile_n = 128 if (not causal and head_dim == 128 and seq_len >= 2048) else 64
     max_d64 = 160 if accum_mode == "fp32" else 128  # 64-row eight-wave kernels
     if (0 < head_dim <= max_d64 and n_bh > 0 and seq_len > 0
-            and n_bh * ((seq_len + 63) // 64) <= _CU_COUNT):
+            and n_bh * ((seq_len + 63) // 64) <= compute_units):
         return 64, tile_n
     return 128, tile_n
 
@@ -258,7 +259,15 @@ def _resolve_sync_mode() -> str:
     return sync_mode
 
 
-_CU_COUNT = 256  # MI355X
+_CU_COUNTS: dict[int, int] = {}
+
+
+def _compute_units(torch_mod, device_index: int) -> int:
+    """The device's compute units (multiProcessorCount), read once per device."""
+    n = _CU_COUNTS.get(device_index)
+    if n is None:
+        n = _CU_COUNTS[device_index] = int(torch_mod.cuda.get_device_properties(device_index).multi_processor_count)
+    return n
 
 
 def _workgroups_per_cu(*, tile_m: int, tile_n: int, accum_code: int, head_dim: int = 128,
@@ -283,16 +292,18 @@ def _workgroups_per_cu(*, tile_m: int, tile_n: int, accum_code: int, head_dim: i
 
 
 def _resolve_sched(*, n_blocks: int, causal: bool, tile_m: int, tile_n: int,
-                   accum_code: int = _lib.TA_ACC_FP32, head_dim: int = 128) -> int:
+                   accum_code: int = _lib.TA_ACC_FP32, head_dim: int = 128,
+                   compute_units: int) -> int:
     """Workgroup order.  XCD grouping needs the grid to split evenly over the 8 XCDs.  Causal
     tiles go heaviest first (each CU takes the next tile as its last one ends, pairing heavy
-    with light ones); when every workgroup is resident at once there is no "next", and the
-    complementary order (sched 2) places heavy and light tiles on the same CU instead."""
+    with light ones); when every workgroup is resident at once on the device's
+    ``compute_units`` CUs there is no "next", and the complementary order (sched 2) places
+    heavy and light tiles on the same CU instead."""
     raw = os.getenv("TILEDATTN_SCHED", "").strip()
     if raw == "":
         if n_blocks % 8 != 0:
             return 0
-        resident = _CU_COUNT * _workgroups_per_cu(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code,
+        resident = compute_units * _workgroups_per_cu(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code,
                                                   head_dim=head_dim, causal=causal)
         return 2 if causal and n_blocks <= resident else 1
     if raw not in {"0", "1", "2", "3"}:
@@ -329,22 +340,39 @@ class _Launcher:
 _SPLIT_PLANS: dict[tuple[int, int, int, int], int] = {}
 
 
+_FAMILY: dict[tuple[int, int, int, int], tuple[bool, bool]] = {}
+
+
+def _kernel_family(*, tile_m: int, tile_n: int, accum_code: int, kernel_head_dim: int) -> tuple[bool, bool]:
+    """(eight-wave kernel, split kernels exist) for a configuration, as the library reports
+    them (``ta_describe_launch_model``: ``in_place_pad``, ``split_capable``); (False, False)
+    for a configuration the library has no kernel for."""
+    key = (tile_m, tile_n, accum_code, kernel_head_dim)
+    fam = _FAMILY.get(key)
+    if fam is None:
+        lib = _lib.load()
+        args = _lib.shape_args(D=kernel_head_dim, tile_m=tile_m, tile_n=tile_n, accum=accum_code)
+        out = _lib.LaunchDesc()
+        st = lib.ta_describe_launch_model(ctypes.byref(args), 0, 256, ctypes.byref(out))
+        fam = _FAMILY[key] = (bool(out.in_place_pad), bool(out.split_capable)) if st == _lib.TA_OK \
+            else (False, False)
+    return fam
+
+
 def _eight_wave_kernel(*, tile_m: int, tile_n: int, accum_code: int, kernel_head_dim: int) -> bool:
     """Whether the configuration runs an eight-wave kernel, the ones with in-place padding of
-    narrower head dims: fp32 accumulation with tile (128, 64) or (128, 128) at kernel head
-    dim 64, 128 or 160 (workgroup step 128 rows x 128 keys, 64 keys per wave group, so it
-    serves both 128-row tiles), or with tile (64, 64) or (64, 128) at 64 or 128 (the
-    64-row form, the same 128-key steps); input-dtype accumulation with any tile at 64 or
-    128."""
-    return _lib.eight_wave_family(tile_m=tile_m, tile_n=tile_n, accum=accum_code,
-                                  head_dim=kernel_head_dim)
+    narrower head dims (fp32 accumulation with 128-row tiles at kernel head dims up to 160 or
+    64-row tiles at 64, 96, 128 and 160; input-dtype accumulation with any tile at 64 or
+    128).  Read from the library, whose kernel selection it is."""
+    return _kernel_family(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code,
+                          kernel_head_dim=kernel_head_dim)[0]
 
 
 def _split_capable(*, tile_m: int, tile_n: int, accum_code: int, kernel_head_dim: int) -> bool:
-    """Whether split key ranges exist: the 128-row eight-wave kernel with fp32 accumulation."""
-    return tile_m == 128 and accum_code == _lib.TA_ACC_FP32 and _eight_wave_kernel(
-        tile_m=tile_m, tile_n=tile_n, accum_code=accum_code, kernel_head_dim=kernel_head_dim)
-
+    """Whether split key ranges exist (the 128-row eight-wave kernel with fp32
+    accumulation), as the library reports it."""
+    return _kernel_family(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code,
+                          kernel_head_dim=kernel_head_dim)[1]
 
 
 def _resolve_split(lib, args: _lib.FwdArgs, *, capable: bool) -> int:
@@ -386,10 +414,14 @@ def _resolve_split(lib, args: _lib.FwdArgs, *, capable: bool) -> int:
 
 
 def _split_preferred(lib, q, batch: int, heads: int, seq_len: int, head_dim: int, causal: bool,
-                     torch_mod) -> bool:
+                     torch_mod, accum_mode: str = "fp32") -> bool:
     """Whether the 128-row kernel runs split key ranges for this shape (a forced chunk
     length, or the library's dispatch model under ``TILEDATTN_SPLIT=auto``): the default
-    tile then stays at 128 rows, the tile the split path exists for."""
+    tile then stays at 128 rows, the tile the split path exists for.  Split kernels exist
+    for fp32 accumulation only, so input-dtype accumulation never prefers them (128 rows
+    would then run unsplit on half the CUs the 64-row default fills)."""
+    if accum_mode != "fp32":
+        return False
     raw = os.getenv("TILEDATTN_SPLIT", "").strip().lower()
     if raw in ("0", "off"):
         return False
@@ -402,7 +434,7 @@ def _split_preferred(lib, q, batch: int, heads: int, seq_len: int, head_dim: int
     args.dtype = _dtype_code_for_torch_dtype(q.dtype)
     args.tile_m, args.tile_n = 128, 64
     args.accum = _lib.TA_ACC_FP32
-    args.device = q.device.index if q.device.index is not None else torch_mod.cuda.current_device()
+    args.device = _device_index(torch_mod, q)
     return _resolve_split(lib, args, capable=True) != 0
 
 
@@ -487,6 +519,10 @@ _PLANS: dict[tuple, _LaunchPlan] = {}
 _PLANS_MAX = 512
 
 
+def _device_index(torch_mod, t) -> int:
+    return t.device.index if t.device.index is not None else torch_mod.cuda.current_device()
+
+
 def _raw_stream(torch_mod, device_index: int) -> int:
     get_raw = getattr(torch_mod._C, "_cuda_getCurrentRawStream", None)
     if get_raw is not None:
@@ -519,9 +555,11 @@ def _build_plan(torch_mod, lib, q, k, v, causal: bool, tile: tuple[int, int] | N
         _check_tile_supported(tile_m, tile_n)
     else:
         tile_m, tile_n = _default_tile_config_for_shape_gfx950(
-            seq_len=seq_len, head_dim=head_dim, causal=causal, n_bh=bh, accum_mode=accum_mode
+            seq_len=seq_len, head_dim=head_dim, causal=causal, n_bh=bh, accum_mode=accum_mode,
+            compute_units=_compute_units(torch_mod, _device_index(torch_mod, q)),
         )
-        if tile_m == 64 and _split_preferred(lib, q, batch, heads, seq_len, head_dim, causal, torch_mod):
+        if tile_m == 64 and _split_preferred(lib, q, batch, heads, seq_len, head_dim, causal, torch_mod,
+                                             accum_mode):
             tile_m = 128
 
     chunk_plan = _resolve_chunk_plan(head_dim)
@@ -564,7 +602,7 @@ def _build_plan(torch_mod, lib, q, k, v, causal: bool, tile: tuple[int, int] | N
         kernel_variant = "direct_aligned"
     else:
         kernel_variant = "direct"
-    device_index = q.device.index if q.device.index is not None else torch_mod.cuda.current_device()
+    device_index = _device_index(torch_mod, q)
     plan.device_index = device_index
 
     kernel_key = (
@@ -604,7 +642,8 @@ def _build_plan(torch_mod, lib, q, k, v, causal: bool, tile: tuple[int, int] | N
     args.accum = accum_code
     args.device = device_index
     args.sched = _resolve_sched(n_blocks=bh * n_qblk, causal=causal, tile_m=tile_m, tile_n=tile_n,
-                                accum_code=accum_code, head_dim=kernel_head_dim)
+                                accum_code=accum_code, head_dim=kernel_head_dim,
+                                compute_units=_compute_units(torch_mod, device_index))
 
     capable = _split_capable(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code,
                              kernel_head_dim=kernel_head_dim)
@@ -619,6 +658,33 @@ def _build_plan(torch_mod, lib, q, k, v, causal: bool, tile: tuple[int, int] | N
             args.sched = 1  # the split grid regroups per XCD whenever it divides evenly
     plan.args = args
     return plan
+
+
+def _plan_for(torch_mod, q, k, v, causal: bool, tile, accum) -> _LaunchPlan:
+    """The cached launch plan of a call (built on the first call of a configuration)."""
+    key = (q.shape, q.stride(), k.stride(), v.stride(), q.dtype, q.device, causal, _knob_snapshot(),
+           tile, accum)
+    plan = _PLANS.get(key)
+    if plan is None or plan.generation != _compile_cache.generation():
+        plan = _build_plan(torch_mod, _runtime.get_native_library(), q, k, v, causal, tile, accum)
+        if len(_PLANS) >= _PLANS_MAX:
+            _PLANS.clear()
+        _PLANS[key] = plan
+    return plan
+
+
+def describe_call(q, k, v, *, causal: bool, tile: tuple[int, int] | None = None,
+                  accum: str | None = None) -> dict:
+    """What ``run_flash_fwd`` enqueues for these inputs under the current knobs, as the
+    library reports it (``ta_describe_launch``: kernel and code object, grid, layout, split,
+    merge kernel, workspace); an empty dict when nothing is launched (zero-size inputs).
+    Launches nothing."""
+    torch_mod = _runtime.get_torch_module()
+    plan = _plan_for(torch_mod, q, k, v, causal, tile, accum)
+    if plan.empty:
+        return {}
+    lib = _runtime.get_native_library()
+    return _lib.describe(lib, plan.args, plan.chunk).as_dict()
 
 
 def run_flash_fwd(
@@ -646,14 +712,7 @@ def run_flash_fwd(
     them unset, as the reference's call does.
     """
     torch_mod = _runtime.get_torch_module()
-    key = (q.shape, q.stride(), k.stride(), v.stride(), q.dtype, q.device, causal, _knob_snapshot(),
-           tile, accum)
-    plan = _PLANS.get(key)
-    if plan is None or plan.generation != _compile_cache.generation():
-        plan = _build_plan(torch_mod, _runtime.get_native_library(), q, k, v, causal, tile, accum)
-        if len(_PLANS) >= _PLANS_MAX:
-            _PLANS.clear()
-        _PLANS[key] = plan
+    plan = _plan_for(torch_mod, q, k, v, causal, tile, accum)
 
     if plan.out_like_q and type(q) is torch_mod.Tensor:
         out = torch_mod.empty_like(q, memory_format=torch_mod.contiguous_format)

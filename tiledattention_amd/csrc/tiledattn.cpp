@@ -503,6 +503,148 @@ bool split_capable(const ta_fwd_args* a) {
   return eight_wave(a->tile_m, a->tile_n, a->accum, a->D);
 }
 
+// Everything one forward launches, decided in one place: ta_sdpa_fwd, ta_sdpa_fwd_split
+// and ta_describe_launch all read it from plan_launch, so the launch and its description
+// cannot disagree.
+struct LaunchPlan {
+  KernelId main;         // the attention kernel
+  int64_t grid = 0;      // its workgroups
+  int32_t rows = 0;      // query rows per query block it processes
+  bool tail = false;     // tail-masked variant
+  int32_t layout = TA_LAYOUT_WHOLE_ROWS;
+  int32_t chunk = 0;     // split actually run (0 = whole rows)
+  bool merge = false;    // a merge kernel follows (split layouts)
+  KernelId merge_id;
+  int64_t merge_grid = 0;
+  SplitLayout split;     // valid when merge
+  int64_t ws_bytes = 0;  // split workspace
+};
+
+// The plan for shape-validated arguments with n_bh * n_qblk > 0, on a device of `ncu`
+// compute units.  chunk_steps = 0, or a chunk length that splits nothing, plans the
+// whole-row launch (pairs or 256-row blocks where their rules pick them); a chunk length
+// that splits something on a configuration without split kernels is TA_EUNSUPPORTED.
+ta_status plan_launch(const ta_fwd_args* a, int64_t n_bh, int64_t n_qblk, int32_t chunk_steps,
+                      int ncu, LaunchPlan* pl) {
+  *pl = LaunchPlan();
+  const bool aligned = unmasked_tail(a);
+  pl->tail = !aligned;
+  const char* dt = a->dtype == TA_BF16 ? "bf16" : "f16";
+  SplitLayout l;
+  if (chunk_steps != 0 && layout_for(a->S, a->causal != 0, chunk_steps, &l)) {
+    if (!split_capable(a))
+      return fail(TA_EUNSUPPORTED,
+                  "split key ranges need tile (128, 64) or (128, 128), fp32 accumulation, D <= 160");
+    if (n_bh * l.items > 0x7fffffffLL || n_bh * l.slots * kSplitRows > 0x7fffffffLL ||
+        n_bh * l.merge * kSplitRows > 0x7fffffffLL)
+      return fail(TA_EINVAL, "split grid too large");
+    const bool paired = chunk_steps == TA_SPLIT_PAIRS;
+    char name[96];
+    snprintf(name, sizeof(name), "ta_fwd_pp_%s_%s_d%d_c%d_t%d", paired ? "psplit" : "split", dt,
+             (int)a->D, a->causal ? 1 : 0, aligned ? 0 : 1);
+    pl->main = KernelId{"attn_fwd_pp.hsaco", name, 512u};
+    pl->grid = n_bh * l.items;
+    pl->rows = kSplitRows;
+    pl->layout = paired ? TA_LAYOUT_PAIRED_SPLIT : TA_LAYOUT_SPLIT;
+    pl->chunk = chunk_steps;
+    // merge: one thread per (row, 16-byte output chunk), merge_rows_per_wg(D) rows a workgroup
+    const int d8 = static_cast<int>(a->D);
+    snprintf(name, sizeof(name), "ta_fwd_merge_%s_d%d_c%d", dt, d8, a->causal ? 1 : 0);
+    pl->merge = true;
+    pl->merge_id = KernelId{"attn_fwd_pp.hsaco", name, static_cast<unsigned>(ta::merge_threads(d8))};
+    pl->merge_grid = n_bh * l.merge * (kSplitRows / ta::merge_rows_per_wg(d8));
+    pl->split = l;
+    pl->ws_bytes = split_ws_bytes(n_bh, a->D, l);
+    ta_status gst = check_grid(pl->grid, 512u, "split kernel");
+    if (gst == TA_OK) gst = check_grid(pl->merge_grid, pl->merge_id.block, "merge kernel");
+    return gst;
+  }
+  pl->main = kernel_id(a->dtype, (int)a->D, a->tile_m, a->tile_n, a->causal, !aligned, a->accum);
+  pl->grid = n_bh * n_qblk;
+  pl->rows = a->tile_m;
+  if (eight_wave(a->tile_m, a->tile_n, a->accum, a->D)) {
+    if (a->causal && use_pairs(a, n_bh, n_qblk, ncu)) {
+      pl->main = pair_kernel_id(a->dtype, (int)a->D, !aligned);
+      pl->grid = n_bh * ((n_qblk + 1) / 2);
+      pl->layout = TA_LAYOUT_PAIRS;
+    } else if (use_rows256(a, n_bh, ncu)) {
+      const int64_t nq256 = (a->S + 255) / 256;
+      const bool t256 = !(aligned && a->S % 256 == 0);
+      char name[64];
+      snprintf(name, sizeof(name), "ta_fwd_pp256_%s_d%d_c0_t%d", dt, (int)a->D, t256 ? 1 : 0);
+      pl->main = KernelId{"attn_fwd_pp.hsaco", name, 512u};
+      pl->grid = n_bh * nq256;
+      pl->rows = 256;
+      pl->tail = t256;
+      pl->layout = TA_LAYOUT_ROWS256;
+    }
+  }
+  return check_grid(pl->grid, pl->main.block, "kernel");
+}
+
+void fill_desc(const ta_fwd_args* a, const LaunchPlan& pl, int ncu, ta_launch_desc* d) {
+  memset(d, 0, sizeof(*d));
+  snprintf(d->code_object, sizeof(d->code_object), "%s", pl.main.file.c_str());
+  snprintf(d->kernel, sizeof(d->kernel), "%s", pl.main.name.c_str());
+  d->grid = pl.grid;
+  d->block = static_cast<int32_t>(pl.main.block);
+  d->rows = pl.rows;
+  d->tail = pl.tail ? 1 : 0;
+  d->layout = pl.layout;
+  d->chunk_steps = pl.chunk;
+  d->compute_units = ncu;
+  if (pl.merge) {
+    snprintf(d->merge_kernel, sizeof(d->merge_kernel), "%s", pl.merge_id.name.c_str());
+    d->merge_grid = pl.merge_grid;
+    d->merge_block = static_cast<int32_t>(pl.merge_id.block);
+  }
+  d->workspace_bytes = pl.ws_bytes;
+  d->in_place_pad = eight_wave_family(a->tile_m, a->tile_n, a->accum, a->D) ? 1 : 0;
+  d->split_capable = split_capable(a) ? 1 : 0;
+}
+
+// Shape checks, then the plan and its description (no device, no tensors).
+ta_status describe_model(const ta_fwd_args* a, int32_t chunk_steps, int ncu, ta_launch_desc* out) {
+  if (out == nullptr) return fail(TA_EINVAL, "out is NULL");
+  memset(out, 0, sizeof(*out));
+  if (chunk_steps < 0 && chunk_steps != TA_SPLIT_PAIRS) return fail(TA_EINVAL, "chunk_steps %d", chunk_steps);
+  if (ncu <= 0) return fail(TA_EINVAL, "compute_units %d", ncu);
+  int64_t n_bh = 0, n_qblk = 0;
+  ta_status vst = validate_args(a, &n_bh, &n_qblk, false);
+  if (vst != TA_OK) return vst;
+  out->compute_units = ncu;
+  out->in_place_pad = eight_wave_family(a->tile_m, a->tile_n, a->accum, a->D) ? 1 : 0;
+  out->split_capable = split_capable(a) ? 1 : 0;
+  if (n_qblk == 0) return TA_OK;  // zero-size: nothing is launched
+  LaunchPlan pl;
+  ta_status st = plan_launch(a, n_bh, n_qblk, chunk_steps, ncu, &pl);
+  if (st != TA_OK) return st;
+  fill_desc(a, pl, ncu, out);
+  return TA_OK;
+}
+
+// Resolves the plan's kernels and enqueues them.  Caller holds g_mu and has made the device
+// current; p carries the tensors (and, for a split, the workspace).
+ta_status launch_plan_locked(const ta_fwd_args* a, const LaunchPlan& pl, ta::FwdParams* p,
+                             void* stream) {
+  hipFunction_t fn = nullptr, mfn = nullptr;
+  ta_status s = get_function_locked(a->device, pl.main, &fn);
+  if (s == TA_OK && pl.merge) s = get_function_locked(a->device, pl.merge_id, &mfn);
+  if (s != TA_OK) return s;
+  if (pl.layout == TA_LAYOUT_ROWS256) p->n_qblk = static_cast<int32_t>((a->S + 255) / 256);
+  void* params[] = {p};
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  hipError_t e = hipModuleLaunchKernel(fn, static_cast<unsigned>(pl.grid), 1, 1, pl.main.block, 1, 1,
+                                       0, hs, params, nullptr);
+  if (e != hipSuccess) return fail(TA_EHIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
+  if (pl.merge) {
+    e = hipModuleLaunchKernel(mfn, static_cast<unsigned>(pl.merge_grid), 1, 1, pl.merge_id.block, 1,
+                              1, 0, hs, params, nullptr);
+    if (e != hipSuccess) return fail(TA_EHIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
+  }
+  return TA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -565,48 +707,47 @@ ta_status ta_sdpa_fwd(const ta_fwd_args* a, void* stream) {
   int64_t n_bh = 0, n_qblk = 0;
   ta_status vst = validate_args(a, &n_bh, &n_qblk);
   if (vst != TA_OK || n_qblk == 0) return vst;
-
-  const bool aligned = unmasked_tail(a);
-  KernelId id =
-      kernel_id(a->dtype, (int)a->D, a->tile_m, a->tile_n, a->causal, !aligned, a->accum);
-  ta_status gst = check_grid(n_bh * n_qblk, id.block, "kernel");
+  // The whole-row grid bounds every layout's (pairs and 256-row blocks only shrink it), so
+  // an oversized request is rejected before any device call.
+  const KernelId base = kernel_id(a->dtype, (int)a->D, a->tile_m, a->tile_n, a->causal,
+                                  !unmasked_tail(a), a->accum);
+  ta_status gst = check_grid(n_bh * n_qblk, base.block, "kernel");
   if (gst != TA_OK) return gst;
   ta::FwdParams p;
   fill_params(a, n_bh, n_qblk, &p);
 
-  // Resolve and launch under the cache lock (a concurrent ta_cache_reset cannot unload the
-  // module in between); the launch only enqueues.
+  // Plan, resolve and launch under the cache lock (a concurrent ta_cache_reset cannot unload
+  // the module in between); the launch only enqueues.
   std::lock_guard<std::mutex> lock(g_mu);
   DeviceGuard guard(a->device);
   if (guard.err != hipSuccess)
     return fail(TA_EHIP, "set device %d: %s", a->device, hipGetErrorString(guard.err));
-  int64_t blocks = n_bh * n_qblk;
-  if (eight_wave(a->tile_m, a->tile_n, a->accum, a->D)) {
-    int ncu = 0;
-    ta_status cst = cu_count_locked(a->device, &ncu);
+  int ncu = 0;
+  ta_status cst = cu_count_locked(a->device, &ncu);
+  if (cst != TA_OK) return cst;
+  LaunchPlan pl;
+  ta_status st = plan_launch(a, n_bh, n_qblk, 0, ncu, &pl);
+  if (st != TA_OK) return st;
+  return launch_plan_locked(a, pl, &p, stream);
+}
+
+ta_status ta_describe_launch_model(const ta_fwd_args* args, int32_t chunk_steps,
+                                   int32_t compute_units, ta_launch_desc* out) {
+  return describe_model(args, chunk_steps, compute_units, out);
+}
+
+ta_status ta_describe_launch(const ta_fwd_args* args, int32_t chunk_steps, ta_launch_desc* out) {
+  if (args == nullptr) return fail(TA_EINVAL, "args is NULL");
+  int ncu = 0;
+  {
+    std::lock_guard<std::mutex> lock(g_mu);
+    DeviceGuard guard(args->device);
+    if (guard.err != hipSuccess)
+      return fail(TA_EHIP, "set device %d: %s", args->device, hipGetErrorString(guard.err));
+    ta_status cst = cu_count_locked(args->device, &ncu);
     if (cst != TA_OK) return cst;
-    if (a->causal && use_pairs(a, n_bh, n_qblk, ncu)) {
-      id = pair_kernel_id(a->dtype, (int)a->D, !aligned);
-      blocks = n_bh * ((n_qblk + 1) / 2);
-    } else if (use_rows256(a, n_bh, ncu)) {
-      const int64_t nq256 = (a->S + 255) / 256;
-      char name[64];
-      snprintf(name, sizeof(name), "ta_fwd_pp256_%s_d%d_c0_t%d", a->dtype == TA_BF16 ? "bf16" : "f16",
-               (int)a->D, aligned && a->S % 256 == 0 ? 0 : 1);
-      id = KernelId{"attn_fwd_pp.hsaco", name, 512u};
-      p.n_qblk = static_cast<int32_t>(nq256);
-      blocks = n_bh * nq256;
-    }
   }
-  hipFunction_t fn = nullptr;
-  ta_status s = get_function_locked(a->device, id, &fn);
-  if (s != TA_OK) return s;
-  void* params[] = {&p};
-  const unsigned grid = static_cast<unsigned>(blocks);
-  hipError_t e = hipModuleLaunchKernel(fn, grid, 1, 1, id.block, 1, 1, 0,
-                                       static_cast<hipStream_t>(stream), params, nullptr);
-  if (e != hipSuccess) return fail(TA_EHIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
-  return TA_OK;
+  return describe_model(args, chunk_steps, ncu, out);
 }
 
 ta_status ta_split_plan(const ta_fwd_args* a, int32_t* chunk_steps) {
@@ -651,10 +792,13 @@ ta_status ta_split_workspace_size(const ta_fwd_args* a, int32_t chunk_steps, int
   int64_t n_bh = 0, n_qblk = 0;
   ta_status vst = validate_args(a, &n_bh, &n_qblk, false);
   if (vst != TA_OK || n_qblk == 0 || chunk_steps == 0) return vst;
+  // A chunk length that splits nothing runs whole rows (as ta_sdpa_fwd_split does): no
+  // workspace, on any kernel.
+  SplitLayout l;
+  if (!layout_for(a->S, a->causal != 0, chunk_steps, &l)) return TA_OK;
   if (!split_capable(a))
     return fail(TA_EUNSUPPORTED, "split key ranges need tile (128, 64) or (128, 128), fp32 accumulation, D <= 160");
-  SplitLayout l;
-  if (layout_for(a->S, a->causal != 0, chunk_steps, &l)) *bytes = split_ws_bytes(n_bh, a->D, l);
+  *bytes = split_ws_bytes(n_bh, a->D, l);
   return TA_OK;
 }
 
@@ -667,34 +811,15 @@ ta_status ta_sdpa_fwd_split(const ta_fwd_args* a, int32_t chunk_steps, void* wor
   SplitLayout l;
   if (chunk_steps == 0 || !layout_for(a->S, a->causal != 0, chunk_steps, &l))
     return ta_sdpa_fwd(a, stream);
-  if (!split_capable(a))
-    return fail(TA_EUNSUPPORTED, "split key ranges need tile (128, 64) or (128, 128), fp32 accumulation, D <= 160");
-  const int64_t need = split_ws_bytes(n_bh, a->D, l);
-  if (workspace == nullptr || workspace_bytes < need)
-    return fail(TA_EINVAL, "workspace of %lld bytes needed, %lld given", (long long)need,
+  // The split plan needs no compute-unit count (only whole rows choose by it).
+  LaunchPlan pl;
+  ta_status st = plan_launch(a, n_bh, n_qblk, chunk_steps, 1, &pl);
+  if (st != TA_OK) return st;
+  if (workspace == nullptr || workspace_bytes < pl.ws_bytes)
+    return fail(TA_EINVAL, "workspace of %lld bytes needed, %lld given", (long long)pl.ws_bytes,
                 (long long)(workspace == nullptr ? 0 : workspace_bytes));
   if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
     return fail(TA_EINVAL, "workspace must be 256-byte aligned");
-  if (n_bh * l.items > 0x7fffffffLL || n_bh * l.slots * kSplitRows > 0x7fffffffLL ||
-      n_bh * l.merge * kSplitRows > 0x7fffffffLL)
-    return fail(TA_EINVAL, "split grid too large");
-  // merge: one thread per (row, 16-byte output chunk), merge_rows_per_wg(D) rows a workgroup
-  const int d8 = static_cast<int>(a->D);
-  const unsigned merge_block = static_cast<unsigned>(ta::merge_threads(d8));
-  const int64_t merge_wgs = n_bh * l.merge * (kSplitRows / ta::merge_rows_per_wg(d8));
-  ta_status gst = check_grid(n_bh * l.items, 512u, "split kernel");
-  if (gst == TA_OK) gst = check_grid(merge_wgs, merge_block, "merge kernel");
-  if (gst != TA_OK) return gst;
-
-  const bool aligned = unmasked_tail(a);
-  const char* dt = a->dtype == TA_BF16 ? "bf16" : "f16";
-  char name[96];
-  const bool paired = chunk_steps == TA_SPLIT_PAIRS;
-  snprintf(name, sizeof(name), "ta_fwd_pp_%s_%s_d%d_c%d_t%d", paired ? "psplit" : "split", dt,
-           (int)a->D, a->causal ? 1 : 0, aligned ? 0 : 1);
-  const KernelId sid{"attn_fwd_pp.hsaco", name, 512u};
-  snprintf(name, sizeof(name), "ta_fwd_merge_%s_d%d_c%d", dt, (int)a->D, a->causal ? 1 : 0);
-  const KernelId mid{"attn_fwd_pp.hsaco", name, 256u};
   ta::FwdParams p;
   fill_params(a, n_bh, n_qblk, &p);
   const int64_t rows = n_bh * l.slots * kSplitRows;
@@ -703,7 +828,7 @@ ta_status ta_sdpa_fwd_split(const ta_fwd_args* a, int32_t chunk_steps, void* wor
                                         (rows * a->D * 4 + 255) / 256 * 256);
   p.split_c = chunk_steps;
   p.split_items = static_cast<int32_t>(l.items);
-  p.split_ns = paired ? kPairCut : static_cast<int32_t>(l.ns);
+  p.split_ns = chunk_steps == TA_SPLIT_PAIRS ? kPairCut : static_cast<int32_t>(l.ns);
   p.split_slots = static_cast<int32_t>(l.slots);
 
   // Resolve and launch under the cache lock, as ta_sdpa_fwd does.
@@ -711,19 +836,7 @@ ta_status ta_sdpa_fwd_split(const ta_fwd_args* a, int32_t chunk_steps, void* wor
   DeviceGuard guard(a->device);
   if (guard.err != hipSuccess)
     return fail(TA_EHIP, "set device %d: %s", a->device, hipGetErrorString(guard.err));
-  hipFunction_t sfn = nullptr, mfn = nullptr;
-  ta_status s = get_function_locked(a->device, sid, &sfn);
-  if (s == TA_OK) s = get_function_locked(a->device, mid, &mfn);
-  if (s != TA_OK) return s;
-  void* params[] = {&p};
-  hipStream_t hs = static_cast<hipStream_t>(stream);
-  hipError_t e = hipModuleLaunchKernel(sfn, static_cast<unsigned>(n_bh * l.items), 1, 1, 512, 1,
-                                       1, 0, hs, params, nullptr);
-  if (e != hipSuccess) return fail(TA_EHIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
-  e = hipModuleLaunchKernel(mfn, static_cast<unsigned>(merge_wgs), 1, 1, merge_block, 1, 1, 0, hs, params,
-                            nullptr);
-  if (e != hipSuccess) return fail(TA_EHIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
-  return TA_OK;
+  return launch_plan_locked(a, pl, &p, stream);
 }
 
 }  // extern "C"
