@@ -66,6 +66,18 @@ def run_gpu(q, k, v, *, causal, scale=None, **env):
     return out
 
 
+def kernel_for(q, k, v, *, causal, **env) -> str:
+    """The attention kernel the library launches for these inputs under the given knobs
+    (``describe_call``, i.e. ``ta_describe_launch``); nothing is launched."""
+    import torch
+
+    from tiledattention.kernels import flash_fwd
+
+    dev = torch.device("cuda:0")
+    with knobs(**env):
+        return flash_fwd.describe_call(q.to(dev), k.to(dev), v.to(dev), causal=causal).get("kernel", "")
+
+
 def oracle_f32(q, k, v, *, causal, scale=None, rows=None):
     dc = O.dtype_code(str(q.dtype))
     qb, kb, vb = O.to_bits(q), O.to_bits(k), O.to_bits(v)

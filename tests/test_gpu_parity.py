@@ -18,6 +18,7 @@ from tests.parity_util import (
     as_f32,
     check_close,
     inputs,
+    kernel_for,
     knobs,
     oracle_f32,
     run_gpu,
@@ -261,11 +262,10 @@ def test_eight_wave_d160(gpu, d, dtype, causal, s):
     missing tail columns read as zero.  Ragged S, both dtypes, [B,S,H,D] views."""
     import torch
 
-    from tiledattention import _lib, sdpa
+    from tiledattention import sdpa
 
-    assert _lib.kernel_symbol(dtype=_lib.TA_BF16, head_dim=160, tile_m=128, tile_n=64,
-                              causal=causal, tail=False, accum=_lib.TA_ACC_FP32)[1].startswith("ta_fwd_pp_")
     q, k, v = inputs((2, 3, s, d), dtype, 160 + d + s)
+    assert kernel_for(q, k, v, causal=causal, tile_m=128, tile_n=64).startswith("ta_fwd_pp_")
     rows = None if s <= 2048 else sample_rows(s, 96)
     ref = oracle_f32(q, k, v, causal=causal, rows=rows)
     say(f"eight-wave D={d} {dtype} (2,3,{s},{d}) causal={causal}")
@@ -295,11 +295,10 @@ def test_64_row_d160(gpu, d, dtype, causal, s, tn):
     dtypes, [B,S,H,D] views."""
     import torch
 
-    from tiledattention import _lib, sdpa
+    from tiledattention import sdpa
 
-    assert _lib.kernel_symbol(dtype=_lib.TA_BF16, head_dim=160, tile_m=64, tile_n=tn, causal=causal,
-                              tail=True, accum=_lib.TA_ACC_FP32)[1].startswith("ta_fwd_pp64_")
     q, k, v = inputs((2, 3, s, d), dtype, 640 + d + s)
+    assert kernel_for(q, k, v, causal=causal, tile_m=64, tile_n=tn).startswith("ta_fwd_pp64_")
     rows = None if s <= 2048 else sample_rows(s, 96)
     ref = oracle_f32(q, k, v, causal=causal, rows=rows)
     say(f"64-row D={d} {dtype} (2,3,{s},{d}) causal={causal} tile (64,{tn})")
@@ -371,13 +370,11 @@ def test_eight_wave_64_row_tiles(gpu, tn, s, causal, dtype):
     narrower head dims padded in place (D = 48 and 96); [B,S,H,D] views for one case."""
     import torch
 
-    from tiledattention import _lib, sdpa
+    from tiledattention import sdpa
 
-    for d in (64, 128):
-        assert _lib.kernel_symbol(dtype=_lib.TA_BF16, head_dim=d, tile_m=64, tile_n=tn, causal=causal,
-                                  tail=True, accum=_lib.TA_ACC_FP32)[1].startswith("ta_fwd_pp64_")
     for d in (64, 128, 48, 96):
         q, k, v = inputs((2, 3, s, d), dtype, 6400 + s + d + tn)
+        assert kernel_for(q, k, v, causal=causal, tile_m=64, tile_n=tn).startswith("ta_fwd_pp64_")
         say(f"64-row eight-wave {dtype} (2,3,{s},{d}) causal={causal} tiles=(64,{tn})")
         out = run_gpu(q, k, v, causal=causal, tile_m=64, tile_n=tn)
         assert out.shape == (2, 3, s, d)

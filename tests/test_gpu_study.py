@@ -1,5 +1,5 @@
 """The study harness on the GPU: a tiny grid through every method, the tuning sweep and the
-CLI's files (schemas and statuses; the timings themselves are not checked)."""
+CLI's files (schemas and statuses), and every timed method's output against the oracle."""
 
 from __future__ import annotations
 
@@ -50,3 +50,39 @@ def test_tune_and_cli_files(gpu, tmp_path):
     assert list(got[0].keys()) == list(study.BENCH_FIELDS)
     assert (tmp_path / "table3_reproducibility.md").read_text().startswith("# Table 3")
     assert "| float16 | False | 128 | 64 |" in (tmp_path / "study_summary.md").read_text()
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_harness_methods_compute_attention(gpu, dtype, causal):
+    """Every method the study times computes the attention it is timed for: the inputs the
+    harness generates (torch.manual_seed(1234), N(0,1) on the GPU, run_study.py:526-529),
+    each method's output against the explicit fp32 oracle on the same values.  The
+    ``tiledattention`` rows meet the north-star bound; PyTorch's own paths 5e-2 (the eager
+    path rounds its scores to the input dtype; the check is that they are attention, which
+    a transposed operand, a dropped scale or a shifted mask would miss by far more)."""
+    import torch
+
+    from tests.parity_util import TOL, check_close, oracle_f32
+
+    b, h, s, d = 1, 2, 200, 64
+    torch.manual_seed(1234)
+    q = torch.randn((b, h, s, d), device="cuda", dtype=getattr(torch, dtype))
+    k = torch.randn((b, h, s, d), device="cuda", dtype=getattr(torch, dtype))
+    v = torch.randn((b, h, s, d), device="cuda", dtype=getattr(torch, dtype))
+    ref = oracle_f32(q.cpu(), k.cpu(), v.cpu(), causal=causal)
+    checked = set()
+    for method, fn in study.build_methods(q, k, v, causal=causal, forced_backends=True, flashattention=True):
+        say(f"study method {method} {dtype} causal={causal} (1,2,200,64)")
+        try:
+            out = fn()
+        except Exception as exc:  # the harness classifies these; only ok methods are checked
+            status, _ = study.classify_failure(method, exc)
+            assert status in OK_OR_SKIPPED and method != "tiledattention", (method, exc)
+            continue
+        torch.cuda.synchronize()
+        got = out.float().cpu().numpy()
+        tol = TOL[dtype] if method == "tiledattention" else 5e-2
+        check_close(got, ref, dtype, tol=tol, what=f"study {method}")
+        checked.add(method)
+    assert {"tiledattention", "standard_eager"} <= checked
