@@ -222,6 +222,44 @@ ta_status ta_describe_launch(const ta_fwd_args* args, int32_t chunk_steps, ta_la
 ta_status ta_describe_launch_model(const ta_fwd_args* args, int32_t chunk_steps,
                                    int32_t compute_units, ta_launch_desc* out);
 
+/* Chunk length meaning "the library's dispatch model decides" (TILEDATTN_SPLIT=auto). */
+#define TA_SPLIT_AUTO (-2)
+
+/* Knob values of one call, as the TILEDATTN_* environment knobs or an operator's arguments
+ * give them. */
+typedef struct ta_call_knobs {
+  int32_t tile_m, tile_n; /* both 0: the default rule; else the tile, 64 or 128 each */
+  int32_t accum;          /* -1 auto (fp32 on gfx950), TA_ACC_FP32 or TA_ACC_INPUT */
+  int32_t aligned;        /* 1: the aligned fast path is allowed; 0: disabled */
+  int32_t sched;          /* -1: the default order; 0..3 as ta_fwd_args.sched */
+  int32_t split;          /* TA_SPLIT_AUTO, 0 (whole rows), a chunk length or TA_SPLIT_PAIRS */
+} ta_call_knobs;
+
+/* What one call runs: the launch arguments (all but q, k, v, o, the strides and scale,
+ * which the caller fills) and what the caller does around the launch. */
+typedef struct ta_call_plan {
+  ta_fwd_args args;        /* shape (D = the kernel's head dim), dtype, causal, tiles, accum,
+                              device, sched, d_real, aligned */
+  int32_t chunk_steps;     /* 0: ta_sdpa_fwd; else ta_sdpa_fwd_split with this chunk length */
+  int32_t host_pad;        /* zero columns the caller appends to q, k and v (0: none) */
+  int32_t out_width;       /* columns of the output buffer (the caller's head dim, or the
+                              kernel's when padded on the host: slice it back) */
+  int32_t reserved;
+  int64_t workspace_bytes; /* device workspace of the split (0: none) */
+} ta_call_plan;
+
+/* The host policy of one forward of q, k, v [B, H, S, D] (the reference's
+ * run_flash_fwd up to its launch, flash_fwd.py:821-969): tile (the knob or the default
+ * rule), accumulation, kernel head dim and padding (in the kernel where it can, else on
+ * the host), the aligned fast path, workgroup order and split key ranges.  compute_units
+ * 0 reads the device's count; a positive value plans for such a device without touching
+ * one.  No counterpart in the reference's C++ (its policy is Python); the library's torch
+ * operator and any non-Python caller plan through it, and the Python package applies the
+ * same rules. */
+ta_status ta_plan_call(int64_t B, int64_t H, int64_t S, int64_t D, int32_t dtype, int32_t causal,
+                       int32_t device, int32_t compute_units, const ta_call_knobs* knobs,
+                       ta_call_plan* out);
+
 /* Unload every cached module on every device (compile_cache.reset_cache_for_tests). */
 ta_status ta_cache_reset(void);
 

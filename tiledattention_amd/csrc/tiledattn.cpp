@@ -645,6 +645,151 @@ ta_status launch_plan_locked(const ta_fwd_args* a, const LaunchPlan& pl, ta::Fwd
   return TA_OK;
 }
 
+// ---- call policy ------------------------------------------------------------------
+// What a call with given knobs runs: tile, accumulation, kernel head dim and padding, the
+// aligned fast path, workgroup order and split.  The rules restate the host policy of the
+// reference (flash_fwd.py:47-259, 851-921) with this build's gfx950 choices, and are the
+// same rules tiledattention/kernels/flash_fwd.py applies (a CPU test compares the two over
+// a grid of shapes and knob values).
+
+// Head dim of the kernel that runs `d`, and its zero padding: kernels exist for 64, 128,
+// 160 and 256, and 96 with fp32 accumulation on tiles of 64 or 128 keys (native_96); other
+// head dims pad up to the next (flash_fwd.py:149-163 pads to a power of two).
+bool kernel_head_dim(int64_t d, bool native_96, int* kd, int* pad) {
+  if (d <= 0) return false;
+  if (native_96 && d > 64 && d <= 96) {
+    *kd = 96;
+    *pad = (int)(96 - d);
+    return true;
+  }
+  for (int k : {64, 128, 160, 256}) {
+    if (d <= k) {
+      *kd = k;
+      *pad = (int)(k - d);
+      return true;
+    }
+  }
+  return false;
+}
+
+// Default tile when no tile is given: 128 query rows, or 64 when the 64-row blocks of every
+// head fit the compute units once (head dims up to 128, up to 160 with fp32 accumulation);
+// TILE_N 128 for non-causal D = 128 at S >= 2048, else 64 (the reference's rule,
+// flash_fwd.py:254-259).
+void default_tile(int64_t S, int64_t d, bool causal, int64_t n_bh, bool fp32, int ncu, int* tm, int* tn) {
+  *tn = (!causal && d == 128 && S >= 2048) ? 128 : 64;
+  const int64_t max_d64 = fp32 ? 160 : 128;
+  *tm = (d > 0 && d <= max_d64 && n_bh > 0 && S > 0 && n_bh * ((S + 63) / 64) <= ncu) ? 64 : 128;
+}
+
+// Workgroups of one launch resident on a CU: two for the non-causal eight-wave kernels at
+// D = 64 with fp32 accumulation, one for the other eight-wave kernels; for the four-wave
+// kernels two at (128, 64) with input-dtype accumulation, two at (64, 128) up to D = 128,
+// four at (64, 64) up to D = 128 and two above, one otherwise.
+int workgroups_per_cu(int tm, int tn, int accum, int d, bool causal) {
+  if (eight_wave_family(tm, tn, accum, d)) return (accum == TA_ACC_FP32 && d <= 64 && !causal) ? 2 : 1;
+  if (tm == 128 && tn == 64 && accum == TA_ACC_INPUT) return 2;
+  if (tm == 64 && tn == 128 && d <= 128) return 2;
+  if (tm == 64 && tn == 64) return d <= 128 ? 4 : 2;
+  return 1;
+}
+
+// Default workgroup order: XCD grouping when the grid splits evenly over the 8 XCDs; for
+// causal grids that are resident all at once, the heavy/light complementary order.
+int default_sched(int64_t n_blocks, bool causal, int tm, int tn, int accum, int d, int ncu) {
+  if (n_blocks % 8 != 0) return 0;
+  const int64_t resident = (int64_t)ncu * workgroups_per_cu(tm, tn, accum, d, causal);
+  return (causal && n_blocks <= resident) ? 2 : 1;
+}
+
+ta_status plan_call(int64_t B, int64_t H, int64_t S, int64_t D, int32_t dtype, int32_t causal,
+                    int32_t device, int ncu, const ta_call_knobs* k, ta_call_plan* out) {
+  if (dtype != TA_FP16 && dtype != TA_BF16) return fail(TA_EINVAL, "dtype %d", dtype);
+  if (causal != 0 && causal != 1) return fail(TA_EINVAL, "causal %d", causal);
+  if (B < 0 || H < 0 || S < 0) return fail(TA_EINVAL, "negative shape");
+  if ((k->tile_m == 0) != (k->tile_n == 0))
+    return fail(TA_EINVAL, "tile_m and tile_n must both be 0 (default) or both be given");
+  if (k->accum != -1 && k->accum != TA_ACC_FP32 && k->accum != TA_ACC_INPUT)
+    return fail(TA_EINVAL, "accum %d", k->accum);
+  if (k->sched < -1 || k->sched > 3) return fail(TA_EINVAL, "sched %d", k->sched);
+  if (k->split < 0 && k->split != TA_SPLIT_AUTO && k->split != TA_SPLIT_PAIRS)
+    return fail(TA_EINVAL, "split %d", k->split);
+  if (D <= 0) return fail(TA_EINVAL, "head dimension D must be positive");
+  const int64_t n_bh = B * H;
+  const bool cz = causal != 0;
+  const int accum = k->accum == TA_ACC_INPUT ? TA_ACC_INPUT : TA_ACC_FP32;  // auto: fp32 on gfx950
+  const bool explicit_tile = k->tile_m != 0;
+  int tm = k->tile_m, tn = k->tile_n;
+  if (explicit_tile) {
+    if (!valid_tile(tm) || !valid_tile(tn))
+      return fail(TA_EUNSUPPORTED, "tile (%d, %d) (supported: 64 or 128 each)", tm, tn);
+  } else {
+    default_tile(S, D, cz, n_bh, accum == TA_ACC_FP32, ncu, &tm, &tn);
+    // Keep 128 rows where the 128-row kernel would split key ranges (split kernels exist
+    // for fp32 accumulation only).
+    if (tm == 64 && accum == TA_ACC_FP32 && k->split != 0) {
+      if (k->split != TA_SPLIT_AUTO) {
+        tm = 128;
+      } else {
+        int kd = 0, pad = 0;
+        if (kernel_head_dim(D, true, &kd, &pad) && plan_split(S, n_bh, cz, ncu) != 0) tm = 128;
+      }
+    }
+  }
+  int kd = 0, pad = 0;
+  if (!kernel_head_dim(D, (tn == 64 || tn == 128) && accum == TA_ACC_FP32, &kd, &pad))
+    return fail(TA_EUNSUPPORTED, "head dimension D=%lld is not supported: the gfx950 kernels cover D <= 256",
+                (long long)D);
+  if (kd > 128 && tn != 64) {
+    if (explicit_tile)
+      return fail(TA_EUNSUPPORTED, "TILE_N=%d is not supported for head dimension D=%lld: head dims above 128 run with TILE_N=64",
+                  tn, (long long)D);
+    tn = 64;
+  }
+  ta_status st = check_shape(kd, tm, tn, accum);
+  if (st != TA_OK) return st;
+  const bool in_place = pad > 0 && D % 8 == 0 && eight_wave_family(tm, tn, accum, kd);
+  memset(out, 0, sizeof(*out));
+  ta_fwd_args& a = out->args;
+  a.B = B;
+  a.H = H;
+  a.S = S;
+  a.D = kd;
+  a.causal = causal;
+  a.dtype = dtype;
+  a.tile_m = tm;
+  a.tile_n = tn;
+  a.accum = accum;
+  a.device = device;
+  a.d_real = in_place ? (int32_t)D : 0;
+  a.aligned = (k->aligned && S % tm == 0 && S % tn == 0) ? 1 : 0;
+  const int64_t n_qblk = (S + tm - 1) / tm;
+  a.sched = k->sched >= 0 ? k->sched : default_sched(n_bh * n_qblk, cz, tm, tn, accum, kd, ncu);
+  out->host_pad = in_place ? 0 : pad;
+  out->out_width = in_place ? (int32_t)D : kd;
+  if (n_bh == 0 || S == 0) return TA_OK;
+  // Split: the dispatch model (auto), a forced chunk length or the paired split.
+  const bool capable = split_capable(&a);
+  int32_t chunk = 0;
+  if (k->split == TA_SPLIT_AUTO) {
+    chunk = capable ? plan_split(S, n_bh, cz, ncu) : 0;
+  } else if (k->split != 0) {
+    if (!capable)
+      return fail(TA_EUNSUPPORTED,
+                  "split key ranges need tile (128, 64) or (128, 128), fp32 accumulation and a head dim of at most 160");
+    chunk = k->split;
+  }
+  out->chunk_steps = chunk;
+  if (chunk != 0) {
+    SplitLayout l;
+    if (layout_for(S, cz, chunk, &l)) {
+      out->workspace_bytes = split_ws_bytes(n_bh, kd, l);
+      if (k->sched < 0) a.sched = 1;  // the split grid regroups per XCD whenever it divides evenly
+    }
+  }
+  return TA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -729,6 +874,23 @@ ta_status ta_sdpa_fwd(const ta_fwd_args* a, void* stream) {
   ta_status st = plan_launch(a, n_bh, n_qblk, 0, ncu, &pl);
   if (st != TA_OK) return st;
   return launch_plan_locked(a, pl, &p, stream);
+}
+
+ta_status ta_plan_call(int64_t B, int64_t H, int64_t S, int64_t D, int32_t dtype, int32_t causal,
+                       int32_t device, int32_t compute_units, const ta_call_knobs* knobs,
+                       ta_call_plan* out) {
+  if (knobs == nullptr || out == nullptr) return fail(TA_EINVAL, "knobs or out is NULL");
+  int ncu = compute_units;
+  if (ncu == 0) {
+    std::lock_guard<std::mutex> lock(g_mu);
+    DeviceGuard guard(device);
+    if (guard.err != hipSuccess)
+      return fail(TA_EHIP, "set device %d: %s", device, hipGetErrorString(guard.err));
+    ta_status cst = cu_count_locked(device, &ncu);
+    if (cst != TA_OK) return cst;
+  }
+  if (ncu <= 0) return fail(TA_EINVAL, "compute_units %d", ncu);
+  return plan_call(B, H, S, D, dtype, causal, device, ncu, knobs, out);
 }
 
 ta_status ta_describe_launch_model(const ta_fwd_args* args, int32_t chunk_steps,
