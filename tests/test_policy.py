@@ -312,7 +312,7 @@ def test_split_preference_needs_fp32_accumulation(monkeypatch):
     lib = _lib.load()
     assert lib.ta_split_plan_model(16384, 1, 1, 256) != 0
     monkeypatch.delenv("TILEDATTN_SPLIT", raising=False)
-    assert ff._split_preferred(lib, None, 1, 1, 16384, 128, True, None, "fp16") is False
+    assert ff._split_preferred(lib, 1, 1, 16384, 128, True, 256, "fp16") is False
     monkeypatch.setenv("TILEDATTN_SPLIT", "4")  # forced: fp32 prefers the split tile
-    assert ff._split_preferred(lib, None, 1, 1, 16384, 128, True, None, "fp32") is True
-    assert ff._split_preferred(lib, None, 1, 1, 16384, 128, True, None, "fp16") is False
+    assert ff._split_preferred(lib, 1, 1, 16384, 128, True, 256, "fp32") is True
+    assert ff._split_preferred(lib, 1, 1, 16384, 128, True, 256, "fp16") is False

@@ -30,6 +30,7 @@ TA_BF16 = 1
 TA_ACC_FP32 = 0
 TA_ACC_INPUT = 1
 TA_SPLIT_PAIRS = -1  # chunk length of the paired split
+TA_SPLIT_AUTO = -2   # chunk length chosen by the dispatch model
 
 TILE_SHAPES = ((64, 64), (64, 128), (128, 64), (128, 128))
 STATIC_SCRATCH_BYTES = 64 << 20  # TA_STATIC_SCRATCH_BYTES
@@ -55,6 +56,7 @@ EXPORTED_SYMBOLS = (
     "ta_sdpa_fwd_split_static",
     "ta_describe_launch",
     "ta_describe_launch_model",
+    "ta_plan_call",
     "ta_cache_reset",
     "ta_cache_size",
     "ta_last_error",
@@ -121,6 +123,21 @@ class LaunchDesc(ctypes.Structure):
             val = getattr(self, name)
             out[name] = val.decode() if isinstance(val, bytes) else int(val)
         return out
+
+
+class CallKnobs(ctypes.Structure):
+    """Mirror of ``ta_call_knobs``."""
+
+    _fields_ = [("tile_m", ctypes.c_int32), ("tile_n", ctypes.c_int32), ("accum", ctypes.c_int32),
+                ("aligned", ctypes.c_int32), ("sched", ctypes.c_int32), ("split", ctypes.c_int32)]
+
+
+class CallPlan(ctypes.Structure):
+    """Mirror of ``ta_call_plan``."""
+
+    _fields_ = [("args", FwdArgs), ("chunk_steps", ctypes.c_int32), ("host_pad", ctypes.c_int32),
+                ("out_width", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("workspace_bytes", ctypes.c_int64)]
 
 
 def shape_args(*, B: int = 1, H: int = 1, S: int = 128, D: int = 128, causal: bool = False,
@@ -208,6 +225,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ta_describe_launch.restype = i32
     lib.ta_describe_launch_model.argtypes = [ctypes.POINTER(FwdArgs), i32, i32, ctypes.POINTER(LaunchDesc)]
     lib.ta_describe_launch_model.restype = i32
+    lib.ta_plan_call.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, i32, i32, i32,
+                                 i32, ctypes.POINTER(CallKnobs), ctypes.POINTER(CallPlan)]
+    lib.ta_plan_call.restype = i32
     lib.ta_cache_reset.argtypes = []
     lib.ta_cache_reset.restype = i32
     lib.ta_cache_size.argtypes = []

@@ -375,19 +375,26 @@ def _split_capable(*, tile_m: int, tile_n: int, accum_code: int, kernel_head_dim
                           kernel_head_dim=kernel_head_dim)[1]
 
 
-def _resolve_split(lib, args: _lib.FwdArgs, *, capable: bool) -> int:
+def _resolve_split(lib, args: _lib.FwdArgs, *, capable: bool, compute_units: int = 0) -> int:
     """``TILEDATTN_SPLIT`` -> chunk length in 128-key steps (0 = whole rows,
-    ``_lib.TA_SPLIT_PAIRS`` = the paired split)."""
+    ``_lib.TA_SPLIT_PAIRS`` = the paired split).  ``auto`` asks the library's dispatch
+    model for a device of ``compute_units`` CUs (``ta_split_plan_model``), or for the
+    arguments' device when 0 (``ta_split_plan``)."""
     raw = os.getenv("TILEDATTN_SPLIT", "").strip().lower()
     if raw in ("", "auto"):
         if not capable:
             return 0
-        key = (int(args.S), int(args.B * args.H), int(args.causal), int(args.device))
+        key = (int(args.S), int(args.B * args.H), int(args.causal), int(compute_units) or -1 - int(args.device))
         chunk = _SPLIT_PLANS.get(key)
         if chunk is None:
-            out = ctypes.c_int32(0)
-            _raise_for_status(lib, lib.ta_split_plan(ctypes.byref(args), ctypes.byref(out)))
-            chunk = _SPLIT_PLANS[key] = int(out.value)
+            if compute_units:
+                chunk = int(lib.ta_split_plan_model(int(args.S), int(args.B * args.H), int(args.causal),
+                                                    int(compute_units)))
+            else:
+                out = ctypes.c_int32(0)
+                _raise_for_status(lib, lib.ta_split_plan(ctypes.byref(args), ctypes.byref(out)))
+                chunk = int(out.value)
+            _SPLIT_PLANS[key] = chunk
         return chunk
     if raw in ("0", "off"):
         return 0
@@ -413,8 +420,8 @@ def _resolve_split(lib, args: _lib.FwdArgs, *, capable: bool) -> int:
     return chunk
 
 
-def _split_preferred(lib, q, batch: int, heads: int, seq_len: int, head_dim: int, causal: bool,
-                     torch_mod, accum_mode: str = "fp32") -> bool:
+def _split_preferred(lib, batch: int, heads: int, seq_len: int, head_dim: int, causal: bool,
+                     compute_units: int, accum_mode: str = "fp32") -> bool:
     """Whether the 128-row kernel runs split key ranges for this shape (a forced chunk
     length, or the library's dispatch model under ``TILEDATTN_SPLIT=auto``): the default
     tile then stays at 128 rows, the tile the split path exists for.  Split kernels exist
@@ -428,14 +435,8 @@ def _split_preferred(lib, q, batch: int, heads: int, seq_len: int, head_dim: int
     if raw not in ("", "auto"):
         return True
     kernel_head_dim, _ = _resolve_kernel_head_dim_gfx950(head_dim, native_96=True)
-    args = _lib.FwdArgs()
-    args.B, args.H, args.S, args.D = batch, heads, seq_len, kernel_head_dim
-    args.causal = int(causal)
-    args.dtype = _dtype_code_for_torch_dtype(q.dtype)
-    args.tile_m, args.tile_n = 128, 64
-    args.accum = _lib.TA_ACC_FP32
-    args.device = _device_index(torch_mod, q)
-    return _resolve_split(lib, args, capable=True) != 0
+    args = _lib.shape_args(B=batch, H=heads, S=seq_len, D=kernel_head_dim, causal=causal)
+    return _resolve_split(lib, args, capable=True, compute_units=compute_units) != 0
 
 
 def _raise_for_status(lib, status: int) -> None:
@@ -530,6 +531,111 @@ def _raw_stream(torch_mod, device_index: int) -> int:
     return int(torch_mod.cuda.current_stream(device_index).cuda_stream)
 
 
+def _call_knobs(tile: tuple[int, int] | None = None, accum: str | None = None) -> _lib.CallKnobs:
+    """The knob values of a call as ``ta_call_knobs`` (the library's ``ta_plan_call``):
+    parsed from the ``TILEDATTN_*`` environment exactly as this module parses them, with
+    ``tile`` / ``accum`` taking the place of the tile and accumulation knobs when given."""
+    k = _lib.CallKnobs()
+    if tile is not None:
+        k.tile_m, k.tile_n = int(tile[0]), int(tile[1])
+    elif os.getenv("TILEDATTN_TILE_M") or os.getenv("TILEDATTN_TILE_N"):
+        k.tile_m, k.tile_n = _resolve_tile_config()
+    if accum is None:
+        raw = (os.getenv("TILEDATTN_ACCUM_MODE") or "").strip().lower()
+        accum = None if raw in ("", "auto") else _resolve_accum_mode(seq_len=0, head_dim=0, causal=False)
+    k.accum = -1 if accum is None else (_lib.TA_ACC_INPUT if accum == "fp16" else _lib.TA_ACC_FP32)
+    k.aligned = 0 if _aligned_fastpath_disabled() else 1
+    raw = os.getenv("TILEDATTN_SCHED", "").strip()
+    k.sched = -1 if raw == "" else int(raw)
+    raw = os.getenv("TILEDATTN_SPLIT", "").strip().lower()
+    k.split = (_lib.TA_SPLIT_AUTO if raw in ("", "auto") else 0 if raw in ("0", "off")
+               else _lib.TA_SPLIT_PAIRS if raw == "pairs" else int(raw))
+    return k
+
+
+class _CallPolicy:
+    """The resolved policy of one call, independent of tensor addresses and strides."""
+
+    __slots__ = ("accum_mode", "accum_code", "tile_m", "tile_n", "explicit_tile", "chunk_plan",
+                 "kernel_head_dim", "pad_dim", "pad_in_kernel", "width", "aligned", "sched", "chunk",
+                 "ws_bytes")
+
+
+def _resolve_call(lib, *, batch: int, heads: int, seq_len: int, head_dim: int, dtype_code: int,
+                  causal: bool, compute_units: int, tile: tuple[int, int] | None = None,
+                  accum: str | None = None, device_index: int = 0) -> _CallPolicy:
+    """Knobs and policies of a call (flash_fwd.py:821-921) for a device of ``compute_units``
+    CUs: accumulation, tile, kernel head dim and padding, aligned fast path, workgroup order
+    and split.  Needs no tensors and no device.  The library's ``ta_plan_call`` applies the
+    same rules for callers outside Python (the C++ operator); tests compare the two."""
+    if accum is not None:
+        if accum not in ("fp32", "fp16"):
+            raise ValueError(f"Unsupported accumulation mode {accum!r}. Use fp32 or fp16.")
+        accum_mode = accum
+    else:
+        accum_mode = _resolve_accum_mode(seq_len=seq_len, head_dim=head_dim, causal=causal)
+    bh = batch * heads
+    pol = _CallPolicy()
+    pol.accum_mode = accum_mode
+    pol.explicit_tile = tile is not None or bool(os.getenv("TILEDATTN_TILE_M") or os.getenv("TILEDATTN_TILE_N"))
+    if tile is not None:
+        tile_m, tile_n = int(tile[0]), int(tile[1])
+        _check_tile_supported(tile_m, tile_n)
+    elif pol.explicit_tile:
+        tile_m, tile_n = _resolve_tile_config()
+        _check_tile_supported(tile_m, tile_n)
+    else:
+        tile_m, tile_n = _default_tile_config_for_shape_gfx950(
+            seq_len=seq_len, head_dim=head_dim, causal=causal, n_bh=bh, accum_mode=accum_mode,
+            compute_units=compute_units,
+        )
+        if tile_m == 64 and _split_preferred(lib, batch, heads, seq_len, head_dim, causal, compute_units,
+                                             accum_mode):
+            tile_m = 128
+
+    pol.chunk_plan = _resolve_chunk_plan(head_dim)
+    kernel_head_dim, pad_dim = _resolve_kernel_head_dim_gfx950(
+        head_dim, native_96=tile_n in (64, 128) and accum_mode == "fp32")
+    if kernel_head_dim > 128 and tile_n != _WIDE_HEAD_DIM_TILE_N:
+        if pol.explicit_tile:
+            raise ValueError(
+                f"TILEDATTN_TILE_N={tile_n} is not supported for head dimension D={head_dim} "
+                f"on gfx950: head dims above 128 run with TILE_N=64."
+            )
+        tile_n = _WIDE_HEAD_DIM_TILE_N
+    accum_code = _lib.TA_ACC_INPUT if accum_mode == "fp16" else _lib.TA_ACC_FP32
+    # A narrower head dim that is a multiple of 8 runs in place on the eight-wave kernel
+    # (ta_fwd_args.d_real: missing columns read as zero, not written); others are zero-padded
+    # on the host as the reference does (flash_fwd.py:868-872) and the output is sliced.
+    pol.pad_in_kernel = pad_dim > 0 and head_dim % 8 == 0 and _eight_wave_kernel(
+        tile_m=tile_m, tile_n=tile_n, accum_code=accum_code, kernel_head_dim=kernel_head_dim)
+    pol.pad_dim = pad_dim
+    pol.width = head_dim if pol.pad_in_kernel else kernel_head_dim
+    pol.tile_m, pol.tile_n, pol.kernel_head_dim, pol.accum_code = tile_m, tile_n, kernel_head_dim, accum_code
+    pol.aligned = int(_use_unmasked_tail_kernel(seq_len=seq_len, tile_m=tile_m, tile_n=tile_n))
+    n_qblk = (seq_len + tile_m - 1) // tile_m
+    pol.sched = _resolve_sched(n_blocks=bh * n_qblk, causal=causal, tile_m=tile_m, tile_n=tile_n,
+                               accum_code=accum_code, head_dim=kernel_head_dim, compute_units=compute_units)
+    pol.chunk, pol.ws_bytes = 0, 0
+    if bh == 0 or seq_len == 0:
+        return pol
+    args = _lib.shape_args(B=batch, H=heads, S=seq_len, D=kernel_head_dim, causal=causal, dtype=dtype_code,
+                           tile_m=tile_m, tile_n=tile_n, accum=accum_code, sched=pol.sched,
+                           aligned=pol.aligned, d_real=head_dim if pol.pad_in_kernel else 0,
+                           device=device_index)
+    capable = _split_capable(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code,
+                             kernel_head_dim=kernel_head_dim)
+    pol.chunk = _resolve_split(lib, args, capable=capable, compute_units=compute_units)
+    if pol.chunk:
+        ws_bytes = ctypes.c_int64(0)
+        _raise_for_status(lib, lib.ta_split_workspace_size(ctypes.byref(args), pol.chunk,
+                                                           ctypes.byref(ws_bytes)))
+        pol.ws_bytes = int(ws_bytes.value)
+        if pol.ws_bytes and not os.getenv("TILEDATTN_SCHED", "").strip():
+            pol.sched = 1  # the split grid regroups per XCD whenever it divides evenly
+    return pol
+
+
 def _build_plan(torch_mod, lib, q, k, v, causal: bool, tile: tuple[int, int] | None = None,
                 accum: str | None = None) -> _LaunchPlan:
     """Resolve knobs and policies for a call (flash_fwd.py:821-969), up to the launch.
@@ -539,70 +645,34 @@ def _build_plan(torch_mod, lib, q, k, v, causal: bool, tile: tuple[int, int] | N
     sync_mode = _resolve_sync_mode()
 
     batch, heads, seq_len, head_dim = map(int, q.shape)
-    if accum is not None:
-        if accum not in ("fp32", "fp16"):
-            raise ValueError(f"Unsupported accumulation mode {accum!r}. Use fp32 or fp16.")
-        accum_mode = accum
-    else:
-        accum_mode = _resolve_accum_mode(seq_len=seq_len, head_dim=head_dim, causal=causal)
-    bh = batch * heads
-    explicit_tile = tile is not None or bool(os.getenv("TILEDATTN_TILE_M") or os.getenv("TILEDATTN_TILE_N"))
-    if tile is not None:
-        tile_m, tile_n = int(tile[0]), int(tile[1])
-        _check_tile_supported(tile_m, tile_n)
-    elif explicit_tile:
-        tile_m, tile_n = _resolve_tile_config()
-        _check_tile_supported(tile_m, tile_n)
-    else:
-        tile_m, tile_n = _default_tile_config_for_shape_gfx950(
-            seq_len=seq_len, head_dim=head_dim, causal=causal, n_bh=bh, accum_mode=accum_mode,
-            compute_units=_compute_units(torch_mod, _device_index(torch_mod, q)),
-        )
-        if tile_m == 64 and _split_preferred(lib, q, batch, heads, seq_len, head_dim, causal, torch_mod,
-                                             accum_mode):
-            tile_m = 128
-
-    chunk_plan = _resolve_chunk_plan(head_dim)
-    kernel_head_dim, pad_dim = _resolve_kernel_head_dim_gfx950(
-        head_dim, native_96=tile_n in (64, 128) and accum_mode == "fp32")
-    if kernel_head_dim > 128 and tile_n != _WIDE_HEAD_DIM_TILE_N:
-        if explicit_tile:
-            raise ValueError(
-                f"TILEDATTN_TILE_N={tile_n} is not supported for head dimension D={head_dim} "
-                f"on gfx950: head dims above 128 run with TILE_N=64."
-            )
-        tile_n = _WIDE_HEAD_DIM_TILE_N
     dtype_code = _dtype_code_for_torch_dtype(q.dtype)
-    accum_code = _lib.TA_ACC_INPUT if accum_mode == "fp16" else _lib.TA_ACC_FP32
-    # A narrower head dim that is a multiple of 8 runs in place on the eight-wave kernel
-    # (ta_fwd_args.d_real: missing columns read as zero, not written); others are zero-padded
-    # on the host as the reference does (flash_fwd.py:868-872) and the output is sliced.
-    pad_in_kernel = pad_dim > 0 and head_dim % 8 == 0 and _eight_wave_kernel(
-        tile_m=tile_m, tile_n=tile_n, accum_code=accum_code, kernel_head_dim=kernel_head_dim)
-    width = head_dim if pad_in_kernel else kernel_head_dim
+    device_index = _device_index(torch_mod, q)
+    pol = _resolve_call(lib, batch=batch, heads=heads, seq_len=seq_len, head_dim=head_dim,
+                        dtype_code=dtype_code, causal=causal, tile=tile, accum=accum,
+                        compute_units=_compute_units(torch_mod, device_index), device_index=device_index)
+    tile_m, tile_n, kernel_head_dim, width = pol.tile_m, pol.tile_n, pol.kernel_head_dim, pol.width
 
     plan = _LaunchPlan()
     plan.generation = _compile_cache.generation()
     plan.device = q.device
     plan.dtype = q.dtype
     plan.head_dim = head_dim
-    plan.pad_dim = 0 if pad_in_kernel else pad_dim
+    plan.pad_dim = 0 if pol.pad_in_kernel else pol.pad_dim
     plan.width = width
     plan.out_shape = (batch, heads, seq_len, width)
     plan.out_like_q = width == head_dim
     plan.sync_mode = sync_mode
-    plan.empty = bh == 0 or seq_len == 0
+    plan.empty = batch * heads == 0 or seq_len == 0
     if plan.empty:
         return plan
 
-    aligned = int(_use_unmasked_tail_kernel(seq_len=seq_len, tile_m=tile_m, tile_n=tile_n))
-    if chunk_plan is not None:
+    aligned = pol.aligned
+    if pol.chunk_plan is not None:
         kernel_variant = "chunked"
     elif aligned:
         kernel_variant = "direct_aligned"
     else:
         kernel_variant = "direct"
-    device_index = _device_index(torch_mod, q)
     plan.device_index = device_index
 
     kernel_key = (
@@ -612,50 +682,31 @@ def _build_plan(torch_mod, lib, q, k, v, causal: bool, tile: tuple[int, int] | N
         kernel_variant,
         str(q.dtype),
         causal,
-        accum_mode,
+        pol.accum_mode,
         opt_level,
         occupancy if occupancy is not None else -1,
         num_ctas if num_ctas is not None else -1,
         aligned,
         device_index,
     )
-    config = (dtype_code, kernel_head_dim, tile_m, tile_n, int(causal), accum_code, aligned)
+    config = (dtype_code, kernel_head_dim, tile_m, tile_n, int(causal), pol.accum_code, aligned)
     plan.kernel = get_kernel(kernel_key, lambda: _Launcher(lib, device_index, config))
 
     # Which inputs the kernel cannot read in place (host padding or strides); addresses are
     # checked per call.
     plan.copy = tuple(plan.pad_dim > 0 or not _strides_ok(t.stride(), t.shape, width)
                       for t in (q, k, v))
-    n_qblk = (seq_len + tile_m - 1) // tile_m
-    args = _lib.FwdArgs()
-    args.B, args.H, args.S, args.D = batch, heads, seq_len, kernel_head_dim
-    args.d_real = head_dim if pad_in_kernel else 0
-    args.aligned = aligned
+    args = _lib.shape_args(B=batch, H=heads, S=seq_len, D=kernel_head_dim, causal=causal, dtype=dtype_code,
+                           tile_m=tile_m, tile_n=tile_n, accum=pol.accum_code, sched=pol.sched,
+                           aligned=aligned, d_real=head_dim if pol.pad_in_kernel else 0,
+                           device=device_index)
     contiguous = (heads * seq_len * width, seq_len * width, width, 1)
     for name, t, cp in (("q_stride", q, plan.copy[0]), ("k_stride", k, plan.copy[1]),
                         ("v_stride", v, plan.copy[2])):
         getattr(args, name)[:] = contiguous if cp else tuple(t.stride())
     args.o_stride[:] = contiguous
-    args.causal = int(causal)
-    args.dtype = dtype_code
-    args.tile_m, args.tile_n = tile_m, tile_n
-    args.accum = accum_code
-    args.device = device_index
-    args.sched = _resolve_sched(n_blocks=bh * n_qblk, causal=causal, tile_m=tile_m, tile_n=tile_n,
-                                accum_code=accum_code, head_dim=kernel_head_dim,
-                                compute_units=_compute_units(torch_mod, device_index))
-
-    capable = _split_capable(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code,
-                             kernel_head_dim=kernel_head_dim)
-    plan.chunk = _resolve_split(lib, args, capable=capable)
-    plan.ws_bytes = 0
-    if plan.chunk:
-        ws_bytes = ctypes.c_int64(0)
-        _raise_for_status(lib, lib.ta_split_workspace_size(ctypes.byref(args), plan.chunk,
-                                                           ctypes.byref(ws_bytes)))
-        plan.ws_bytes = int(ws_bytes.value)
-        if plan.ws_bytes and not os.getenv("TILEDATTN_SCHED", "").strip():
-            args.sched = 1  # the split grid regroups per XCD whenever it divides evenly
+    plan.chunk = pol.chunk
+    plan.ws_bytes = pol.ws_bytes
     plan.args = args
     return plan
 
