@@ -75,3 +75,15 @@ def test_overrides_map_to_run_flash_fwd_keywords():
     assert torch_op._overrides(64, 128, -1) == {"tile": (64, 128)}
     assert torch_op._overrides(0, 0, 1) == {"accum": "fp16"}
     assert torch_op._overrides(128, 64, 0) == {"tile": (128, 64), "accum": "fp32"}
+
+
+def test_operator_kernel_is_the_cpp_library():
+    """The schema and the GPU kernel are registered by libtiledattn_torch.so (C++), the fake
+    (Meta) kernel by this package: libtorch callers reach the operator without Python."""
+    dump = torch._C._dispatch_dump("tiledattention::sdpa_fwd")
+    lines = {ln.split(":", 1)[0]: ln for ln in dump.splitlines() if ":" in ln}
+    assert "torch_ext.cpp" in lines["debug"]
+    assert "torch_ext.cpp" in lines["CUDA"]
+    assert "torch_ext.cpp" not in lines["Meta"]
+    assert torch._C._dispatch_has_kernel_for_dispatch_key("tiledattention::sdpa_fwd", "CUDA")
+    assert not torch._C._dispatch_has_kernel_for_dispatch_key("tiledattention::sdpa_fwd", "CPU")

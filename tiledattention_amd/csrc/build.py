@@ -9,7 +9,9 @@ Outputs (into ``tiledattention_amd/lib/`` unless told otherwise):
   serve the (128, 64) tile shape with fp32 accumulation, from ``attn_fwd_pp.hip``;
 * ``libtiledattn.so``: the host library implementing ``include/tiledattn.h``, linked from
   ``tiledattn.cpp`` (g++) and ``tiledattn_static.hip`` (hipcc; the static device scratch of
-  ``ta_sdpa_fwd_split_static``).
+  ``ta_sdpa_fwd_split_static``);
+* ``libtiledattn_torch.so``: the C++ torch operator ``tiledattention::sdpa_fwd``
+  (``torch_ext.cpp``, g++ against the installed torch), linked to ``libtiledattn.so``.
 
 Run as ``python -m tiledattention_amd.csrc.build``.
 """
@@ -110,11 +112,52 @@ def library_cmd(out_dir: Path, static_obj: Path) -> list[str]:
     ]
 
 
+def torch_ext_cmd(out_dir: Path) -> list[str]:
+    """The C++ torch operator (torch.ops.tiledattention.sdpa_fwd) over the C ABI, linked
+    against the installed torch and libtiledattn.so beside it."""
+    import torch
+    from torch.utils import cpp_extension
+
+    tlib = Path(torch.__file__).resolve().parent / "lib"
+    abi = int(bool(getattr(torch._C, "_GLIBCXX_USE_CXX11_ABI", True)))
+    return [
+        os.environ.get("CXX", "g++"),
+        "-O2",
+        "-std=c++17",
+        "-fPIC",
+        "-shared",
+        "-Wall",
+        "-D__HIP_PLATFORM_AMD__",
+        "-DUSE_ROCM",
+        f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+        *[f"-I{p}" for p in cpp_extension.include_paths()],
+        f"-I{ROCM / 'include'}",
+        f"-I{REPO / 'include'}",
+        "-o",
+        str(out_dir / "libtiledattn_torch.so"),
+        str(HERE / "torch_ext.cpp"),
+        f"-L{tlib}",
+        f"-Wl,-rpath,{tlib}",
+        "-ltorch",
+        "-ltorch_cpu",
+        "-lc10",
+        "-lc10_hip",
+        "-ltorch_hip",
+        f"-L{out_dir}",
+        "-ltiledattn",
+        "-Wl,-rpath,$ORIGIN",
+        f"-L{ROCM / 'lib'}",
+        f"-Wl,-rpath,{ROCM / 'lib'}",
+        "-lamdhip64",
+    ]
+
+
 def _build_library(out_dir: Path) -> None:
     with tempfile.TemporaryDirectory(prefix="tiledattn_build_") as tmp:
         obj = Path(tmp) / "tiledattn_static.o"
         _run(static_object_cmd(obj))
         _run(library_cmd(out_dir, obj))
+    _run(torch_ext_cmd(out_dir))
 
 
 def build(out_dir: Path | None = None, jobs: int | None = None) -> Path:

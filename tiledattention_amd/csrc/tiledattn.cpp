@@ -373,6 +373,20 @@ int32_t plan_split(int64_t S, int64_t n_bh, bool causal, int ncu) {
   return best_c;
 }
 
+// plan_split memoised per (S, B*H, causal, CUs): the dispatch model runs once per shape.
+int32_t cached_split_plan(int64_t S, int64_t n_bh, bool causal, int ncu) {
+  {
+    std::lock_guard<std::mutex> lock(g_mu);
+    auto it = g_plans.find(std::make_tuple(S, n_bh, (int)causal, ncu));
+    if (it != g_plans.end()) return it->second;
+  }
+  // The model runs without the lock; two threads planning one shape compute the same value.
+  const int32_t c = plan_split(S, n_bh, causal, ncu);
+  std::lock_guard<std::mutex> lock(g_mu);
+  g_plans.emplace(std::make_tuple(S, n_bh, (int)causal, ncu), c);
+  return c;
+}
+
 // Checks shared by every entry point that takes ta_fwd_args.  Fills the grid size.  The
 // planning queries (launch = false) need only the shape fields, not tensors or strides.
 ta_status validate_args(const ta_fwd_args* a, int64_t* n_bh_out, int64_t* n_qblk_out,
@@ -732,7 +746,7 @@ ta_status plan_call(int64_t B, int64_t H, int64_t S, int64_t D, int32_t dtype, i
         tm = 128;
       } else {
         int kd = 0, pad = 0;
-        if (kernel_head_dim(D, true, &kd, &pad) && plan_split(S, n_bh, cz, ncu) != 0) tm = 128;
+        if (kernel_head_dim(D, true, &kd, &pad) && cached_split_plan(S, n_bh, cz, ncu) != 0) tm = 128;
       }
     }
   }
@@ -772,7 +786,7 @@ ta_status plan_call(int64_t B, int64_t H, int64_t S, int64_t D, int32_t dtype, i
   const bool capable = split_capable(&a);
   int32_t chunk = 0;
   if (k->split == TA_SPLIT_AUTO) {
-    chunk = capable ? plan_split(S, n_bh, cz, ncu) : 0;
+    chunk = capable ? cached_split_plan(S, n_bh, cz, ncu) : 0;
   } else if (k->split != 0) {
     if (!capable)
       return fail(TA_EUNSUPPORTED,
@@ -926,18 +940,8 @@ ta_status ta_split_plan(const ta_fwd_args* a, int32_t* chunk_steps) {
       return fail(TA_EHIP, "set device %d: %s", a->device, hipGetErrorString(guard.err));
     ta_status cst = cu_count_locked(a->device, &ncu);
     if (cst != TA_OK) return cst;
-    auto it = g_plans.find(std::make_tuple(a->S, n_bh, (int)a->causal, ncu));
-    if (it != g_plans.end()) {
-      *chunk_steps = it->second;
-      return TA_OK;
-    }
   }
-  // The dispatch model runs without the lock (milliseconds on a shape's first use); two
-  // threads planning the same shape compute the same value.
-  const int32_t c = plan_split(a->S, n_bh, a->causal != 0, ncu);
-  std::lock_guard<std::mutex> lock(g_mu);
-  g_plans.emplace(std::make_tuple(a->S, n_bh, (int)a->causal, ncu), c);
-  *chunk_steps = c;
+  *chunk_steps = cached_split_plan(a->S, n_bh, a->causal != 0, ncu);
   return TA_OK;
 }
 
