@@ -92,8 +92,18 @@ def test_cpp_operator_equals_sdpa(gpu, monkeypatch, knobs):
         if i == 2:  # a [B,S,H,D] tensor viewed as [B,H,S,D]
             q, k, v = (t.transpose(1, 2).contiguous().transpose(1, 2) for t in (q, k, v))
         say(f"C++ operator vs sdpa {shape} causal={causal} knobs={knobs}")
-        got = torch.ops.tiledattention.sdpa_fwd(q, k, v, causal, None)
-        ref = sdpa(q, k, v, causal=causal)
+        errors = []
+        try:
+            got = torch.ops.tiledattention.sdpa_fwd(q, k, v, causal, None)
+        except (RuntimeError, ValueError) as exc:
+            errors.append(exc)
+        try:
+            ref = sdpa(q, k, v, causal=causal)
+        except (RuntimeError, ValueError) as exc:  # the tile knob without a kernel for this D
+            errors.append(exc)
+        assert len(errors) in (0, 2), errors  # both reject, or both run
+        if errors:
+            continue
         torch.cuda.synchronize()
         assert got.shape == ref.shape and got.is_contiguous()
         assert torch.equal(got, ref), (shape, float((got.float() - ref.float()).abs().max()))
