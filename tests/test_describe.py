@@ -84,7 +84,7 @@ def test_whole_row_kernel_per_configuration(lib, objects, dtype, tiles, accum, d
             assert desc.grid == -(-s // tm) and desc.rows == tm
             assert desc.block == (512 if eight else 2 * tm)
             assert desc.in_place_pad == int(eight)
-            assert desc.split_capable == int(accum == _lib.TA_ACC_FP32 and tm == 128 and d <= 160)
+            assert desc.split_capable == int(accum == _lib.TA_ACC_FP32 and d <= 160 and (tm == 128 or d != 256))
             assert desc.merge_kernel == b"" and desc.workspace_bytes == 0
 
 
@@ -186,9 +186,33 @@ def test_paired_split_and_chunks_that_split_nothing(lib):
 
 def test_split_on_a_configuration_without_split_kernels(lib):
     with pytest.raises(ValueError, match="TA_EUNSUPPORTED"):
-        _d(lib, 2, S=1000, D=128, tile_m=64)
+        _d(lib, 2, S=1000, D=128, tile_m=64, accum=_lib.TA_ACC_INPUT)
+    with pytest.raises(ValueError, match="TA_EUNSUPPORTED"):  # the paired split: 128-row tiles
+        _d(lib, _lib.TA_SPLIT_PAIRS, S=8192, D=128, tile_m=64, causal=True)
     # ... unless the chunk splits nothing, which runs whole rows on any kernel
-    assert _d(lib, 64, S=1000, D=128, tile_m=64).layout == _lib.TA_LAYOUT_WHOLE_ROWS
+    assert _d(lib, 64, S=1000, D=128, tile_m=64, accum=_lib.TA_ACC_INPUT).layout == _lib.TA_LAYOUT_WHOLE_ROWS
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("d", [64, 96, 128, 160])
+def test_64_row_split_descriptions(lib, objects, d, causal):
+    """Chunks on the 64-row kernel: the 128-row numbering with two 64-row halves per item
+    (twice the workgroups of the 128-row split), the same merge kernel and workspace."""
+    d128 = _d(lib, 2, B=1, H=2, S=1000, D=d, causal=causal)
+    d64 = _d(lib, 2, B=1, H=2, S=1000, D=d, causal=causal, tile_m=64)
+    assert d64.layout == _lib.TA_LAYOUT_SPLIT and d64.rows == 64
+    assert d64.kernel.decode() == f"ta_fwd_pp64_split_bf16_d{d}_c{int(causal)}_t1"
+    assert d64.grid == 2 * d128.grid
+    assert (d64.merge_kernel, d64.merge_grid, d64.workspace_bytes) == (
+        d128.merge_kernel, d128.merge_grid, d128.workspace_bytes)
+    for sym in (d64.kernel, d64.merge_kernel):
+        assert sym + b"\x00" in objects["attn_fwd_pp.hsaco"], sym
+    # the dispatch model plans the 128-row kernel only: auto leaves 64-row tiles whole
+    plan = lib.ta_split_plan_model(1000, 2, int(causal), 256)
+    a = _lib.shape_args(B=1, H=2, S=1000, D=d, causal=causal, tile_m=64)
+    out = __import__("ctypes").c_int32(-7)
+    assert lib.ta_split_plan(__import__("ctypes").byref(a), __import__("ctypes").byref(out)) in (0, 4)
+    assert plan >= 0
 
 
 def test_zero_size_and_invalid_requests(lib):

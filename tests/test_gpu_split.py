@@ -43,6 +43,42 @@ def test_forced_chunks_match_oracle(gpu, shape, dtype, causal, chunks):
         check_close(as_f32(out), ref, dtype, what=f"split chunk={chunk}")
 
 
+@pytest.mark.parametrize("shape,dtype,causal,chunks,tn", [
+    ((1, 8, 2048, 128), "bfloat16", True, (1, 2, 4, 8), 64),   # C3 S=2048
+    ((1, 8, 1024, 128), "bfloat16", True, (1, 3), 128),
+    ((1, 8, 512, 128), "float16", True, (1, 2), 64),
+    ((1, 2, 1000, 64), "float16", True, (1, 3), 64),           # ragged: the last half past S
+    ((2, 3, 777, 128), "float16", False, (1, 2, 5), 64),
+    ((1, 8, 1024, 64), "float16", False, (2, 4), 64),           # C2's shape
+    ((1, 1, 129, 128), "bfloat16", True, (1,), 64),
+    ((1, 4, 1300, 160), "bfloat16", True, (1, 3), 64),
+    ((1, 3, 1000, 96), "float16", False, (2,), 128),
+    ((1, 3, 700, 72), "bfloat16", True, (2,), 64),              # in-kernel padding to 96
+    ((1, 2, 320, 144), "float16", True, (1,), 64),              # to 160; S = 5 blocks of 64 rows
+])
+def test_64_row_chunks_match_oracle(gpu, shape, dtype, causal, chunks, tn):
+    """Split key ranges on the 64-row kernel (ta_fwd_pp64_split_*: each item of the 128-row
+    numbering as two 64-row halves, the same merge kernel): forced chunk lengths against the
+    oracle and against the 64-row whole-row kernel on the same inputs."""
+    import torch
+
+    from tests.parity_util import kernel_for
+
+    q, k, v = inputs(shape, dtype, 640 + shape[2] + shape[3])
+    ref = oracle_f32(q, k, v, causal=causal)
+    say(f"64-row whole rows {dtype} {shape} causal={causal} tiles=(64,{tn})")
+    whole = run_gpu(q, k, v, causal=causal, split="off", tile_m=64, tile_n=tn, accum_mode="fp32")
+    check_close(as_f32(whole), ref, dtype, what="64-row whole rows")
+    for chunk in chunks:
+        kern = kernel_for(q, k, v, causal=causal, split=chunk, tile_m=64, tile_n=tn, accum_mode="fp32")
+        say(f"64-row split {dtype} {shape} causal={causal} chunk={chunk} kernel={kern}")
+        out = run_gpu(q, k, v, causal=causal, split=chunk, tile_m=64, tile_n=tn, accum_mode="fp32")
+        check_close(as_f32(out), ref, dtype, what=f"64-row split chunk={chunk}")
+        d = (out.float() - whole.float()).abs().max().item()
+        assert d <= 2.0 ** -7 * max(1.0, float(whole.float().abs().max())), d
+        assert torch.isfinite(out).all()
+
+
 @pytest.mark.parametrize("shape", [(1, 8, 2048, 128), (1, 1, 8192, 128), (1, 2, 4096, 128), (1, 8, 2048, 160)])
 def test_split_and_whole_rows_agree(gpu, shape):
     """bf16 causal, seed 1234, forced 8-step chunks (C3's shape) and the automatic plan

@@ -226,7 +226,8 @@ def test_split_capability_rule():
     assert rule(**{**ok, "kernel_head_dim": 64})
     assert rule(**{**ok, "kernel_head_dim": 160})
     assert not rule(**{**ok, "kernel_head_dim": 256})
-    assert not rule(**{**ok, "tile_m": 64})  # the 64-row eight-wave kernel has no split form
+    assert rule(**{**ok, "tile_m": 64})  # the 64-row eight-wave kernel splits chunks too
+    assert not rule(**{**ok, "tile_m": 64, "accum_code": _lib.TA_ACC_INPUT})
     assert rule(**{**ok, "tile_n": 128})  # the eight-wave step is 128 keys
     assert not rule(**{**ok, "accum_code": _lib.TA_ACC_INPUT})
     # in-place padding (d_real) exists on both eight-wave forms

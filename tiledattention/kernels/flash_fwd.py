@@ -369,8 +369,8 @@ def _eight_wave_kernel(*, tile_m: int, tile_n: int, accum_code: int, kernel_head
 
 
 def _split_capable(*, tile_m: int, tile_n: int, accum_code: int, kernel_head_dim: int) -> bool:
-    """Whether split key ranges exist (the 128-row eight-wave kernel with fp32
-    accumulation), as the library reports it."""
+    """Whether split key ranges exist (the eight-wave kernels with fp32 accumulation: chunks
+    and the paired split at 128 rows, chunks at 64 rows), as the library reports it."""
     return _kernel_family(tile_m=tile_m, tile_n=tile_n, accum_code=accum_code,
                           kernel_head_dim=kernel_head_dim)[1]
 
@@ -381,8 +381,9 @@ def _resolve_split(lib, args: _lib.FwdArgs, *, capable: bool, compute_units: int
     model for a device of ``compute_units`` CUs (``ta_split_plan_model``), or for the
     arguments' device when 0 (``ta_split_plan``)."""
     raw = os.getenv("TILEDATTN_SPLIT", "").strip().lower()
+    rows128 = int(args.tile_m) == 128
     if raw in ("", "auto"):
-        if not capable:
+        if not capable or not rows128:  # the dispatch model plans the 128-row kernel's splits
             return 0
         key = (int(args.S), int(args.B * args.H), int(args.causal), int(compute_units) or -1 - int(args.device))
         chunk = _SPLIT_PLANS.get(key)
@@ -399,10 +400,11 @@ def _resolve_split(lib, args: _lib.FwdArgs, *, capable: bool, compute_units: int
     if raw in ("0", "off"):
         return 0
     if raw == "pairs":
-        if not capable:
+        if not capable or not rows128:
             raise ValueError(
-                "TILEDATTN_SPLIT needs tile (128, 64) or (128, 128), fp32 accumulation and a head "
-                "dim of at most 160."
+                "TILEDATTN_SPLIT needs fp32 accumulation with tile (128, 64) or (128, 128) and a head "
+                "dim of at most 160 (pairs: 128-row tiles only; chunks also on tile (64, 64) or "
+                "(64, 128) with D = 64, 96, 128 or 160)."
             )
         return _lib.TA_SPLIT_PAIRS
     try:
@@ -414,8 +416,9 @@ def _resolve_split(lib, args: _lib.FwdArgs, *, capable: bool, compute_units: int
         raise ValueError(f"TILEDATTN_SPLIT must be >= 0, got {chunk}.")
     if chunk and not capable:
         raise ValueError(
-            "TILEDATTN_SPLIT needs tile (128, 64) or (128, 128), fp32 accumulation and a head dim "
-            "of at most 160."
+            "TILEDATTN_SPLIT needs fp32 accumulation with tile (128, 64) or (128, 128) and a head "
+            "dim of at most 160 (pairs: 128-row tiles only; chunks also on tile (64, 64) or "
+            "(64, 128) with D = 64, 96, 128 or 160)."
         )
     return chunk
 

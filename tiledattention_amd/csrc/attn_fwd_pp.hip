@@ -104,8 +104,7 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
                 "steps of 128 keys, blocks of 64, 128 or 256 rows");
   static_assert(!R256 || (!CAUSAL && !SPLIT && LOWP_TN == 0 && (D == 64 || D == 128)),
                 "256-row blocks: non-causal whole rows, fp32 accumulation, D 64 or 128");
-  static_assert(TM != 64 || (!SPLIT && (D == 64 || D == 96 || D == 128 || D == 160)),
-                "64-row blocks: whole rows, D 64, 96, 128 or 160");
+  static_assert(TM != 64 || D == 64 || D == 96 || D == 128 || D == 160, "64-row blocks: D 64, 96, 128 or 160");
   constexpr bool LOWP = LOWP_TN != 0;
   static_assert(!LOWP || (!SPLIT && (D == 64 || D == 128)), "input-dtype accumulation: whole rows, D 64 or 128");
   // Input-dtype accumulation: key steps between roundings of a wave's O, TILE_N keys of its
@@ -895,12 +894,33 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
       for (int n = 0; n < 3; ++n) an[n] = fast_exp2((mq[n] - m) * c);
       float la, lb;
       swap32(l_part * a0 + (lq[0] * an[0] + lq[1] * an[1]) + lq[2] * an[2], la, lb);
-      const float inv = 1.0f / (la + lb);
+      const float l_tot = la + lb;
+      const float inv = 1.0f / l_tot;
       const float w0 = a0 * inv;
       float wn[3];
 #pragma unroll
       for (int n = 0; n < 3; ++n) wn[n] = an[n] * inv;
       if (TAIL && my_q >= S) return;
+      if (SPLIT && slot >= 0) {
+        // One chunk of a split block: rows of this 64-row half of the 128-row slot, each
+        // normalised by its own l, in fp32, and m c + log2(l) (the 128-row split's partial
+        // format, merged by the same kernel).
+        const int srow = my_q - (q0 & ~(kPPRows - 1));
+        float* prow = p.part_o + ((int64_t)slot * kPPRows + srow) * D;
+#pragma unroll
+        for (int cc = 0; cc < CPW; ++cc) {
+          constexpr int U0 = P * CPW;
+          const int u = U0 + cc;
+          f32x4 o4;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            o4[e] = o_acc[u / 4][4 * (u % 4) + e] * w0 + (x[0][cc][e] * wn[0] + x[1][cc][e] * wn[1]) +
+                    x[2][cc][e] * wn[2];
+          *(f32x4*)(prow + 32 * (u / 4) + 8 * (u % 4) + 4 * hl) = o4;
+        }
+        if (P == 0 && hl == 0) p.part_lse[(int64_t)slot * kPPRows + srow] = m * c + fast_log2(l_tot);
+        return;
+      }
       uint16_t* orow = op + (int64_t)my_q * p.o_ss;
 #pragma unroll
       for (int cc = 0; cc < CPW; ++cc) {
@@ -1128,9 +1148,21 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
       attn_fwd_pp_block<DT, D, CAUSAL, TAIL, SPLIT>(p, b, lds_k0, lds_k1, lds_v0, lds_v1);
     }
   } else {
-    const WorkItem wi = SPLIT ? split_item(blockIdx.x, p.n_bh, p.split_items, p.sched, CAUSAL,
-                                           p.split_c, p.split_ns, p.split_slots, p.S)
-                              : whole_item(blockIdx.x, p.n_bh, p.n_qblk, p.sched, CAUSAL);
+    WorkItem wi;
+    if constexpr (SPLIT && TMR == 64) {
+      // Each item of the 128-row split numbering runs as two 64-row halves, the second half
+      // of the grid taking the second halves (an item's halves land on the same XCD): the
+      // same key chunk, rows 64 h .. 64 h + 63 of the block and of its partial slot.
+      const int total = p.split_items * p.n_bh;
+      const int half = (int)blockIdx.x >= total ? 1 : 0;
+      wi = split_item((int)blockIdx.x - half * total, p.n_bh, p.split_items, p.sched, CAUSAL, p.split_c,
+                      p.split_ns, p.split_slots, p.S);
+      wi.qt = 2 * wi.qt + half;
+    } else {
+      wi = SPLIT ? split_item(blockIdx.x, p.n_bh, p.split_items, p.sched, CAUSAL, p.split_c, p.split_ns,
+                              p.split_slots, p.S)
+                 : whole_item(blockIdx.x, p.n_bh, p.n_qblk, p.sched, CAUSAL);
+    }
     attn_fwd_pp_block<DT, D, CAUSAL, TAIL, SPLIT, TMR, LOWP_TN>(p, wi, lds_k0, lds_k1, lds_v0, lds_v1);
   }
 }
@@ -1243,11 +1275,23 @@ __device__ __forceinline__ void attn_merge_body(const FwdParams& p) {
       ta_fwd_pp64_##DTN##_d##D##_c##C##_t##T(ta::FwdParams p) {                            \
     ta::attn_fwd_pp_body<DT, D, (C != 0), (T != 0), false, false, 64>(p);                 \
   }
-#define TA_PP64_DEFINE_CT(DTN, DT, D) \
-  TA_PP64_DEFINE(DTN, DT, D, 0, 0)    \
-  TA_PP64_DEFINE(DTN, DT, D, 0, 1)    \
-  TA_PP64_DEFINE(DTN, DT, D, 1, 0)    \
-  TA_PP64_DEFINE(DTN, DT, D, 1, 1)
+// Their split-key-range form (ta_fwd_pp64_split_<...>): the 128-row split numbering, each
+// item as two 64-row halves, partials in the 128-row slots the merge kernel reads.
+#define TA_PP64_SPLIT_DEFINE(DTN, DT, D, C, T)                                             \
+  extern "C" __global__ void __launch_bounds__(512)                                       \
+      __attribute__((amdgpu_waves_per_eu(2, 2)))                                          \
+      ta_fwd_pp64_split_##DTN##_d##D##_c##C##_t##T(ta::FwdParams p) {                      \
+    ta::attn_fwd_pp_body<DT, D, (C != 0), (T != 0), true, false, 64>(p);                  \
+  }
+#define TA_PP64_DEFINE_CT(DTN, DT, D)   \
+  TA_PP64_DEFINE(DTN, DT, D, 0, 0)      \
+  TA_PP64_DEFINE(DTN, DT, D, 0, 1)      \
+  TA_PP64_DEFINE(DTN, DT, D, 1, 0)      \
+  TA_PP64_DEFINE(DTN, DT, D, 1, 1)      \
+  TA_PP64_SPLIT_DEFINE(DTN, DT, D, 0, 0) \
+  TA_PP64_SPLIT_DEFINE(DTN, DT, D, 0, 1) \
+  TA_PP64_SPLIT_DEFINE(DTN, DT, D, 1, 0) \
+  TA_PP64_SPLIT_DEFINE(DTN, DT, D, 1, 1)
 
 // Input-dtype accumulation (D = 64 and 128, whole rows), one kernel per TILE_N (the keys of
 // a wave's slice between roundings of O): ta_fwd_ppl_n<TN>_<f16|bf16>_d<D>_c_t (128-row

@@ -512,9 +512,18 @@ bool use_rows256(const ta_fwd_args* a, int64_t n_bh, int ncu) {
   return n_bh * ((a->S + 255) / 256) >= 2 * (int64_t)ncu;
 }
 
-// Whether the split path exists for this configuration (the eight-wave kernel).
+// Whether split key ranges exist for this configuration: the eight-wave kernels with fp32
+// accumulation, 128-row blocks (chunks and the paired split) or 64-row blocks (chunks, each
+// 128-row item of the numbering run as two 64-row halves).
 bool split_capable(const ta_fwd_args* a) {
-  return eight_wave(a->tile_m, a->tile_n, a->accum, a->D);
+  return eight_wave(a->tile_m, a->tile_n, a->accum, a->D) || eight_wave64(a->tile_m, a->tile_n, a->accum, a->D);
+}
+
+// Whether a chunk length can run on this configuration: the paired split needs 128-row
+// blocks.
+bool split_runs(const ta_fwd_args* a, int32_t chunk_steps) {
+  if (!split_capable(a)) return false;
+  return chunk_steps != TA_SPLIT_PAIRS || a->tile_m == 128;
 }
 
 // Everything one forward launches, decided in one place: ta_sdpa_fwd, ta_sdpa_fwd_split
@@ -546,19 +555,23 @@ ta_status plan_launch(const ta_fwd_args* a, int64_t n_bh, int64_t n_qblk, int32_
   const char* dt = a->dtype == TA_BF16 ? "bf16" : "f16";
   SplitLayout l;
   if (chunk_steps != 0 && layout_for(a->S, a->causal != 0, chunk_steps, &l)) {
-    if (!split_capable(a))
+    if (!split_runs(a, chunk_steps))
       return fail(TA_EUNSUPPORTED,
-                  "split key ranges need tile (128, 64) or (128, 128), fp32 accumulation, D <= 160");
+                  "split key ranges need fp32 accumulation on tile (128, 64) or (128, 128) with D <= 160, "
+                  "or chunks on tile (64, 64) or (64, 128) with D = 64, 96, 128 or 160 (the paired split: "
+                  "128-row tiles)");
     if (n_bh * l.items > 0x7fffffffLL || n_bh * l.slots * kSplitRows > 0x7fffffffLL ||
         n_bh * l.merge * kSplitRows > 0x7fffffffLL)
       return fail(TA_EINVAL, "split grid too large");
     const bool paired = chunk_steps == TA_SPLIT_PAIRS;
+    const bool rows64 = a->tile_m == 64;
     char name[96];
-    snprintf(name, sizeof(name), "ta_fwd_pp_%s_%s_d%d_c%d_t%d", paired ? "psplit" : "split", dt,
-             (int)a->D, a->causal ? 1 : 0, aligned ? 0 : 1);
+    snprintf(name, sizeof(name), "ta_fwd_%s_%s_d%d_c%d_t%d",
+             rows64 ? "pp64_split" : paired ? "pp_psplit" : "pp_split", dt, (int)a->D, a->causal ? 1 : 0,
+             aligned ? 0 : 1);
     pl->main = KernelId{"attn_fwd_pp.hsaco", name, 512u};
-    pl->grid = n_bh * l.items;
-    pl->rows = kSplitRows;
+    pl->grid = (rows64 ? 2 : 1) * n_bh * l.items;  // 64-row: two halves per item
+    pl->rows = rows64 ? 64 : kSplitRows;
     pl->layout = paired ? TA_LAYOUT_PAIRED_SPLIT : TA_LAYOUT_SPLIT;
     pl->chunk = chunk_steps;
     // merge: one thread per (row, 16-byte output chunk), merge_rows_per_wg(D) rows a workgroup
@@ -646,6 +659,8 @@ ta_status launch_plan_locked(const ta_fwd_args* a, const LaunchPlan& pl, ta::Fwd
   if (s == TA_OK && pl.merge) s = get_function_locked(a->device, pl.merge_id, &mfn);
   if (s != TA_OK) return s;
   if (pl.layout == TA_LAYOUT_ROWS256) p->n_qblk = static_cast<int32_t>((a->S + 255) / 256);
+  // the split numbering and the merge count 128-row blocks, whatever rows a workgroup takes
+  if (pl.merge) p->n_qblk = static_cast<int32_t>((a->S + kSplitRows - 1) / kSplitRows);
   void* params[] = {p};
   hipStream_t hs = static_cast<hipStream_t>(stream);
   hipError_t e = hipModuleLaunchKernel(fn, static_cast<unsigned>(pl.grid), 1, 1, pl.main.block, 1, 1,
@@ -783,14 +798,15 @@ ta_status plan_call(int64_t B, int64_t H, int64_t S, int64_t D, int32_t dtype, i
   out->out_width = in_place ? (int32_t)D : kd;
   if (n_bh == 0 || S == 0) return TA_OK;
   // Split: the dispatch model (auto), a forced chunk length or the paired split.
-  const bool capable = split_capable(&a);
   int32_t chunk = 0;
   if (k->split == TA_SPLIT_AUTO) {
-    chunk = capable ? cached_split_plan(S, n_bh, cz, ncu) : 0;
+    chunk = eight_wave(tm, tn, accum, kd) ? cached_split_plan(S, n_bh, cz, ncu) : 0;
   } else if (k->split != 0) {
-    if (!capable)
+    if (!split_runs(&a, k->split))
       return fail(TA_EUNSUPPORTED,
-                  "split key ranges need tile (128, 64) or (128, 128), fp32 accumulation and a head dim of at most 160");
+                  "split key ranges need fp32 accumulation on tile (128, 64) or (128, 128) with D <= 160, "
+                  "or chunks on tile (64, 64) or (64, 128) with D = 64, 96, 128 or 160 (the paired split: "
+                  "128-row tiles)");
     chunk = k->split;
   }
   out->chunk_steps = chunk;
@@ -931,7 +947,8 @@ ta_status ta_split_plan(const ta_fwd_args* a, int32_t* chunk_steps) {
   *chunk_steps = 0;
   int64_t n_bh = 0, n_qblk = 0;
   ta_status vst = validate_args(a, &n_bh, &n_qblk, false);
-  if (vst != TA_OK || n_qblk == 0 || !split_capable(a)) return vst;
+  // the dispatch model plans the 128-row kernel's splits
+  if (vst != TA_OK || n_qblk == 0 || !eight_wave(a->tile_m, a->tile_n, a->accum, a->D)) return vst;
   int ncu = 0;
   {
     std::lock_guard<std::mutex> lock(g_mu);
@@ -962,8 +979,11 @@ ta_status ta_split_workspace_size(const ta_fwd_args* a, int32_t chunk_steps, int
   // workspace, on any kernel.
   SplitLayout l;
   if (!layout_for(a->S, a->causal != 0, chunk_steps, &l)) return TA_OK;
-  if (!split_capable(a))
-    return fail(TA_EUNSUPPORTED, "split key ranges need tile (128, 64) or (128, 128), fp32 accumulation, D <= 160");
+  if (!split_runs(a, chunk_steps))
+    return fail(TA_EUNSUPPORTED,
+                "split key ranges need fp32 accumulation on tile (128, 64) or (128, 128) with D <= 160, "
+                "or chunks on tile (64, 64) or (64, 128) with D = 64, 96, 128 or 160 (the paired split: "
+                "128-row tiles)");
   *bytes = split_ws_bytes(n_bh, a->D, l);
   return TA_OK;
 }
