@@ -209,9 +209,9 @@ def test_static_scratch_entry_rejects_oversize_before_any_device_call(lib):
     assert lib.ta_sdpa_fwd_split_static(ctypes.byref(a), 1, None) == _lib.TA_EINVAL
     assert "exceeds the static scratch of 67108864 bytes" in _lib.last_error(lib)
     assert lib.ta_sdpa_fwd_split_static(None, 1, None) == _lib.TA_EINVAL
-    # a chunk that splits something needs the split kernels (none at 64-row tiles) ...
-    st1000 = (2 * 1000 * 96, 1000 * 96, 96, 1)
-    a = _args(D=96, S=1000, q_stride=st1000, k_stride=st1000, v_stride=st1000, o_stride=st1000)
+    # a chunk that splits something needs the split kernels (none for the D = 256 kernels) ...
+    st1000 = (2 * 1000 * 256, 1000 * 256, 256, 1)
+    a = _args(D=256, S=1000, q_stride=st1000, k_stride=st1000, v_stride=st1000, o_stride=st1000)
     assert lib.ta_sdpa_fwd_split_static(ctypes.byref(a), 1, None) == _lib.TA_EUNSUPPORTED
     assert "split key ranges need" in _lib.last_error(lib)
     # ... one that splits nothing runs ta_sdpa_fwd on any kernel, whose own checks apply

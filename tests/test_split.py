@@ -87,11 +87,20 @@ def test_workspace_size_edge_cases(lib):
     # a chunk as long as the longest row splits nothing
     assert lib.ta_split_workspace_size(ctypes.byref(_args(S=4096)), 32, ctypes.byref(out)) == _lib.TA_OK
     assert out.value == 0
-    for kw in (dict(tile_m=64), dict(tile_m=64, tile_n=128), dict(accum=_lib.TA_ACC_INPUT),
+    for kw in (dict(accum=_lib.TA_ACC_INPUT), dict(tile_m=64, accum=_lib.TA_ACC_INPUT),
                dict(tile_n=128, accum=_lib.TA_ACC_INPUT), dict(D=256)):
         st = lib.ta_split_workspace_size(ctypes.byref(_args(S=4096, **kw)), 4, ctypes.byref(out))
         assert st == _lib.TA_EUNSUPPORTED, kw
         assert "split key ranges" in _lib.last_error(lib)
+    # 64-row tiles split chunks (the 128-row numbering and workspace), not the paired split
+    ref = ctypes.c_int64(0)
+    assert lib.ta_split_workspace_size(ctypes.byref(_args(S=4096)), 4, ctypes.byref(ref)) == _lib.TA_OK
+    for kw in (dict(tile_m=64), dict(tile_m=64, tile_n=128)):
+        assert lib.ta_split_workspace_size(ctypes.byref(_args(S=4096, **kw)), 4, ctypes.byref(out)) == _lib.TA_OK
+        assert out.value == ref.value > 0
+        st = lib.ta_split_workspace_size(ctypes.byref(_args(S=4096, causal=1, **kw)), _lib.TA_SPLIT_PAIRS,
+                                         ctypes.byref(out))
+        assert st == _lib.TA_EUNSUPPORTED and "paired split" in _lib.last_error(lib)
     assert lib.ta_split_workspace_size(None, 4, ctypes.byref(out)) == _lib.TA_EINVAL
 
 
@@ -111,7 +120,7 @@ def test_split_launch_rejects_bad_workspace_before_any_device_call(lib):
     assert st == _lib.TA_EINVAL and "256-byte" in _lib.last_error(lib)
     st = lib.ta_sdpa_fwd_split(ctypes.byref(a), -2, ctypes.c_void_p(0x100000), need.value, None)
     assert st == _lib.TA_EINVAL
-    a.tile_m = 64
+    a.accum = _lib.TA_ACC_INPUT  # no split kernels with input-dtype accumulation
     st = lib.ta_sdpa_fwd_split(ctypes.byref(a), 4, ctypes.c_void_p(0x100000), need.value, None)
     assert st == _lib.TA_EUNSUPPORTED
 
