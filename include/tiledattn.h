@@ -145,6 +145,12 @@ ta_status ta_split_plan(const ta_fwd_args* args, int32_t* chunk_steps);
  * of sequence length S over n_bh (b, h) slices, 0 for no split or invalid sizes. */
 int32_t ta_split_plan_model(int64_t S, int64_t n_bh, int32_t causal, int32_t compute_units);
 
+/* The same for blocks of `rows` query rows (128: the model above; 64: the 64-row kernel's
+ * chunks, planned for grids whose 64-row blocks fill at most half of the compute units) at
+ * kernel head dim `head_dim`; 0 for no split. */
+int32_t ta_split_plan_model_rows(int64_t S, int64_t n_bh, int32_t causal, int32_t head_dim, int32_t rows,
+                                 int32_t compute_units);
+
 /* Device workspace (bytes, 256-byte aligned base required) that ta_sdpa_fwd_split needs
  * for `chunk_steps`; 0 when that chunk length splits nothing.  Needs no device; reads only
  * the shape, dtype, tile and accum fields. */

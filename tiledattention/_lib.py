@@ -51,6 +51,7 @@ EXPORTED_SYMBOLS = (
     "ta_sdpa_fwd",
     "ta_split_plan",
     "ta_split_plan_model",
+    "ta_split_plan_model_rows",
     "ta_split_workspace_size",
     "ta_sdpa_fwd_split",
     "ta_sdpa_fwd_split_static",
@@ -214,6 +215,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ta_split_plan.restype = i32
     lib.ta_split_plan_model.argtypes = [ctypes.c_int64, ctypes.c_int64, i32, i32]
     lib.ta_split_plan_model.restype = i32
+    lib.ta_split_plan_model_rows.argtypes = [ctypes.c_int64, ctypes.c_int64, i32, i32, i32, i32]
+    lib.ta_split_plan_model_rows.restype = i32
     lib.ta_split_workspace_size.argtypes = [ctypes.POINTER(FwdArgs), i32, ctypes.POINTER(ctypes.c_int64)]
     lib.ta_split_workspace_size.restype = i32
     lib.ta_sdpa_fwd_split.argtypes = [ctypes.POINTER(FwdArgs), i32, ctypes.c_void_p, ctypes.c_int64,

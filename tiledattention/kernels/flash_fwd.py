@@ -383,14 +383,15 @@ def _resolve_split(lib, args: _lib.FwdArgs, *, capable: bool, compute_units: int
     raw = os.getenv("TILEDATTN_SPLIT", "").strip().lower()
     rows128 = int(args.tile_m) == 128
     if raw in ("", "auto"):
-        if not capable or not rows128:  # the dispatch model plans the 128-row kernel's splits
+        if not capable:
             return 0
-        key = (int(args.S), int(args.B * args.H), int(args.causal), int(compute_units) or -1 - int(args.device))
+        key = (int(args.S), int(args.B * args.H), int(args.causal), int(compute_units) or -1 - int(args.device),
+               int(args.tile_m), int(args.D))
         chunk = _SPLIT_PLANS.get(key)
         if chunk is None:
             if compute_units:
-                chunk = int(lib.ta_split_plan_model(int(args.S), int(args.B * args.H), int(args.causal),
-                                                    int(compute_units)))
+                chunk = int(lib.ta_split_plan_model_rows(int(args.S), int(args.B * args.H), int(args.causal),
+                                                         int(args.D), int(args.tile_m), int(compute_units)))
             else:
                 out = ctypes.c_int32(0)
                 _raise_for_status(lib, lib.ta_split_plan(ctypes.byref(args), ctypes.byref(out)))
@@ -592,8 +593,15 @@ def _resolve_call(lib, *, batch: int, heads: int, seq_len: int, head_dim: int, d
             seq_len=seq_len, head_dim=head_dim, causal=causal, n_bh=bh, accum_mode=accum_mode,
             compute_units=compute_units,
         )
-        if tile_m == 64 and _split_preferred(lib, batch, heads, seq_len, head_dim, causal, compute_units,
-                                             accum_mode):
+        # Keep 128 rows where the 128-row kernel would split key ranges, unless the 64-row
+        # grid fills at most half the CUs: there the 64-row kernel, whole or split by its own
+        # plan, is faster (B1 H1 S2048 causal D = 128: 128-row split 20.0 us, 64-row whole
+        # 17.0, 64-row chunks of 4 steps 13.2; B1 H2 S8192, 256 blocks of 64 rows: the
+        # 128-row plan 47.2 against 53.9 for the best 64-row split).
+        small64 = 2 * bh * ((seq_len + 63) // 64) <= compute_units
+        raw_split = os.getenv("TILEDATTN_SPLIT", "").strip().lower()
+        if (tile_m == 64 and not (small64 and raw_split in ("", "auto"))
+                and _split_preferred(lib, batch, heads, seq_len, head_dim, causal, compute_units, accum_mode)):
             tile_m = 128
 
     pol.chunk_plan = _resolve_chunk_plan(head_dim)

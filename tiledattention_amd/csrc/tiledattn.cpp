@@ -373,6 +373,41 @@ int32_t plan_split(int64_t S, int64_t n_bh, bool causal, int ncu) {
   return best_c;
 }
 
+// Split plan for the 64-row kernel (ta_fwd_pp64_split_*): 0 (whole rows) or the chunk
+// length with the shortest modelled time, for grids whose 64-row blocks fill at most half
+// of the CUs (larger grids keep whole rows, or the 128-row kernel's plan).  Time model,
+// in units of one 128-key step of the D = 128 kernel at low occupancy, fitted to MI355X
+// timings at B*H = 1-4, S = 1024-16384, causal and not (one box: whole rows of 64 blocks
+// at S = 2048 17.0 us, chunks of 4 steps 13.2 us): a workgroup's fixed cost F (launch,
+// prologue, fill and drain, the four-way merge of key slices, stores), t per key step (scaled
+// with the head dim, and slower the more CUs the grid keeps busy), and for a split the merge
+// kernel's M plus m per chunk of the longest block (partials written, read and combined).
+// A split must beat whole rows by 8 % and keep every workgroup resident at once.
+int32_t plan_split64(int64_t S, int64_t n_bh, bool causal, int64_t d, int ncu) {
+  const double kF = 9.0, kM = 3.4, kChunk = 0.77, kLoad = 0.3;
+  const double t = d <= 64 ? 0.55 : d <= 96 ? 0.8 : d <= 128 ? 1.0 : 1.25;
+  const int64_t nq64 = (S + 63) / 64;
+  const int64_t len = (S + ta::kPPKeys - 1) / ta::kPPKeys;
+  if (ncu < 8 || S <= 0 || n_bh <= 0 || 2 * n_bh * nq64 > ncu || len < 2) return 0;
+  auto step = [&](int64_t wgs) { return t * (1.0 + kLoad * (double)wgs / ncu); };
+  const double whole = kF + (double)len * step(n_bh * nq64);
+  double best = whole * 0.92;
+  int32_t best_c = 0;
+  for (int64_t c = 1; c < len; ++c) {
+    SplitLayout l;
+    if (!layout_for(S, causal, c, &l)) continue;
+    const int64_t wgs = 2 * n_bh * l.items;  // two 64-row halves per item
+    if (wgs > ncu) continue;                 // one wave of workgroups
+    const int64_t ns = (len + c - 1) / c;    // chunks of the longest block
+    const double tc = kF + kM + (double)c * step(wgs) + kChunk * (double)ns;
+    if (tc < best) {
+      best = tc;
+      best_c = (int32_t)c;
+    }
+  }
+  return best_c;
+}
+
 // plan_split memoised per (S, B*H, causal, CUs): the dispatch model runs once per shape.
 int32_t cached_split_plan(int64_t S, int64_t n_bh, bool causal, int ncu) {
   {
@@ -755,8 +790,10 @@ ta_status plan_call(int64_t B, int64_t H, int64_t S, int64_t D, int32_t dtype, i
   } else {
     default_tile(S, D, cz, n_bh, accum == TA_ACC_FP32, ncu, &tm, &tn);
     // Keep 128 rows where the 128-row kernel would split key ranges (split kernels exist
-    // for fp32 accumulation only).
-    if (tm == 64 && accum == TA_ACC_FP32 && k->split != 0) {
+    // for fp32 accumulation only), unless the 64-row grid fills at most half the CUs: there
+    // the 64-row kernel, whole or split by its own plan, is faster.
+    const bool small64 = 2 * n_bh * ((S + 63) / 64) <= ncu;
+    if (tm == 64 && accum == TA_ACC_FP32 && k->split != 0 && !(small64 && k->split == TA_SPLIT_AUTO)) {
       if (k->split != TA_SPLIT_AUTO) {
         tm = 128;
       } else {
@@ -800,7 +837,8 @@ ta_status plan_call(int64_t B, int64_t H, int64_t S, int64_t D, int32_t dtype, i
   // Split: the dispatch model (auto), a forced chunk length or the paired split.
   int32_t chunk = 0;
   if (k->split == TA_SPLIT_AUTO) {
-    chunk = eight_wave(tm, tn, accum, kd) ? cached_split_plan(S, n_bh, cz, ncu) : 0;
+    chunk = eight_wave(tm, tn, accum, kd) ? cached_split_plan(S, n_bh, cz, ncu)
+            : eight_wave64(tm, tn, accum, kd) ? plan_split64(S, n_bh, cz, kd, ncu) : 0;
   } else if (k->split != 0) {
     if (!split_runs(&a, k->split))
       return fail(TA_EUNSUPPORTED,
@@ -947,8 +985,7 @@ ta_status ta_split_plan(const ta_fwd_args* a, int32_t* chunk_steps) {
   *chunk_steps = 0;
   int64_t n_bh = 0, n_qblk = 0;
   ta_status vst = validate_args(a, &n_bh, &n_qblk, false);
-  // the dispatch model plans the 128-row kernel's splits
-  if (vst != TA_OK || n_qblk == 0 || !eight_wave(a->tile_m, a->tile_n, a->accum, a->D)) return vst;
+  if (vst != TA_OK || n_qblk == 0 || !split_capable(a)) return vst;
   int ncu = 0;
   {
     std::lock_guard<std::mutex> lock(g_mu);
@@ -958,8 +995,16 @@ ta_status ta_split_plan(const ta_fwd_args* a, int32_t* chunk_steps) {
     ta_status cst = cu_count_locked(a->device, &ncu);
     if (cst != TA_OK) return cst;
   }
-  *chunk_steps = cached_split_plan(a->S, n_bh, a->causal != 0, ncu);
+  *chunk_steps = a->tile_m == 64 ? plan_split64(a->S, n_bh, a->causal != 0, a->D, ncu)
+                                 : cached_split_plan(a->S, n_bh, a->causal != 0, ncu);
   return TA_OK;
+}
+
+int32_t ta_split_plan_model_rows(int64_t S, int64_t n_bh, int32_t causal, int32_t head_dim, int32_t rows,
+                                 int32_t compute_units) {
+  if (S <= 0 || n_bh <= 0 || compute_units <= 0 || S > 0x7fffffffLL || n_bh > 0x7fffffffLL) return 0;
+  if (rows == 64) return plan_split64(S, n_bh, causal != 0, head_dim, compute_units);
+  return rows == 128 ? plan_split(S, n_bh, causal != 0, compute_units) : 0;
 }
 
 int32_t ta_split_plan_model(int64_t S, int64_t n_bh, int32_t causal, int32_t compute_units) {
