@@ -207,6 +207,47 @@ def test_plan_model_uses_the_compute_unit_count(lib):
     assert _plan(lib, 8192, 1, 1, 32) == 0
 
 
+def _plan64(lib, S, n_bh, causal, d=128, cus=MI355X_CUS):
+    return lib.ta_split_plan_model_rows(S, n_bh, causal, d, 64, cus)
+
+
+def _split_items(S, causal, c):
+    """Items of the split grid: causal 128-row block i holds i + 1 key steps of 128 keys,
+    cut into ceil((i + 1) / c) chunks; non-causal blocks all hold ceil(S / 128) steps."""
+    nq = -(-S // 128)
+    if causal:
+        return sum(-(-(i + 1) // c) for i in range(nq))
+    return nq * -(-nq // c)
+
+
+def test_plan_model_rows64_matches_measured_picks(lib):
+    # MI355X timings (us, bf16): whole 64-row blocks against the chosen chunk length.
+    # D128 causal B*H 1 S2048 17.2 -> 14.1 (chunks of 4), S4096 28.7 -> 17.6; D64 causal
+    # B*H 1 S4096 21.0 -> 14.8; D160 non-causal B*H 2 S4096 33.4 -> 32.5.
+    for S, n_bh, causal, d in ((2048, 1, 1, 128), (4096, 1, 1, 128), (4096, 1, 1, 64),
+                               (4096, 2, 0, 160), (2048, 2, 1, 128), (8192, 1, 0, 96)):
+        c = _plan64(lib, S, n_bh, causal, d)
+        assert c > 0, (S, n_bh, causal, d)
+        # every workgroup resident at once: two 64-row halves per item, one per CU
+        assert 2 * n_bh * _split_items(S, causal, c) <= MI355X_CUS, (S, n_bh, causal, d, c)
+    # whole rows where they were as fast or faster: a full chip of 64-row blocks (D128
+    # non-causal B*H 4 S2048 17.7 whole against 20.4 split; D160 20.0 against 23.1), short
+    # rows (S1024: one workgroup's fixed cost dominates), D96 B*H 2 S2048 (14.3 against 14.9)
+    for S, n_bh, causal, d in ((2048, 4, 0, 128), (2048, 4, 0, 160), (1024, 1, 1, 128),
+                               (1024, 2, 0, 64), (2048, 2, 0, 96), (2048, 4, 1, 96)):
+        assert _plan64(lib, S, n_bh, causal, d) == 0, (S, n_bh, causal, d)
+    # outside the region the planner covers (64-row blocks fill more than half the CUs)
+    assert _plan64(lib, 8192, 2, 1) == 0 and _plan64(lib, 4096, 8, 0) == 0
+    assert _plan64(lib, 8192, 1, 1, cus=128) == 0
+    # other row counts: 128 is the 128-row model, anything else no plan
+    for S, n_bh, causal in ((8192, 1, 1), (4096, 8, 1), (2048, 16, 1)):
+        assert lib.ta_split_plan_model_rows(S, n_bh, causal, 128, 128, MI355X_CUS) == \
+            _plan(lib, S, n_bh, causal)
+    assert lib.ta_split_plan_model_rows(4096, 1, 1, 128, 256, MI355X_CUS) == 0
+    assert _plan64(lib, 0, 1, 1) == 0 and _plan64(lib, 4096, 0, 1) == 0
+    assert _plan64(lib, 4096, 1, 1, cus=0) == 0
+
+
 # ---------------------------------------------------------------- TILEDATTN_SPLIT knob
 
 @pytest.mark.parametrize("raw,capable,expect", [

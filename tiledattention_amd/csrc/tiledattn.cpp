@@ -375,23 +375,24 @@ int32_t plan_split(int64_t S, int64_t n_bh, bool causal, int ncu) {
 
 // Split plan for the 64-row kernel (ta_fwd_pp64_split_*): 0 (whole rows) or the chunk
 // length with the shortest modelled time, for grids whose 64-row blocks fill at most half
-// of the CUs (larger grids keep whole rows, or the 128-row kernel's plan).  Time model,
-// in units of one 128-key step of the D = 128 kernel at low occupancy, fitted to MI355X
-// timings at B*H = 1-4, S = 1024-16384, causal and not (one box: whole rows of 64 blocks
-// at S = 2048 17.0 us, chunks of 4 steps 13.2 us): a workgroup's fixed cost F (launch,
-// prologue, fill and drain, the four-way merge of key slices, stores), t per key step (scaled
-// with the head dim, and slower the more CUs the grid keeps busy), and for a split the merge
-// kernel's M plus m per chunk of the longest block (partials written, read and combined).
-// A split must beat whole rows by 8 % and keep every workgroup resident at once.
+// of the CUs (larger grids keep whole rows, or the 128-row kernel's plan).  Time model in
+// microseconds, least-squares fitted (4.9 % rms) to 241 MI355X timings of whole rows and
+// forced chunks at D = 64-160, B*H = 1-8, S = 1024-8192, causal and not: a workgroup's
+// fixed cost F (launch, prologue, fill and drain, the four-way merge of key slices,
+// stores), t_D per 128-key step of the longest workgroup, slower the more CUs the grid
+// keeps busy, and for a split the merge kernel's M, m per chunk of the longest block and a
+// cost per partial slot written and read back (n_bh * slots 128-row partials of D floats,
+// spread over the CUs).  A split must beat whole rows by 2 % and keep every workgroup
+// resident at once (one 64-row workgroup per CU).
 int32_t plan_split64(int64_t S, int64_t n_bh, bool causal, int64_t d, int ncu) {
-  const double kF = 9.0, kM = 3.4, kChunk = 0.77, kLoad = 0.3;
-  const double t = d <= 64 ? 0.55 : d <= 96 ? 0.8 : d <= 128 ? 1.0 : 1.25;
+  const double kF = 6.08, kM = 3.96, kChunk = 0.30, kLoad = 0.25, kSlot = 3.67;
+  const double t = d <= 64 ? 0.40 : d <= 96 ? 0.50 : d <= 128 ? 0.65 : 0.81;
   const int64_t nq64 = (S + 63) / 64;
   const int64_t len = (S + ta::kPPKeys - 1) / ta::kPPKeys;
   if (ncu < 8 || S <= 0 || n_bh <= 0 || 2 * n_bh * nq64 > ncu || len < 2) return 0;
   auto step = [&](int64_t wgs) { return t * (1.0 + kLoad * (double)wgs / ncu); };
   const double whole = kF + (double)len * step(n_bh * nq64);
-  double best = whole * 0.92;
+  double best = whole * 0.98;
   int32_t best_c = 0;
   for (int64_t c = 1; c < len; ++c) {
     SplitLayout l;
@@ -399,7 +400,8 @@ int32_t plan_split64(int64_t S, int64_t n_bh, bool causal, int64_t d, int ncu) {
     const int64_t wgs = 2 * n_bh * l.items;  // two 64-row halves per item
     if (wgs > ncu) continue;                 // one wave of workgroups
     const int64_t ns = (len + c - 1) / c;    // chunks of the longest block
-    const double tc = kF + kM + (double)c * step(wgs) + kChunk * (double)ns;
+    const double slots = (double)(n_bh * l.slots) * (double)d / 128.0 / ncu;
+    const double tc = kF + kM + (double)c * step(wgs) + kChunk * (double)ns + kSlot * slots;
     if (tc < best) {
       best = tc;
       best_c = (int32_t)c;
