@@ -23,7 +23,9 @@ The JSON line also carries:
   (benchmark-gb10/results/benchmark_results.csv, line cited per point); ``ceiling``, what
   bounds the headline on the same box in the same run: hipBLASLt's bf16 GEMM (torch.matmul,
   8192^3) and the headline workload on inputs whose mantissas are cleared (same
-  instructions and memory traffic, least multiplier activity).
+  instructions and memory traffic, least multiplier activity); ``small``, grids of one to
+  four heads at S 2048/4096 (bf16, D 64 and 128, causal and not), the default call policy
+  beside whole 64-row blocks and the 128-row tile's own plan.
 
 Inputs are generated on the CPU from a seeded ``torch.Generator`` (q, k, v drawn in that
 order, as run_study.py:526-529 does) and copied to the GPU before any timing.
@@ -231,11 +233,17 @@ class _Env:
                 os.environ[k] = v
 
 
-def _kernel_of(q, k, v, causal: bool) -> str:
-    """The attention kernel the library launches for this call (``ta_describe_launch``)."""
+def _describe(q, k, v, causal: bool) -> dict:
+    """The launch the library makes for this call under the current knobs
+    (``ta_describe_launch``); nothing is launched."""
     from tiledattention.kernels import flash_fwd
 
-    return flash_fwd.describe_call(q, k, v, causal=causal).get("kernel", "")
+    return flash_fwd.describe_call(q, k, v, causal=causal)
+
+
+def _kernel_of(q, k, v, causal: bool) -> str:
+    """The attention kernel the library launches for this call."""
+    return _describe(q, k, v, causal).get("kernel", "")
 
 
 def clear_mantissa(t, keep_bits: int = 0):
@@ -336,7 +344,54 @@ def run_blocks(dev, only: str = "") -> dict:
                             outlier_frac=0.01, outlier_gain=20.0, outlier_seed=1235)
     if want("ceiling"):
         blocks["ceiling"] = run_ceiling(dev)
+    if want("small"):
+        blocks["small"] = run_small_grids(dev)
     return blocks
+
+
+# Small B*H grids (64-row blocks fill at most half the CUs): the default call policy beside
+# the two plans it chooses between, bf16, seed 1234.
+SMALL_GRIDS = ((1, 2048), (1, 4096), (2, 4096), (4, 2048))
+SMALL_ALTERNATIVES = (
+    ("whole64", {"tile_m": 64, "tile_n": 64, "split": "off"}),
+    ("plan128", {"tile_m": 128, "tile_n": 64}),
+)
+
+
+def run_small_grids(dev) -> dict:
+    """Default knobs against whole 64-row blocks and against the 128-row tile's own plan
+    (its split or paired split), on grids of one to four heads: the range where the
+    64-row kernel's key-range split is planned (``ta_split_plan_model_rows``)."""
+    import torch
+
+    from tiledattention import sdpa
+
+    out: dict = {}
+    for d in (64, 128):
+        for causal in (False, True):
+            for bh, s_ in SMALL_GRIDS:
+                shape = (1, bh, s_, d)
+                q, k, v = (t.to(dev) for t in make_inputs(shape, "bfloat16", 1234))
+                row: dict = {}
+                for label, env in (("default", {}),) + SMALL_ALTERNATIVES:
+                    with _Env(**env):
+                        fn = lambda: sdpa(q, k, v, causal=causal)  # noqa: E731
+                        rec = measure(fn, flops=flops_of(*shape, causal), nbytes=alg_bytes(*shape),
+                                      hot_s=0.1, regions=3, per_region=10, calls=20)
+                        desc = _describe(q, k, v, causal)
+                    row[label] = {"us": round(rec["mean_ms"] * 1e3, 2), "tflops": rec["tflops"],
+                                  "kernel": desc.get("kernel", ""), "chunk_steps": desc.get("chunk_steps", 0)}
+                for label, _ in SMALL_ALTERNATIVES:
+                    row[label]["vs_default"] = round(row["default"]["us"] / row[label]["us"], 3)
+                key = f"d{d}_{'causal' if causal else 'noncausal'}_bh{bh}_s{s_}"
+                out[key] = row
+                _log(f"block small {key}: default {row['default']['us']} us "
+                     f"({row['default']['kernel']}/c{row['default']['chunk_steps']}), " + ", ".join(
+                         f"{lb} {row[lb]['us']} us" for lb, _ in SMALL_ALTERNATIVES))
+                del q, k, v
+                torch.cuda.empty_cache()
+    return out
+
 
 
 def run_ceiling(dev) -> dict:

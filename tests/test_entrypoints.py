@@ -93,3 +93,17 @@ def test_bench_reference_grid_covers_the_metric():
     assert line_no == 548 and abs(ref - bench.REFERENCE_GB10_C3_S8192) < 0.01
     lines = [v[0] for v in bench.REFERENCE_GB10_GRID.values()]
     assert len(set(lines)) == len(lines)
+
+
+def test_bench_small_block_stays_in_the_planned_range():
+    """The small-grid block's shapes are ones whose 64-row blocks fill at most half of an
+    MI355X's 256 CUs (where the 64-row split is planned), and its alternatives name knobs
+    the library reads."""
+    sys.path.insert(0, str(ROOT))
+    import bench
+    from tiledattention.kernels import flash_fwd
+
+    for bh, s in bench.SMALL_GRIDS:
+        assert 2 * bh * -(-s // 64) <= 256, (bh, s)
+    names = {"TILEDATTN_" + k.upper() for _, env in bench.SMALL_ALTERNATIVES for k in env}
+    assert names <= set(flash_fwd._KNOBS)
