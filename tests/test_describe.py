@@ -111,6 +111,9 @@ def test_pairing_rule(lib, objects, kw, pairs):
     if pairs:
         assert desc.kernel.decode() == f"ta_fwd_pp_pair_bf16_d{args['D']}_c1_t0"
         assert desc.grid == args["B"] * args["H"] * ((nq + 1) // 2)
+    elif desc.layout == _lib.TA_LAYOUT_ROWS256:  # non-causal B1 H8 S8192: one round of 256 rows
+        assert not args["causal"] and _rounds_rule(args["B"], args["H"], args["S"])
+        assert desc.grid == args["B"] * args["H"] * -(-args["S"] // 256)
     else:
         assert desc.grid == args["B"] * args["H"] * nq
     assert desc.kernel + b"\x00" in objects[desc.code_object.decode()]
@@ -124,33 +127,54 @@ def test_pairing_follows_the_compute_units(lib):
     assert _d(lib, cu=512, **kw).compute_units == 512
 
 
-# 256-row blocks: non-causal, fp32, tiles (128, 64) / (128, 128), D 64 or 128, and at least
-# two 256-row blocks per CU (B*H*ceil(S/256) >= 2 CUs).
+# 256-row blocks: non-causal, fp32, tiles (128, 64) / (128, 128), D 64 or 128, when the
+# 256-row grid needs at most half the rounds (one workgroup per CU) of the 128-row grid:
+# 2 * ceil(B*H*ceil(S/256) / CUs) <= ceil(B*H*ceil(S/128) / CUs).
+def _rounds_rule(b, h, s, cu=CU):
+    r256 = -(-(b * h * -(-s // 256)) // cu)
+    r128 = -(-(b * h * -(-s // 128)) // cu)
+    return 2 * r256 <= r128
+
+
 @pytest.mark.parametrize("kw,rows256", [
     (dict(), True),                                     # C4: 64 heads x 16 blocks = 1024
     (dict(D=64), True), (dict(tile_n=128), True),
     (dict(causal=True), False), (dict(D=160), False), (dict(D=96), False),
-    (dict(H=7), False),                                 # 448 < 512 blocks
-    (dict(H=8), True),                                  # 512
+    (dict(H=7), True),                                  # 448 blocks: 2 rounds against 4
+    (dict(H=6), False),                                 # 384: 2 rounds against 3
+    (dict(H=10), False),                                # 640: 3 rounds against 5
+    (dict(B=1, H=8, S=8192), True),                     # 256 blocks: 1 round against 2
+    (dict(B=1, H=8, S=4096), False),                    # 128: 1 round against 1
+    (dict(B=1, H=7, S=8192), True),                     # 224: 1 round against 2
+    (dict(B=4, H=16, S=2100), False),                   # 576: 3 rounds against 5
     (dict(accum=_lib.TA_ACC_INPUT), False), (dict(tile_m=64), False),
 ])
 def test_rows256_rule(lib, objects, kw, rows256):
     args = dict(B=4, H=16, S=4096, D=128, causal=False, tile_m=128, tile_n=64, accum=_lib.TA_ACC_FP32,
                 sched=1, dtype=_lib.TA_FP16)
     args.update(kw)
+    if args["D"] in (64, 128) and not args["causal"] and args["tile_m"] == 128 and args["accum"] == _lib.TA_ACC_FP32:
+        assert _rounds_rule(args["B"], args["H"], args["S"]) is rows256
     desc = _d(lib, **args)
     assert (desc.layout == _lib.TA_LAYOUT_ROWS256) is rows256
     if rows256:
-        assert desc.kernel.decode() == f"ta_fwd_pp256_f16_d{args['D']}_c0_t0"
-        assert desc.grid == args["B"] * args["H"] * 16 and desc.rows == 256
+        assert desc.kernel.decode() == f"ta_fwd_pp256_f16_d{args['D']}_c0_t{int(args['S'] % 256 != 0)}"
+        assert desc.grid == args["B"] * args["H"] * -(-args["S"] // 256) and desc.rows == 256
     assert desc.kernel + b"\x00" in objects[desc.code_object.decode()]
 
 
+def test_rows256_rule_follows_the_compute_units(lib):
+    """The same grid is one round of 256-row blocks on 256 CUs, half a round on 512."""
+    kw = dict(B=1, H=8, S=8192, D=128, causal=False)
+    assert _d(lib, cu=256, **kw).layout == _lib.TA_LAYOUT_ROWS256
+    assert _d(lib, cu=512, **kw).layout == _lib.TA_LAYOUT_WHOLE_ROWS
+
+
 def test_rows256_tail_variant_when_s_is_not_a_multiple_of_256(lib):
-    desc = _d(lib, B=4, H=16, S=4224, D=128, causal=False)  # 128-aligned, not 256
+    desc = _d(lib, B=4, H=15, S=4224, D=128, causal=False)  # 128-aligned, not 256
     assert desc.layout == _lib.TA_LAYOUT_ROWS256
     assert desc.tail == 1 and desc.kernel.decode() == "ta_fwd_pp256_bf16_d128_c0_t1"
-    assert desc.grid == 64 * 17
+    assert desc.grid == 60 * 17
 
 
 @pytest.mark.parametrize("d", [64, 96, 128, 160])

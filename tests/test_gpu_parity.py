@@ -630,24 +630,28 @@ def test_golden_fixture_c1(gpu):
 
 @pytest.mark.parametrize("shape,dtype,tiles", [
     ((4, 16, 2048, 128), "bfloat16", (128, 64)),
-    ((4, 16, 2100, 64), "float16", (128, 64)),     # ragged: the tail-masked variant
-    ((2, 32, 2304, 120), "bfloat16", (128, 128)),  # kernel head dim 128, columns 120.. zero
+    ((8, 7, 2100, 64), "float16", (128, 64)),      # ragged: the tail-masked variant
+    ((2, 28, 2304, 120), "bfloat16", (128, 128)),  # kernel head dim 128, columns 120.. zero
     ((8, 8, 2000, 128), "float16", (128, 64)),
+    ((1, 8, 8192, 128), "bfloat16", (128, 64)),    # one block per CU
 ])
 def test_rows256_noncausal(gpu, shape, dtype, tiles):
-    """Non-causal grids of two or more 256-row blocks per CU run ta_fwd_pp256_* (the two wave
-    groups on different rows, every key of a step each): sampled rows against the oracle,
-    contiguous and [B,S,H,D] views."""
+    """Non-causal grids whose 256-row blocks need at most half the rounds of 128-row ones
+    run ta_fwd_pp256_* (the two wave groups on different rows, every key of a step each):
+    sampled rows against the oracle, contiguous and [B,S,H,D] views."""
     import torch
 
     from tiledattention import sdpa
+    from tiledattention.kernels import flash_fwd
 
     b, h, s, d = shape
-    assert b * h * -(-s // 256) >= 512
     q, k, v = inputs(shape, dtype, 256 + s + d)
     rows = sample_rows(s, 64)
     ref = oracle_f32(q, k, v, causal=False, rows=rows)
     say(f"256-row blocks {dtype} {shape} non-causal tiles={tiles}")
+    with knobs(tile_m=tiles[0], tile_n=tiles[1], accum_mode="fp32"):
+        desc = flash_fwd.describe_call(q.to("cuda:0"), k.to("cuda:0"), v.to("cuda:0"), causal=False)
+    assert desc["kernel"].startswith("ta_fwd_pp256_"), desc
     out = run_gpu(q, k, v, causal=False, tile_m=tiles[0], tile_n=tiles[1], accum_mode="fp32")
     check_close(as_f32(out, rows), ref, dtype, what=f"256-row {shape}")
     dev = torch.device("cuda:0")

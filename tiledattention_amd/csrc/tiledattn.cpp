@@ -541,12 +541,17 @@ bool use_pairs(const ta_fwd_args* a, int64_t n_bh, int64_t n_qblk, int ncu) {
 
 // Whether a whole-row launch runs 256-row blocks (ta_fwd_pp256_*: the two wave groups own
 // different rows and each takes every key of a step, 64 MFMAs a cluster): non-causal, the
-// eight-wave kernel at D = 64 or 128 with fp32 accumulation, a grid of two or more such
-// blocks per CU (fewer leave CUs idle or unbalanced).
+// eight-wave kernel at D = 64 or 128 with fp32 accumulation, when the grid takes no more
+// rounds of one workgroup per CU than half the 128-row grid's (a 256-row block is two
+// 128-row blocks of work at ≈4 % less time: B1 H8 S8192 D = 128, 256 blocks on 256 CUs,
+// 222 -> 214 µs bf16; a round more, e.g. 384 blocks against 768, loses).
 bool use_rows256(const ta_fwd_args* a, int64_t n_bh, int ncu) {
-  if (a->causal || !eight_wave(a->tile_m, a->tile_n, a->accum, a->D) || (a->D != 64 && a->D != 128))
+  if (a->causal || !eight_wave(a->tile_m, a->tile_n, a->accum, a->D) || (a->D != 64 && a->D != 128) ||
+      ncu <= 0)
     return false;
-  return n_bh * ((a->S + 255) / 256) >= 2 * (int64_t)ncu;
+  const int64_t rounds256 = (n_bh * ((a->S + 255) / 256) + ncu - 1) / ncu;
+  const int64_t rounds128 = (n_bh * ((a->S + 127) / 128) + ncu - 1) / ncu;
+  return 2 * rounds256 <= rounds128;
 }
 
 // Whether split key ranges exist for this configuration: the eight-wave kernels with fp32
