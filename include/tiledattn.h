@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define TA_ABI_VERSION 4
+#define TA_ABI_VERSION 5
 
 typedef enum ta_status {
   TA_OK = 0,
@@ -159,7 +159,10 @@ ta_status ta_split_workspace_size(const ta_fwd_args* args, int32_t chunk_steps, 
 /* Enqueue one SDPA forward with split key ranges on `stream`.  chunk_steps = 0, or a
  * chunk length that splits nothing, is exactly ta_sdpa_fwd.  The workspace is owned by the
  * caller, needs no initialisation, and must not be used by another call until this one's
- * work on `stream` has finished. */
+ * work on `stream` has finished.  The split blocks are merged by the split kernel itself
+ * (ta_launch_desc.merge_in_kernel) with arrival counters the library keeps per (device,
+ * stream) in the code object, or, past 16 streams on a device, by a merge kernel on
+ * `stream` after it. */
 ta_status ta_sdpa_fwd_split(const ta_fwd_args* args, int32_t chunk_steps, void* workspace,
                             int64_t workspace_bytes, void* stream);
 
@@ -210,7 +213,10 @@ typedef struct ta_launch_desc {
   int32_t merge_block;
   int32_t in_place_pad;   /* 1: the kernel family reads d_real < D in place (eight-wave) */
   int32_t split_capable;  /* 1: split kernels exist for this configuration */
-  int32_t reserved;
+  int32_t merge_in_kernel; /* 1: the split kernel merges its blocks itself (the last
+                              workgroup to finish a block combines its partials), so the
+                              merge kernel runs only when the launching stream finds no
+                              free counter region (more than 16 streams launching splits) */
   int64_t workspace_bytes; /* workspace ta_sdpa_fwd_split needs for chunk_steps (0 if none) */
 } ta_launch_desc;
 

@@ -58,6 +58,7 @@ static void check_case(int S, int n_bh, bool causal, int c, int sched) {
   }
   // split grid: coverage of key steps
   std::map<std::pair<int, int>, std::vector<std::tuple<int, int, int>>> chunks;  // (bh,qt) -> (beg,end,slot)
+  std::map<std::pair<int, int>, std::pair<int, int>> block_of;  // (bh,qt) -> (slot0, ns) of its chunks
   std::set<int> slots;
   const int total = (int)(n_bh * l.items);
   for (int blk = 0; blk < total; ++blk) {
@@ -69,6 +70,14 @@ static void check_case(int S, int n_bh, bool causal, int c, int sched) {
     if (w.slot >= 0) {
       CHECK(w.slot < n_bh * l.slots, "slot %d of %lld", w.slot, (long long)(n_bh * l.slots));
       CHECK(slots.insert(w.slot).second, "slot %d reused", w.slot);
+      // the block's chunk-0 slot and chunk count, as the in-kernel merge reads them
+      auto ins = block_of.emplace(std::make_pair(w.bh, w.qt), std::make_pair(w.slot0, w.ns));
+      const auto& bi = ins.first->second;
+      CHECK(bi.first == w.slot0 && bi.second == w.ns, "S=%d c=%d chunk slot0/ns %d/%d vs %d/%d", S, c,
+            w.slot0, w.ns, bi.first, bi.second);
+      CHECK(w.slot0 <= w.slot && w.slot < w.slot0 + w.ns, "slot %d outside [%d, +%d)", w.slot, w.slot0, w.ns);
+    } else {
+      CHECK(w.slot0 == -1 && w.ns == 1, "whole block slot0/ns %d/%d", w.slot0, w.ns);
     }
     chunks[{w.bh, w.qt}].emplace_back(w.t_beg, w.t_end, w.slot);
   }
@@ -105,6 +114,9 @@ static void check_case(int S, int n_bh, bool causal, int c, int sched) {
     CHECK((int)it->second.size() == m.ns, "merge ns %d vs %zu", m.ns, it->second.size());
     for (int i = 0; i < m.ns && i < (int)it->second.size(); ++i)
       CHECK(it->second[i] == m.slot0 + i, "merge slot %d vs %d", m.slot0 + i, it->second[i]);
+    const auto bi = block_of.count({m.bh, m.qt}) ? block_of[{m.bh, m.qt}] : std::make_pair(-2, -2);
+    CHECK(bi.first == m.slot0 && bi.second == m.ns, "chunks' slot0/ns %d/%d vs merge %d/%d", bi.first, bi.second,
+          m.slot0, m.ns);
     CHECK(merged.insert({m.bh, m.qt}).second, "block merged twice");
   }
   CHECK(merged.size() == split_blocks.size(), "S=%d c=%d merged %zu of %zu", S, c, merged.size(), split_blocks.size());
@@ -151,6 +163,7 @@ static void check_psplit(int S, int n_bh, int sched, int f) {
   if (split) CHECK(l.items == nq && l.slots == 2 * P && l.merge == P, "S=%d layout", S);
   std::map<std::pair<int, int>, std::vector<std::tuple<int, int, int>>> chunks;
   std::set<int> slots;
+  std::map<std::pair<int, int>, std::set<int>> ps_slot0;  // (bh,qt) -> slot0 of its chunks
   for (int blk = 0; blk < n_bh * nq; ++blk) {
     ta::WorkItem it[2];
     ta::psplit_items(blk, n_bh, nq, sched, f, &it[0], &it[1]);
@@ -167,6 +180,11 @@ static void check_psplit(int S, int n_bh, int sched, int f) {
       if (w.slot >= 0) {
         CHECK(w.slot < n_bh * 2 * P, "slot %d of %d", w.slot, n_bh * 2 * P);
         CHECK(slots.insert(w.slot).second, "slot %d reused", w.slot);
+        CHECK(w.ns == 2 && (w.slot == w.slot0 || w.slot == w.slot0 + 1), "psplit slot0/ns %d/%d slot %d", w.slot0,
+              w.ns, w.slot);
+        ps_slot0[{w.bh, w.qt}].insert(w.slot0);
+      } else {
+        CHECK(w.slot0 == -1 && w.ns == 1, "psplit whole block slot0/ns %d/%d", w.slot0, w.ns);
       }
       chunks[{w.bh, w.qt}].emplace_back(w.t_beg, w.t_end, w.slot);
     }
@@ -198,6 +216,8 @@ static void check_psplit(int S, int n_bh, int sched, int f) {
     if (itc == cut.end()) continue;
     CHECK(m.ns == 2 && itc->second[0] == m.slot0 && itc->second[1] == m.slot0 + 1,
           "merge slots %d vs %d %d", m.slot0, itc->second[0], itc->second[1]);
+    const auto& s0 = ps_slot0[{m.bh, m.qt}];
+    CHECK(s0.size() == 1 && *s0.begin() == m.slot0, "psplit chunks' slot0 vs merge %d", m.slot0);
     CHECK(merged.insert({m.bh, m.qt}).second, "block merged twice");
   }
   CHECK(merged.size() == cut.size(), "S=%d f=%d merged %zu of %zu", S, f, merged.size(), cut.size());

@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_status_names(lib):
-    assert lib.ta_abi_version() == _lib.ABI_VERSION == 4
+    assert lib.ta_abi_version() == _lib.ABI_VERSION == 5
     names = [lib.ta_status_string(i).decode() for i in range(5)]
     assert names == ["TA_OK", "TA_EINVAL", "TA_EUNSUPPORTED", "TA_ENOKERNEL", "TA_EHIP"]
     assert lib.ta_status_string(99).decode() == "TA_UNKNOWN"

@@ -188,12 +188,49 @@ def test_split_descriptions(lib, objects, d, causal):
     assert desc.merge_kernel.decode() == f"ta_fwd_merge_bf16_d{d}_c{int(causal)}"
     assert desc.block == 512 and desc.merge_block > 0 and desc.merge_grid > 0
     assert desc.workspace_bytes > 0
+    # 8 blocks, chunks of 2: up to 4 chunks a block, 2 x 6 (causal) or 2 x 8 split blocks,
+    # far below 3/8 of the CUs: the merge kernel runs
+    assert desc.merge_in_kernel == 0
     need = __import__("ctypes").c_int64(0)
     a = _lib.shape_args(B=1, H=2, S=1000, D=d, causal=causal)
     assert lib.ta_split_workspace_size(__import__("ctypes").byref(a), 2, __import__("ctypes").byref(need)) == 0
     assert need.value == desc.workspace_bytes
     for sym in (desc.kernel, desc.merge_kernel):
         assert sym + b"\x00" in objects["attn_fwd_pp.hsaco"], sym
+
+
+@pytest.mark.parametrize("kw,chunk,mik", [
+    # the paired split: two chunks a block
+    (dict(B=1, H=8, S=4096, causal=True), _lib.TA_SPLIT_PAIRS, 1),
+    (dict(B=1, H=1, S=4096, causal=True), _lib.TA_SPLIT_PAIRS, 1),
+    # at most two chunks a block, any grid
+    (dict(B=1, H=1, S=2048, causal=True), 8, 1),        # 16 blocks: 8 split in 2
+    (dict(B=1, H=2, S=4096, causal=False), 16, 1),      # 32 steps in 2 chunks
+    # more chunks: only with 3/8 of the CUs' worth of split blocks (96 of 256)
+    (dict(B=1, H=8, S=2048, causal=True), 4, 1),        # 8 x 12 = 96 split blocks, 4 chunks
+    (dict(B=1, H=4, S=4096, causal=True), 11, 0),       # 4 x 21 = 84, 3 chunks
+    (dict(B=1, H=1, S=4096, causal=True), 5, 0),        # 27, 7 chunks
+    (dict(B=1, H=1, S=2048, causal=False), 4, 0),       # 16, 4 chunks
+    (dict(B=1, H=8, S=4096, causal=True), 1, 1),        # 8 x 31 = 248 split blocks
+    # more partial slots than a counter region (16384) holds: the merge kernel
+    (dict(B=4, H=16, S=4096, causal=True), 1, 0),       # 64 heads x 496 slots
+])
+def test_in_kernel_merge_rule(lib, kw, chunk, mik):
+    """The split kernel merges its own blocks (the last workgroup of a block combines its
+    partials; a counter per block, its chunk-0 slot) when the counters fit a region and no
+    block has more than two chunks or the split blocks number 3/8 of the CUs or more;
+    otherwise the merge kernel runs after it."""
+    desc = _d(lib, chunk, D=128, **kw)
+    assert desc.layout in (_lib.TA_LAYOUT_SPLIT, _lib.TA_LAYOUT_PAIRED_SPLIT)
+    assert desc.merge_in_kernel == mik and desc.merge_grid > 0 and desc.merge_kernel != b""
+
+
+def test_in_kernel_merge_rule_follows_the_compute_units(lib):
+    kw = dict(B=1, H=8, S=2048, D=128, causal=True)  # 96 split blocks of up to 4 chunks
+    assert _d(lib, 4, cu=256, **kw).merge_in_kernel == 1
+    assert _d(lib, 4, cu=512, **kw).merge_in_kernel == 0
+    whole = _d(lib, 0, B=1, H=8, S=4096, D=128, causal=True)
+    assert whole.merge_in_kernel == 0 and whole.merge_kernel == b""
 
 
 def test_paired_split_and_chunks_that_split_nothing(lib):

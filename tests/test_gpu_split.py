@@ -275,3 +275,51 @@ def test_automatic_plan_runs_the_paired_split(gpu):
     assert any(key[0] == 4096 and key[1] == 6 and key[2] == 1 and c == _lib.TA_SPLIT_PAIRS
                for key, c in flash_fwd._SPLIT_PLANS.items()), flash_fwd._SPLIT_PLANS
     check_close(as_f32(out, rows), ref, "bfloat16", what="automatic paired split")
+
+
+@pytest.mark.parametrize("shape,dtype,split,tm", [
+    ((1, 8, 4096, 128), "bfloat16", "pairs", 128),   # paired split: 13 cut pairs a head
+    ((2, 3, 777, 128), "float16", 4, 128),           # non-causal chunks of 4 steps (2 a block)
+    ((1, 8, 2048, 128), "bfloat16", 4, 64),          # 64-row halves: 2 arrivals a chunk,
+                                                     # 96 split blocks of up to 4 chunks
+])
+def test_in_kernel_merge_repeated_and_on_many_streams(gpu, shape, dtype, split, tm):
+    """Split launches are merged by their own last workgroup per block (arrival counters
+    per (device, stream), left at zero by every launch).  Forty back-to-back calls on one
+    stream give bit-identical outputs (a counter not reset would merge early or never);
+    the same call on 20 streams, more than the 16 counter regions, so the last streams
+    run the merge kernel instead, gives the same bits everywhere; and it meets the oracle."""
+    import torch
+
+    from tiledattention import sdpa
+    from tiledattention.kernels import flash_fwd
+
+    causal = split == "pairs" or shape[2] != 777
+    s = shape[2]
+    q, k, v = inputs(shape, dtype, 700 + s)
+    rows = None if s <= 2048 else sample_rows(s, 96)
+    ref = oracle_f32(q, k, v, causal=causal, rows=rows)
+    dev = torch.device("cuda:0")
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    kn = dict(split=split, tile_m=tm, tile_n=64, accum_mode="fp32")
+    with knobs(**kn):
+        desc = flash_fwd.describe_call(qd, kd, vd, causal=causal)
+    assert desc["merge_kernel"] and desc["merge_in_kernel"] == 1, desc
+    say(f"in-kernel merge {dtype} {shape} split={split} rows={tm}: 40 calls on one stream")
+    with knobs(**kn):
+        first = sdpa(qd, kd, vd, causal=causal)
+        outs = [sdpa(qd, kd, vd, causal=causal) for _ in range(40)]
+    torch.cuda.synchronize()
+    assert all(torch.equal(o, first) for o in outs)
+    check_close(as_f32(first, rows), ref, dtype, what=f"in-kernel merge {shape}")
+    say(f"in-kernel merge {dtype} {shape} split={split} rows={tm}: 20 streams")
+    streams = [torch.cuda.Stream(dev) for _ in range(20)]
+    per = []
+    with knobs(**kn):
+        for st in streams:
+            st.wait_stream(torch.cuda.current_stream(dev))
+            with torch.cuda.stream(st):
+                per.append(sdpa(qd, kd, vd, causal=causal))
+    torch.cuda.synchronize()
+    for i, o in enumerate(per):
+        assert torch.equal(o, first), f"stream {i}: max |diff| {float((o.float() - first.float()).abs().max())}"

@@ -17,7 +17,7 @@ from threading import Lock
 
 from ._errors import DependencyError
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 TA_OK = 0
 TA_EINVAL = 1
@@ -112,7 +112,7 @@ class LaunchDesc(ctypes.Structure):
         ("merge_block", ctypes.c_int32),
         ("in_place_pad", ctypes.c_int32),
         ("split_capable", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("merge_in_kernel", ctypes.c_int32),
         ("workspace_bytes", ctypes.c_int64),
     ]
 

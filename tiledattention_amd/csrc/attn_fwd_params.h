@@ -31,6 +31,16 @@ struct FwdParams {
   int32_t d_real;      // head-dim columns present in q/k/v/o (eight-wave kernel; <= D,
                        // multiple of 8): columns d_real..D-1 read as zero, are not written
   int32_t pad0;
+  // Split launches merged in the kernel: arrival counters of this launch's split blocks
+  // (counter slot0 of a block, see WorkItem), zero on entry and left zero; null when a
+  // merge kernel follows instead.
+  unsigned* merge_cnt;
 };
+
+// In-kernel merge counters (attn_fwd_pp.hip's ta_merge_counters): kMergeRegions regions of
+// kMergeRegionCounters, one region per stream that launches split work, so launches that
+// may overlap never share counters.
+constexpr int kMergeRegions = 16;
+constexpr int kMergeRegionCounters = 16384;
 
 }  // namespace ta

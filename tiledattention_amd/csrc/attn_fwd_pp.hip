@@ -56,6 +56,45 @@ __device__ static inline int pp_swz_v(int row) {
 // Stage size of the eight-wave kernel at head dim D: 128 key rows of 2 D bytes.
 constexpr int pp_stage_bytes(int d) { return kPPKeys * 2 * d; }
 
+// Partials of split blocks (part_o, part_lse) are written and, by the in-kernel merge,
+// read with agent-scope cache policy (SC1: the form the compiler gives agent-scope atomic
+// stores and loads), through a buffer resource over the workspace.  Such a store is
+// visible to SC1 loads on every CU, whatever its XCD, once it has completed (vmcnt), so the
+// merge needs no flush or invalidation of the L2 (agent-scope fences cost 8-9 us a launch
+// at C3 S = 4096).  The workspace of an in-kernel merge is below 2^31 bytes (at most
+// kMergeRegionCounters slots of 128 rows of D <= 160 floats).
+constexpr int kAgentScope = 16;  // cache policy bit SC1
+__device__ inline __amdgpu_buffer_rsrc_t partial_rsrc(const FwdParams& p) {
+  return __builtin_amdgcn_make_buffer_rsrc(p.part_o, (short)0, 0x7fffffff, 0x00020000);
+}
+__device__ inline int partial_offset(const FwdParams& p, const float* at) {
+  return (int)((const char*)at - (const char*)p.part_o);
+}
+// (A launch followed by the merge kernel stores plainly: its workspace may exceed 2^31
+// bytes, and the kernel boundary makes the stores visible.)
+__device__ inline void store_partial(const FwdParams& p, float* at, f32x4 v) {
+  if (p.merge_cnt == nullptr) {
+    *(f32x4*)at = v;
+    return;
+  }
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), partial_rsrc(p), partial_offset(p, at), 0,
+                                         kAgentScope);
+}
+__device__ inline void store_partial(const FwdParams& p, float* at, float v) {
+  if (p.merge_cnt == nullptr) {
+    *at = v;
+    return;
+  }
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), partial_rsrc(p), partial_offset(p, at), 0, kAgentScope);
+}
+__device__ inline f32x4 load_partial4(const FwdParams& p, const float* at) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(partial_rsrc(p), partial_offset(p, at), 0,
+                                                                         kAgentScope));
+}
+__device__ inline float load_partial(const FwdParams& p, const float* at) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(partial_rsrc(p), partial_offset(p, at), 0, kAgentScope));
+}
+
 // One query block (or, with SPLIT, one chunk of its key steps) on the whole workgroup: the
 // prologue, the key loop and the merge of the key slices with the output stores.  TMR is
 // the block's query rows: 128 (four 32-row blocks; a wave group's four waves take one row
@@ -780,9 +819,9 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) *(f32x4*)(prow + 32 * (LO + b) + 8 * g + 4 * hl) = merged(b, g);
+        for (int g = 0; g < 4; ++g) store_partial(p, prow + 32 * (LO + b) + 8 * g + 4 * hl, merged(b, g));
       }
-      if (grp == 0 && hl == 0) p.part_lse[(int64_t)slot * TM + (my_q - q0)] = m * c + fast_log2(l_tot);
+      if (grp == 0 && hl == 0) store_partial(p, p.part_lse + (int64_t)slot * TM + (my_q - q0), m * c + fast_log2(l_tot));
       return;
     }
     // Whole-row kernels at D = 128, and causal ones at D = 64, stage the wave's 32 rows x
@@ -916,9 +955,9 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
           for (int e = 0; e < 4; ++e)
             o4[e] = o_acc[u / 4][4 * (u % 4) + e] * w0 + (x[0][cc][e] * wn[0] + x[1][cc][e] * wn[1]) +
                     x[2][cc][e] * wn[2];
-          *(f32x4*)(prow + 32 * (u / 4) + 8 * (u % 4) + 4 * hl) = o4;
+          store_partial(p, prow + 32 * (u / 4) + 8 * (u % 4) + 4 * hl, o4);
         }
-        if (P == 0 && hl == 0) p.part_lse[(int64_t)slot * kPPRows + srow] = m * c + fast_log2(l_tot);
+        if (P == 0 && hl == 0) store_partial(p, p.part_lse + (int64_t)slot * kPPRows + srow, m * c + fast_log2(l_tot));
         return;
       }
       uint16_t* orow = op + (int64_t)my_q * p.o_ss;
@@ -1016,10 +1055,10 @@ __device__ __forceinline__ void attn_fwd_pp_block(const FwdParams& p, const Work
           const int r = 4 * g + e;
           o4[e] = o_acc[db][r] * w0s + x1[db][r] * w1s;
         }
-        *(f32x4*)(prow + 32 * db + 8 * g + 4 * hl) = o4;
+        store_partial(p, prow + 32 * db + 8 * g + 4 * hl, o4);
       }
     }
-    if (hl == 0) p.part_lse[(int64_t)slot * TM + (my_q - q0)] = m * c + fast_log2(l_tot);
+    if (hl == 0) store_partial(p, p.part_lse + (int64_t)slot * TM + (my_q - q0), m * c + fast_log2(l_tot));
     return;
   }
   if constexpr (kStageOut && D == 160) {
@@ -1132,6 +1171,12 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
   __shared__ __attribute__((aligned(1024))) char lds_k1[STAGE];
   __shared__ __attribute__((aligned(1024))) char lds_v0[STAGE];
   __shared__ __attribute__((aligned(1024))) char lds_v1[STAGE];
+  // In-kernel merge: whether this workgroup arrived last at its block, in the last word of
+  // a stage (every stage access of the block has completed at the arrival, and the next
+  // block's loads start only after the barrier that follows every wave's read of it; D = 160
+  // fills the LDS).
+  int* const s_last = (int*)(lds_v1 + STAGE - sizeof(int));
+  const bool merge_here = SPLIT && p.merge_cnt != nullptr;
   if constexpr (PAIR) {
     static_assert(CAUSAL, "pairs of causal query blocks");
     WorkItem a, b;
@@ -1146,6 +1191,12 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
       __builtin_amdgcn_s_waitcnt(0xC07F);
       __builtin_amdgcn_s_barrier();
       attn_fwd_pp_block<DT, D, CAUSAL, TAIL, SPLIT>(p, b, lds_k0, lds_k1, lds_v0, lds_v1);
+    }
+    if (merge_here) {
+      // At most one of a workgroup's items is a chunk of a cut block (psplit_items: the
+      // heavy block's remainder as `a`, or its first chunk as `b`), and it is the last one.
+      const WorkItem& w = b.qt >= 0 ? b : a;
+      if (w.slot >= 0) split_arrive_and_merge<DT, D>(p, w, w.qt, 1, s_last);
     }
   } else {
     WorkItem wi;
@@ -1164,6 +1215,8 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
                  : whole_item(blockIdx.x, p.n_bh, p.n_qblk, p.sched, CAUSAL);
     }
     attn_fwd_pp_block<DT, D, CAUSAL, TAIL, SPLIT, TMR, LOWP_TN>(p, wi, lds_k0, lds_k1, lds_v0, lds_v1);
+    if (merge_here && wi.slot >= 0)
+      split_arrive_and_merge<DT, D>(p, wi, TMR == 64 ? wi.qt >> 1 : wi.qt, TMR == 64 ? 2 : 1, s_last);
   }
 }
 
@@ -1175,31 +1228,24 @@ __device__ __forceinline__ void attn_fwd_pp_body(const FwdParams& p) {
 // (merge_threads(D) threads), so a split block takes 128 / merge_rows_per_wg(D)
 // workgroups; the partial reads of the chunks are independent and contiguous across the
 // D/8 threads of a row, and a row is written by those threads as one contiguous run.
-template <int DT, int D, bool CAUSAL>
-__device__ __forceinline__ void attn_merge_body(const FwdParams& p) {
+// One (row, 16-byte output chunk) of a split block: the block's ns partials in slots
+// slot0 .. slot0 + ns - 1 combined and written to O.
+template <int DT, int D>
+__device__ __forceinline__ void merge_row_chunk(const FwdParams& p, int bh, int qt, int slot0, int ns, int row,
+                                                int c8) {
   constexpr int TM = kPPRows;
-  constexpr int CH = D / 8;        // 16-byte output chunks per row
-  constexpr int RPW = merge_rows_per_wg(D);  // rows per workgroup
-  constexpr int WPB = TM / RPW;              // workgroups per split block
-  static_assert(merge_threads(D) <= 256 && TM % RPW == 0, "workgroups must cover whole rows");
   using DTy = DType<DT>;
-  const int blk = blockIdx.x / WPB;
-  const MergeItem mi = CAUSAL && p.split_c == kSplitPairs
-                           ? psplit_merge_item(blk, p.n_qblk, p.split_ns)
-                           : merge_item(blk, p.n_qblk, CAUSAL, p.split_c, p.split_ns, p.split_slots);
-  const int row = (blockIdx.x - blk * WPB) * RPW + threadIdx.x / CH;
-  const int c8 = threadIdx.x % CH;
-  const int q = mi.qt * TM + row;
+  const int q = qt * TM + row;
   if (q >= p.S || 8 * c8 >= p.d_real) return;
-  const int b = mi.bh / p.H;
-  const int h = mi.bh - b * p.H;
-  const float* lse = p.part_lse + (int64_t)mi.slot0 * TM + row;
-  const float* po = p.part_o + ((int64_t)mi.slot0 * TM + row) * D + 8 * c8;
+  const int b = bh / p.H;
+  const int h = bh - b * p.H;
+  const float* lse = p.part_lse + (int64_t)slot0 * TM + row;
+  const float* po = p.part_o + ((int64_t)slot0 * TM + row) * D + 8 * c8;
   float mx = lse[0];
   f32x4 acc0 = *(const f32x4*)po;
   f32x4 acc1 = *(const f32x4*)(po + 4);
   float wsum = 1.0f;
-  for (int i = 1; i < mi.ns; ++i) {
+  for (int i = 1; i < ns; ++i) {
     const float li = lse[i * TM];
     const f32x4 x0 = *(const f32x4*)(po + (int64_t)i * TM * D);
     const f32x4 x1 = *(const f32x4*)(po + (int64_t)i * TM * D + 4);
@@ -1217,7 +1263,111 @@ __device__ __forceinline__ void attn_merge_body(const FwdParams& p) {
   *(u32x4*)(p.o + b * p.o_sb + h * p.o_sh + (int64_t)q * p.o_ss + 8 * c8) = o;
 }
 
+template <int DT, int D, bool CAUSAL>
+__device__ __forceinline__ void attn_merge_body(const FwdParams& p) {
+  constexpr int TM = kPPRows;
+  constexpr int CH = D / 8;        // 16-byte output chunks per row
+  constexpr int RPW = merge_rows_per_wg(D);  // rows per workgroup
+  constexpr int WPB = TM / RPW;              // workgroups per split block
+  static_assert(merge_threads(D) <= 256 && TM % RPW == 0, "workgroups must cover whole rows");
+  const int blk = blockIdx.x / WPB;
+  const MergeItem mi = CAUSAL && p.split_c == kSplitPairs
+                           ? psplit_merge_item(blk, p.n_qblk, p.split_ns)
+                           : merge_item(blk, p.n_qblk, CAUSAL, p.split_c, p.split_ns, p.split_slots);
+  const int row = (blockIdx.x - blk * WPB) * RPW + threadIdx.x / CH;
+  merge_row_chunk<DT, D>(p, mi.bh, mi.qt, mi.slot0, mi.ns, row, threadIdx.x % CH);
+}
+
+// The merge of one split block by one workgroup (512 threads): thread t takes the
+// (row, 16-byte chunk) items t, t + 512, ... of the block's 128 rows, with the merge
+// kernel's arithmetic (merge_row_chunk: the same running max, the same order, so both give
+// the same bits).  The loads of an item's chunks do not depend on the running sums, so
+// with the chunk loop unrolled they are in flight together.
+template <int DT, int D>
+__device__ __forceinline__ void merge_block_in_kernel(const FwdParams& p, int bh, int qt, int slot0, int ns) {
+  constexpr int TM = kPPRows;
+  constexpr int CH = D / 8;
+  constexpr int NI = (TM * CH + 511) / 512;  // items a thread
+  using DTy = DType<DT>;
+  const int b = bh / p.H;
+  const int h = bh - b * p.H;
+  int row[NI], c8[NI];
+  bool ok[NI];
+  const float* lse[NI];
+  const float* po[NI];
+  float mx[NI], wsum[NI];
+  f32x4 acc0[NI], acc1[NI];
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    const int idx = threadIdx.x + 512 * j;
+    row[j] = idx / CH;
+    c8[j] = idx - row[j] * CH;
+    ok[j] = idx < TM * CH && qt * TM + row[j] < p.S && 8 * c8[j] < p.d_real;
+    const int r = ok[j] ? row[j] : 0;
+    lse[j] = p.part_lse + (int64_t)slot0 * TM + r;
+    po[j] = p.part_o + ((int64_t)slot0 * TM + r) * D + 8 * (ok[j] ? c8[j] : 0);
+    mx[j] = load_partial(p, lse[j]);
+    acc0[j] = load_partial4(p, po[j]);
+    acc1[j] = load_partial4(p, po[j] + 4);
+    wsum[j] = 1.0f;
+  }
+#pragma unroll 4
+  for (int i = 1; i < ns; ++i) {
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      const float li = load_partial(p, lse[j] + i * TM);
+      const f32x4 x0 = load_partial4(p, po[j] + (int64_t)i * TM * D);
+      const f32x4 x1 = load_partial4(p, po[j] + (int64_t)i * TM * D + 4);
+      const float m_new = vmax(mx[j], li);
+      const float a = fast_exp2(mx[j] - m_new);
+      const float w = fast_exp2(li - m_new);
+      mx[j] = m_new;
+      wsum[j] = wsum[j] * a + w;
+      acc0[j] = acc0[j] * a + w * x0;
+      acc1[j] = acc1[j] * a + w * x1;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    if (!ok[j]) continue;
+    const float inv = 1.0f / wsum[j];
+    const u32x4 o = {DTy::pack(acc0[j][0] * inv, acc0[j][1] * inv), DTy::pack(acc0[j][2] * inv, acc0[j][3] * inv),
+                     DTy::pack(acc1[j][0] * inv, acc1[j][1] * inv), DTy::pack(acc1[j][2] * inv, acc1[j][3] * inv)};
+    *(u32x4*)(p.o + b * p.o_sb + h * p.o_sh + (int64_t)(qt * TM + row[j]) * p.o_ss + 8 * c8[j]) = o;
+  }
+}
+
+// In-kernel merge of a split launch (p.merge_cnt set; no merge kernel follows): after a
+// workgroup has written its chunk's partial (its slot's rows of part_o and part_lse), it
+// counts itself in at the block's counter; the workgroup that arrives last, which knows
+// that every chunk's partial is in memory, combines them into O.  `per_chunk` workgroups
+// write each chunk (two 64-row halves on the 64-row split), so a block of ns chunks counts
+// per_chunk * ns arrivals.  The counter wraps to zero on the last arrival (atomicInc), so
+// it is zero again for the launch after.  Visibility across CUs and XCDs: the partials are
+// stored and loaded at agent scope (store_partial / load_partial, SC1); every wave's stores
+// have completed (vmcnt 0) before the workgroup barrier that precedes the increment, and
+// the last workgroup loads them only after its increment has returned, so every chunk's
+// stores completed before the loads are issued.  Every wave of the workgroup runs this
+// (uniform: the item is the workgroup's), so its two barriers match.
+template <int DT, int D>
+__device__ __forceinline__ void split_arrive_and_merge(const FwdParams& p, const WorkItem& w, int qt128,
+                                                       int per_chunk, int* s_last) {
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // this wave's partial stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned last = (unsigned)(per_chunk * w.ns) - 1u;
+    const unsigned old = atomicInc(p.merge_cnt + w.slot0, last);
+    *s_last = old == last ? 1 : 0;
+  }
+  __syncthreads();
+  if (*s_last == 0) return;
+  merge_block_in_kernel<DT, D>(p, w.bh, qt128, w.slot0, w.ns);
+}
 }  // namespace ta
+
+// Arrival counters of the in-kernel merge (FwdParams::merge_cnt points into one region).
+// The host zeroes them once when it loads this code object; every launch leaves them zero.
+__device__ unsigned ta_merge_counters[ta::kMergeRegions * ta::kMergeRegionCounters];
 
 // Two extern "C" entries per (dtype, D, causal, tail): the whole-row kernel
 // ta_fwd_pp_<f16|bf16>_d<D>_c<0|1>_t<0|1> and the split-key-range kernel

@@ -120,6 +120,9 @@ struct WorkItem {
   int t_beg;  // key steps [t_beg, t_end); t_end = -1 for "every step the block needs"
   int t_end;
   int slot;   // partial slot, or -1 when the item is the block's only chunk
+  int slot0;  // with slot >= 0: the slot of the block's chunk 0 (chunk i is in slot0 + i),
+              // which also names the block among the launch's split blocks
+  int ns;     // with slot >= 0: the block's chunk count
 };
 
 // Whole-row grid: one item per (b, h, query block).  sched >= 1 (with 8 | total) maps
@@ -148,6 +151,8 @@ TA_HD inline WorkItem whole_item(int blk, int n_bh, int nq, int sched, bool caus
   w.t_beg = 0;
   w.t_end = -1;
   w.slot = -1;
+  w.slot0 = -1;
+  w.ns = 1;
   return w;
 }
 
@@ -170,6 +175,8 @@ TA_HD inline void pair_items(int blk, int n_bh, int nq, int sched, WorkItem* a, 
   a->t_beg = b->t_beg = 0;
   a->t_end = b->t_end = -1;
   a->slot = b->slot = -1;
+  a->slot0 = b->slot0 = -1;
+  a->ns = b->ns = 1;
 }
 
 // Split grid: `items` per (b, h), ranked from the heaviest block down; sched >= 1 (with
@@ -210,6 +217,8 @@ TA_HD inline WorkItem split_item(int blk, int n_bh, int items, int sched, bool c
   w.t_beg = part == 0 ? 0 : len - (ns - part) * c;
   w.t_end = len - (ns - 1 - part) * c;
   w.slot = ns > 1 ? w.bh * slots + w.slot : -1;
+  w.slot0 = ns > 1 ? w.slot - part : -1;
+  w.ns = ns;
   return w;
 }
 
@@ -243,6 +252,8 @@ TA_HD inline void psplit_items(int blk, int n_bh, int nq, int sched, int f, Work
   b->t_beg = b->t_end = 0;
   b->slot = -1;
   a->slot = -1;
+  a->slot0 = b->slot0 = -1;
+  a->ns = b->ns = 1;
   const int np = nq >> 1;
   if (r >= 2 * np) {  // the middle block of an odd nq
     a->qt = np;
@@ -257,7 +268,11 @@ TA_HD inline void psplit_items(int blk, int n_bh, int nq, int sched, int f, Work
     a->qt = heavy;
     a->t_beg = k;
     a->t_end = heavy + 1;
-    if (k > 0) a->slot = bh * 2 * P + 2 * pr + 1;
+    if (k > 0) {
+      a->slot = bh * 2 * P + 2 * pr + 1;
+      a->slot0 = a->slot - 1;
+      a->ns = 2;
+    }
   } else {
     a->qt = pr;
     a->t_beg = 0;
@@ -267,6 +282,8 @@ TA_HD inline void psplit_items(int blk, int n_bh, int nq, int sched, int f, Work
       b->t_beg = 0;
       b->t_end = k;
       b->slot = bh * 2 * P + 2 * pr;
+      b->slot0 = b->slot;
+      b->ns = 2;
     }
   }
 }

@@ -53,6 +53,13 @@ std::string g_dir;   // code object directory; empty = next to this library
 std::map<std::pair<int, std::string>, hipModule_t> g_modules;  // (device, code object file)
 std::map<std::pair<int, std::string>, hipFunction_t> g_funcs;  // (device, kernel name)
 std::map<int, bool> g_arch_ok;                                 // device -> gfx950?
+// In-kernel merge: the device address of attn_fwd_pp.hsaco's ta_merge_counters per device
+// (zeroed when the module loads), and the counter region each (device, stream) launches
+// with, so that split launches that may overlap (other streams) never share counters.
+std::map<int, unsigned*> g_counters;
+std::map<std::pair<int, void*>, int> g_regions;
+std::map<int, int> g_regions_used;
+const char kPPObject[] = "attn_fwd_pp.hsaco";
 
 std::string default_dir() {
   Dl_info info;
@@ -212,6 +219,27 @@ ta_status get_function_locked(int device, const KernelId& id, hipFunction_t* out
     hipError_t e = hipModuleLoad(&mod, path.c_str());
     if (e != hipSuccess)
       return fail(TA_ENOKERNEL, "hipModuleLoad(%s): %s", path.c_str(), hipGetErrorString(e));
+    if (id.file == kPPObject) {
+      // The merge counters start at zero; every launch leaves them zero.  Zeroed here
+      // once per load, synchronously, before any kernel of the module can run.
+      hipDeviceptr_t cnt = nullptr;
+      size_t bytes = 0;
+      e = hipModuleGetGlobal(&cnt, &bytes, mod, "ta_merge_counters");
+      if (e == hipSuccess && bytes == sizeof(unsigned) * ta::kMergeRegions * ta::kMergeRegionCounters) {
+        e = hipMemsetAsync(cnt, 0, bytes, nullptr);
+        if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+      } else if (e == hipSuccess) {
+        e = hipErrorInvalidValue;
+      }
+      if (e != hipSuccess) {
+        (void)hipModuleUnload(mod);
+        return fail(TA_ENOKERNEL, "merge counters of %s: %s", path.c_str(), hipGetErrorString(e));
+      }
+      g_counters[device] = static_cast<unsigned*>(cnt);
+      for (auto it = g_regions.begin(); it != g_regions.end();)
+        it = it->first.first == device ? g_regions.erase(it) : std::next(it);
+      g_regions_used[device] = 0;
+    }
     g_modules[mk] = mod;
   } else {
     mod = mit->second;
@@ -248,7 +276,30 @@ ta_status cache_reset_locked() {
   }
   g_modules.clear();
   g_funcs.clear();
+  g_counters.clear();
+  g_regions.clear();
+  g_regions_used.clear();
   return st;
+}
+
+// Caller holds g_mu and has loaded attn_fwd_pp.hsaco on `device`.  The counter region of
+// (device, stream): the stream's own, or a new one while any is left; null when every
+// region belongs to other streams (the launch then runs the merge kernel).
+unsigned* merge_counters_locked(int device, void* stream) {
+  auto cit = g_counters.find(device);
+  if (cit == g_counters.end()) return nullptr;
+  const auto key = std::make_pair(device, stream);
+  auto rit = g_regions.find(key);
+  int region;
+  if (rit != g_regions.end()) {
+    region = rit->second;
+  } else {
+    int& used = g_regions_used[device];
+    if (used >= ta::kMergeRegions) return nullptr;
+    region = used++;
+    g_regions[key] = region;
+  }
+  return cit->second + static_cast<int64_t>(region) * ta::kMergeRegionCounters;
 }
 
 // ---- split key ranges ------------------------------------------------------------------
@@ -579,6 +630,7 @@ struct LaunchPlan {
   int32_t layout = TA_LAYOUT_WHOLE_ROWS;
   int32_t chunk = 0;     // split actually run (0 = whole rows)
   bool merge = false;    // a merge kernel follows (split layouts)
+  bool merge_in_kernel = false;  // ... unless the split kernel merges (counters fit)
   KernelId merge_id;
   int64_t merge_grid = 0;
   SplitLayout split;     // valid when merge
@@ -624,6 +676,20 @@ ta_status plan_launch(const ta_fwd_args* a, int64_t n_bh, int64_t n_qblk, int32_
     pl->merge_grid = n_bh * l.merge * (kSplitRows / ta::merge_rows_per_wg(d8));
     pl->split = l;
     pl->ws_bytes = split_ws_bytes(n_bh, a->D, l);
+    // The split kernel merges its blocks itself (the last workgroup to finish a block) when
+    // a counter per block fits a region (a block's counter is its chunk-0 slot, below
+    // n_bh * slots) and either no block has more than two chunks or the merges are many
+    // (3/8 of the CUs or more) and so spread over the chip.  A block of many chunks merged
+    // by one workgroup at the end of a small grid costs more than the merge kernel, which
+    // spreads each block over 8-16 workgroups (B1 H1 S4096 causal, 7 chunks: 17.8 -> 22.2
+    // µs in the kernel; the paired split at C3 S = 4096: 44.4 -> 43.6 µs, D = 64
+    // 30.6 -> 28.9).
+    const int64_t nq128 = (a->S + kSplitRows - 1) / kSplitRows;
+    const int64_t max_ns = chunk_steps == TA_SPLIT_PAIRS ? 2
+                           : a->causal                  ? (nq128 + chunk_steps - 1) / chunk_steps
+                                                        : l.ns;
+    pl->merge_in_kernel = n_bh * l.slots <= ta::kMergeRegionCounters &&
+                          (max_ns <= 2 || 8 * n_bh * l.merge >= 3 * (int64_t)ncu);
     ta_status gst = check_grid(pl->grid, 512u, "split kernel");
     if (gst == TA_OK) gst = check_grid(pl->merge_grid, pl->merge_id.block, "merge kernel");
     return gst;
@@ -665,6 +731,7 @@ void fill_desc(const ta_fwd_args* a, const LaunchPlan& pl, int ncu, ta_launch_de
   if (pl.merge) {
     snprintf(d->merge_kernel, sizeof(d->merge_kernel), "%s", pl.merge_id.name.c_str());
     d->merge_grid = pl.merge_grid;
+    d->merge_in_kernel = pl.merge_in_kernel ? 1 : 0;
     d->merge_block = static_cast<int32_t>(pl.merge_id.block);
   }
   d->workspace_bytes = pl.ws_bytes;
@@ -703,12 +770,14 @@ ta_status launch_plan_locked(const ta_fwd_args* a, const LaunchPlan& pl, ta::Fwd
   if (pl.layout == TA_LAYOUT_ROWS256) p->n_qblk = static_cast<int32_t>((a->S + 255) / 256);
   // the split numbering and the merge count 128-row blocks, whatever rows a workgroup takes
   if (pl.merge) p->n_qblk = static_cast<int32_t>((a->S + kSplitRows - 1) / kSplitRows);
+  p->merge_cnt = nullptr;
+  if (pl.merge && pl.merge_in_kernel) p->merge_cnt = merge_counters_locked(a->device, stream);
   void* params[] = {p};
   hipStream_t hs = static_cast<hipStream_t>(stream);
   hipError_t e = hipModuleLaunchKernel(fn, static_cast<unsigned>(pl.grid), 1, 1, pl.main.block, 1, 1,
                                        0, hs, params, nullptr);
   if (e != hipSuccess) return fail(TA_EHIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
-  if (pl.merge) {
+  if (pl.merge && p->merge_cnt == nullptr) {
     e = hipModuleLaunchKernel(mfn, static_cast<unsigned>(pl.merge_grid), 1, 1, pl.merge_id.block, 1,
                               1, 0, hs, params, nullptr);
     if (e != hipSuccess) return fail(TA_EHIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
@@ -1049,7 +1118,9 @@ ta_status ta_sdpa_fwd_split(const ta_fwd_args* a, int32_t chunk_steps, void* wor
   SplitLayout l;
   if (chunk_steps == 0 || !layout_for(a->S, a->causal != 0, chunk_steps, &l))
     return ta_sdpa_fwd(a, stream);
-  // The split plan needs no compute-unit count (only whole rows choose by it).
+  // Planned once before any device call (grids and the workspace are checked there), and
+  // again under the lock with the device's compute-unit count, which decides whether the
+  // split kernel merges its blocks itself.
   LaunchPlan pl;
   ta_status st = plan_launch(a, n_bh, n_qblk, chunk_steps, 1, &pl);
   if (st != TA_OK) return st;
@@ -1074,6 +1145,10 @@ ta_status ta_sdpa_fwd_split(const ta_fwd_args* a, int32_t chunk_steps, void* wor
   DeviceGuard guard(a->device);
   if (guard.err != hipSuccess)
     return fail(TA_EHIP, "set device %d: %s", a->device, hipGetErrorString(guard.err));
+  int ncu = 0;
+  st = cu_count_locked(a->device, &ncu);
+  if (st == TA_OK) st = plan_launch(a, n_bh, n_qblk, chunk_steps, ncu, &pl);
+  if (st != TA_OK) return st;
   return launch_plan_locked(a, pl, &p, stream);
 }
 
