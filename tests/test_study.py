@@ -110,6 +110,28 @@ def test_rocprof_summary_from_profiler_csvs(tmp_path):
     assert (tmp_path / "o" / "rocprof_summary.md").exists()
 
 
+def test_kernel_trace_table_per_kernel_and_grid(tmp_path):
+    """Dispatch durations grouped by (kernel, workgroups = Grid_Size_X / Workgroup_Size_X):
+    one symbol at two grid sizes is two rows; other kernels are filtered out."""
+    d = tmp_path / "kt"
+    d.mkdir()
+    hdr = ["Kernel_Name", "Grid_Size_X", "Workgroup_Size_X", "Start_Timestamp", "End_Timestamp"]
+    rows = [["ta_fwd_pp64_bf16_d128_c1_t0", 64 * 512, 512, 1000, 9800],      # 8.8 us
+            ["ta_fwd_pp64_bf16_d128_c1_t0", 64 * 512, 512, 20000, 28600],    # 8.6 us
+            ["ta_fwd_pp64_bf16_d128_c1_t0", 64 * 512, 512, 30000, 39000],    # 9.0 us
+            ["ta_fwd_pp64_bf16_d128_c1_t0", 128 * 512, 512, 50000, 61760],   # 11.76 us
+            ["copy_kernel", 1024, 256, 0, 100]]
+    _write(d / "run_kernel_trace.csv", hdr, rows)
+    t = study.kernel_trace_table(d, "ta_fwd")
+    assert [(r["kernel"], r["workgroups"], r["calls"]) for r in t] == [
+        ("ta_fwd_pp64_bf16_d128_c1_t0", 64, 3), ("ta_fwd_pp64_bf16_d128_c1_t0", 128, 1)]
+    assert t[0]["median_us"] == pytest.approx(8.8) and t[0]["min_us"] == pytest.approx(8.6)
+    assert t[0]["mean_us"] == pytest.approx((8.8 + 8.6 + 9.0) / 3)
+    assert study.main(["--out", str(tmp_path / "o"), "--rocprof-dir", str(d), "--trace-table"]) == 0
+    text = (tmp_path / "o" / "kernel_trace.md").read_text()
+    assert "| ta_fwd_pp64_bf16_d128_c1_t0 | 128 | 1 | 11.76 | 11.76 | 11.76 |" in text
+
+
 def test_diagnose_flags():
     assert any("underfed" in x for x in study.diagnose({"SQ_VALU_MFMA_BUSY_CYCLES": 10.0, "GRBM_GUI_ACTIVE": 8.0 * 1.0}))
     assert any("bank conflicts" in x for x in study.diagnose({"SQ_LDS_BANK_CONFLICT": 5.0}))

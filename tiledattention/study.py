@@ -441,6 +441,32 @@ def rocprof_metrics(prof_dir: Path, kernel_substring: str) -> dict[str, float | 
     return m
 
 
+def kernel_trace_table(prof_dir: Path, kernel_substring: str = "ta_fwd") -> list[dict]:
+    """Per (kernel, workgroups) dispatch durations from every ``*kernel_trace.csv`` below a
+    ``rocprofv3 --kernel-trace`` tree: calls, median, min and mean in microseconds.  One
+    kernel symbol can run several workloads (grid sizes), which ``*kernel_stats.csv`` lumps
+    together."""
+    durs: dict[tuple[str, int], list[float]] = {}
+    for trace in Path(prof_dir).rglob("*kernel_trace.csv"):
+        for r in _read_csv(trace):
+            name = r["Kernel_Name"]
+            if kernel_substring not in name:
+                continue
+            wg = int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"]))
+            durs.setdefault((name, wg), []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    return [{"kernel": k, "workgroups": wg, "calls": len(v), "median_us": statistics.median(v),
+             "min_us": min(v), "mean_us": statistics.mean(v)} for (k, wg), v in sorted(durs.items())]
+
+
+def write_kernel_trace_table(path: Path, rows: list[dict], config: dict[str, object]) -> None:
+    lines = ["# rocprofv3 kernel trace: dispatch durations per kernel and grid", ""]
+    lines += [f"- {k}: {v}" for k, v in config.items()]
+    lines += ["", "| kernel | workgroups | calls | median us | min us | mean us |", "|---|---|---|---|---|---|"]
+    lines += [f"| {r['kernel']} | {r['workgroups']} | {r['calls']} | {r['median_us']:.2f} | {r['min_us']:.2f} | "
+              f"{r['mean_us']:.2f} |" for r in rows]
+    Path(path).write_text("\n".join(lines) + "\n")
+
+
 def _ratio(m, a, b, scale=100.0):
     x, y = m.get(a), m.get(b)
     return None if x is None or not y else scale * x / y
@@ -530,6 +556,8 @@ def _args(argv=None):
     ap.add_argument("--rocprof-dir", default=None,
                     help="summarise an existing rocprofv3 output tree instead of benchmarking")
     ap.add_argument("--kernel", default="ta_fwd", help="primary-kernel name filter for --rocprof-dir")
+    ap.add_argument("--trace-table", action="store_true",
+                    help="with --rocprof-dir: also write kernel_trace.md (durations per kernel and grid)")
     return ap.parse_args(argv)
 
 
@@ -542,6 +570,10 @@ def main(argv=None) -> int:
         write_rocprof_summary(out / "rocprof_summary.md", [("tiledattention", m)],
                               {"rocprofv3 output": args.rocprof_dir, "kernel filter": args.kernel})
         print(f"[study] wrote {out / 'rocprof_summary.md'}")
+        if args.trace_table:
+            write_kernel_trace_table(out / "kernel_trace.md", kernel_trace_table(Path(args.rocprof_dir), args.kernel),
+                                     {"rocprofv3 output": args.rocprof_dir, "kernel filter": args.kernel})
+            print(f"[study] wrote {out / 'kernel_trace.md'}")
         return 0
     import torch
 
