@@ -162,7 +162,9 @@ ta_status ta_split_workspace_size(const ta_fwd_args* args, int32_t chunk_steps, 
  * work on `stream` has finished.  The split blocks are merged by the split kernel itself
  * (ta_launch_desc.merge_in_kernel) with arrival counters the library keeps per (device,
  * stream) in the code object, or, past 16 streams on a device, by a merge kernel on
- * `stream` after it. */
+ * `stream` after it.  Every launch leaves its counters at zero, so a launch captured in a
+ * HIP graph replays as it ran (it keeps the capture stream's counter region: its replays
+ * must not overlap a split launch on that stream). */
 ta_status ta_sdpa_fwd_split(const ta_fwd_args* args, int32_t chunk_steps, void* workspace,
                             int64_t workspace_bytes, void* stream);
 

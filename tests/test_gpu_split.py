@@ -323,3 +323,48 @@ def test_in_kernel_merge_repeated_and_on_many_streams(gpu, shape, dtype, split, 
     torch.cuda.synchronize()
     for i, o in enumerate(per):
         assert torch.equal(o, first), f"stream {i}: max |diff| {float((o.float() - first.float()).abs().max())}"
+
+
+def test_split_launch_in_a_hip_graph(gpu):
+    """A split launch merged in the kernel (the paired split at C3's S=4096 shape, on fewer
+    heads) captured in a HIP graph (torch.cuda.graph) and replayed five times, with eager
+    work and synchronisations between the replays: every replay equals the eager result
+    (the arrival counters are left at zero by every launch, so a replay needs no reset), and
+    the eager result meets the oracle.  The code object is loaded by an eager call first."""
+    import torch
+
+    from tiledattention import sdpa
+    from tiledattention.kernels import flash_fwd
+
+    shape = (1, 2, 4096, 128)
+    q, k, v = inputs(shape, "bfloat16", 4242)
+    rows = sample_rows(4096, 96)
+    ref = oracle_f32(q, k, v, causal=True, rows=rows)
+    dev = torch.device("cuda:0")
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    with knobs(split="pairs", tile_m=128, tile_n=64, accum_mode="fp32"):
+        desc = flash_fwd.describe_call(qd, kd, vd, causal=True)
+        assert desc["layout"] == 4 and desc["merge_in_kernel"] == 1, desc
+        say("split launch in a HIP graph: eager call")
+        eager = sdpa(qd, kd, vd, causal=True)
+        torch.cuda.synchronize()
+        s = torch.cuda.Stream(dev)
+        s.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(s):
+            sdpa(qd, kd, vd, causal=True)  # warm the plan cache on the capture stream
+        torch.cuda.current_stream(dev).wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        say("split launch in a HIP graph: capture")
+        with torch.cuda.graph(g):
+            captured = sdpa(qd, kd, vd, causal=True)
+    torch.cuda.synchronize()
+    for i in range(5):
+        say(f"split launch in a HIP graph: replay {i}")
+        captured.fill_(float("nan"))
+        g.replay()
+        # eager work between replays, on the default stream
+        _ = (qd.float() * 2).sum()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, eager), f"replay {i}: max |diff| {float((captured.float() - eager.float()).abs().max())}"
+    check_close(as_f32(eager, rows), ref, "bfloat16", what="split in a graph (eager)")
