@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define TA_ABI_VERSION 5
+#define TA_ABI_VERSION 6
 
 typedef enum ta_status {
   TA_OK = 0,
@@ -146,8 +146,9 @@ ta_status ta_split_plan(const ta_fwd_args* args, int32_t* chunk_steps);
 int32_t ta_split_plan_model(int64_t S, int64_t n_bh, int32_t causal, int32_t compute_units);
 
 /* The same for blocks of `rows` query rows (128: the model above; 64: the 64-row kernel's
- * chunks, planned for grids whose 64-row blocks fill at most half of the compute units) at
- * kernel head dim `head_dim`; 0 for no split. */
+ * chunks, planned for grids whose 64-row blocks fill at most half of the compute units and
+ * where the wide kernel does not run, TA_LAYOUT_WIDE) at kernel head dim `head_dim`; 0 for
+ * no split. */
 int32_t ta_split_plan_model_rows(int64_t S, int64_t n_bh, int32_t causal, int32_t head_dim, int32_t rows,
                                  int32_t compute_units);
 
@@ -193,7 +194,9 @@ typedef enum ta_layout {
   TA_LAYOUT_ROWS256 = 2,      /* non-causal 256-row blocks (the two wave groups own
                                  different rows) */
   TA_LAYOUT_SPLIT = 3,        /* chunks of key steps, merged by a second kernel */
-  TA_LAYOUT_PAIRED_SPLIT = 4  /* the paired split (TA_SPLIT_PAIRS), merged likewise */
+  TA_LAYOUT_PAIRED_SPLIT = 4, /* the paired split (TA_SPLIT_PAIRS), merged likewise */
+  TA_LAYOUT_WIDE = 5          /* 32-row blocks whose eight waves split the keys of every
+                                 pass (64-row tiles on grids of one round of the CUs) */
 } ta_layout;
 
 /* What one forward enqueues: the kernels, their grids and code object, and the decisions
@@ -204,7 +207,7 @@ typedef struct ta_launch_desc {
   char kernel[96];        /* the attention kernel's symbol */
   int64_t grid;           /* its workgroups (0: zero-size problem, nothing launched) */
   int32_t block;          /* its threads per workgroup */
-  int32_t rows;           /* query rows per query block it processes (64, 128 or 256) */
+  int32_t rows;           /* query rows per query block it processes (32, 64, 128 or 256) */
   int32_t tail;           /* 1: the tail-masked variant */
   int32_t layout;         /* ta_layout */
   int32_t chunk_steps;    /* the split that runs: 0 whole rows, > 0 chunk length, or

@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_status_names(lib):
-    assert lib.ta_abi_version() == _lib.ABI_VERSION == 5
+    assert lib.ta_abi_version() == _lib.ABI_VERSION == 6
     names = [lib.ta_status_string(i).decode() for i in range(5)]
     assert names == ["TA_OK", "TA_EINVAL", "TA_EUNSUPPORTED", "TA_ENOKERNEL", "TA_EHIP"]
     assert lib.ta_status_string(99).decode() == "TA_UNKNOWN"
@@ -191,8 +191,9 @@ def test_code_objects_built_for_gfx950():
         # hipcc --genco writes a clang offload bundle holding the gfx950 ELF
         assert data.startswith(b"__CLANG_OFFLOAD_BUNDLE__") or data[:4] == b"\x7fELF"
         assert b"amdgcn-amd-amdhsa--gfx950" in data and b"\x7fELF" in data
-        names = ("ta_fwd_pp_bf16_d128", "ta_fwd_pp_f16_d64") if path.name == "attn_fwd_pp.hsaco" \
-            else ("ta_fwd_bf16_d128", "ta_fwd_f16_d64")
+        names = {"attn_fwd_pp.hsaco": ("ta_fwd_pp_bf16_d128", "ta_fwd_pp_f16_d64"),
+                 "attn_fwd_wide.hsaco": ("ta_fwd_wide_bf16_d128", "ta_fwd_wide_f16_d64")}.get(
+                     path.name, ("ta_fwd_bf16_d128", "ta_fwd_f16_d64"))
         for name in names:
             assert name.encode() in data
 

@@ -63,10 +63,20 @@ def _configs():
             yield dtype, tiles, accum, d
 
 
+def _wide_rule(bh, s, d, cu=CU):
+    """The wide kernel's rule for a whole-row 64-row tile with fp32 accumulation: D 64 or
+    128, 32-row blocks in one round of the CUs, at most two passes (512 keys at D = 128,
+    1024 at D = 64), or at most four on more than half the CUs."""
+    grid = bh * -(-s // 32)
+    passes = -(-s // (512 if d == 128 else 1024))
+    return d in (64, 128) and grid <= cu and (passes <= 2 or (passes <= 4 and 2 * grid > cu))
+
+
 @pytest.mark.parametrize("dtype,tiles,accum,d", list(_configs()))
 def test_whole_row_kernel_per_configuration(lib, objects, dtype, tiles, accum, d):
     """One small head (B1 H1: no pairs, no 256-row blocks) at an aligned and a ragged S;
-    the symbol and the tail variant follow the families, and the kernel exists."""
+    the symbol and the tail variant follow the families, and the kernel exists.  64-row
+    fp32 tiles at D = 64 / 128 run the wide kernel on such grids."""
     dt = "bf16" if dtype == _lib.TA_BF16 else "f16"
     tm, tn = tiles
     eight = (accum == _lib.TA_ACC_FP32 and ((tm == 128 and d <= 160) or (tm == 64 and d in (64, 96, 128, 160)))) \
@@ -78,10 +88,15 @@ def test_whole_row_kernel_per_configuration(lib, objects, dtype, tiles, accum, d
             desc = _d(lib, S=s, D=d, dtype=dtype, tile_m=tm, tile_n=tn, accum=accum, causal=causal,
                       aligned=aligned)
             f, sym = _expected_symbol(dt=dt, d=d, tm=tm, tn=tn, causal=causal, tail=tail, accum=accum)
+            wide = accum == _lib.TA_ACC_FP32 and tm == 64 and _wide_rule(1, s, d)
+            if wide:
+                f, sym = "attn_fwd_wide.hsaco", f"ta_fwd_wide_{dt}_d{d}_c{int(causal)}_t{int(tail)}"
             assert (desc.code_object.decode(), desc.kernel.decode()) == (f, sym)
             assert desc.kernel + b"\x00" in objects[f], sym
-            assert desc.layout == _lib.TA_LAYOUT_WHOLE_ROWS and desc.tail == int(tail)
-            assert desc.grid == -(-s // tm) and desc.rows == tm
+            assert desc.layout == (_lib.TA_LAYOUT_WIDE if wide else _lib.TA_LAYOUT_WHOLE_ROWS)
+            assert desc.tail == int(tail)
+            rows = 32 if wide else tm
+            assert desc.grid == -(-s // rows) and desc.rows == rows
             assert desc.block == (512 if eight else 2 * tm)
             assert desc.in_place_pad == int(eight)
             assert desc.split_capable == int(accum == _lib.TA_ACC_FP32 and d <= 160 and (tm == 128 or d != 256))
@@ -289,12 +304,15 @@ def test_zero_size_and_invalid_requests(lib):
 
 def test_policy_defaults_run_the_described_kernels(lib):
     """The host policy's default tiles for the BASELINE configurations, through the library:
-    C1 64-row causal (tail variant: S = 64 is not a whole 128-key step), C2 (64, 64) non-causal, C3 S=512..2048 the 64-row kernel and S=4096
+    C1 64-row tile on the wide kernel (tail variant: S = 64 is not a whole 128-key step), C2
+    (64, 64) non-causal and C3 S = 512 the wide kernel (32-row blocks in one round of the
+    CUs), C3 S = 2048 the 64-row kernel (512 blocks of 32 rows would be two rounds), S = 4096
     whole 128-row blocks, S=8192 causal pairs, C4 256-row blocks, C5 causal pairs."""
     cases = [
-        ((1, 2, 64, 64), True, "ta_fwd_pp64_f16_d64_c1_t1", _lib.TA_LAYOUT_WHOLE_ROWS, _lib.TA_FP16),
-        ((1, 8, 1024, 64), False, "ta_fwd_pp64_f16_d64_c0_t0", _lib.TA_LAYOUT_WHOLE_ROWS, _lib.TA_FP16),
-        ((1, 8, 512, 128), True, "ta_fwd_pp64_bf16_d128_c1_t0", _lib.TA_LAYOUT_WHOLE_ROWS, _lib.TA_BF16),
+        ((1, 2, 64, 64), True, "ta_fwd_wide_f16_d64_c1_t1", _lib.TA_LAYOUT_WIDE, _lib.TA_FP16),
+        ((1, 8, 1024, 64), False, "ta_fwd_wide_f16_d64_c0_t0", _lib.TA_LAYOUT_WIDE, _lib.TA_FP16),
+        ((1, 8, 512, 128), True, "ta_fwd_wide_bf16_d128_c1_t0", _lib.TA_LAYOUT_WIDE, _lib.TA_BF16),
+        ((1, 8, 1024, 128), True, "ta_fwd_wide_bf16_d128_c1_t0", _lib.TA_LAYOUT_WIDE, _lib.TA_BF16),
         ((1, 8, 2048, 128), True, "ta_fwd_pp64_bf16_d128_c1_t0", _lib.TA_LAYOUT_WHOLE_ROWS, _lib.TA_BF16),
         ((1, 8, 4096, 128), True, "ta_fwd_pp_bf16_d128_c1_t0", _lib.TA_LAYOUT_WHOLE_ROWS, _lib.TA_BF16),
         ((1, 8, 8192, 128), True, "ta_fwd_pp_pair_bf16_d128_c1_t0", _lib.TA_LAYOUT_PAIRS, _lib.TA_BF16),

@@ -7,16 +7,18 @@ causally masked score is replaced by -inf whatever its value, so rows before a N
 finite.  One case is implementation-defined: a NaN in a value row j under the causal mask.
 The oracle computes row i over its visible keys only (rows i >= j are NaN); a tiled kernel
 multiplies the masked keys' P = 0 by V inside the diagonal tile, and 0 x NaN = NaN, so here
-every row of the 128-row query block holding j is NaN as well (the reference's tiled kernel
-does the same at its own tile size; its eager baseline, which multiplies the full masked P,
-makes every row NaN).  That case is checked against exactly that rule."""
+every row of the query block holding j is NaN as well, from the block's first row on (128
+rows for the 128-row and 64-row kernels, whose diagonal key step is 128 keys; 32 for the
+wide kernel's blocks; the reference's tiled kernel does the same at its own tile size; its
+eager baseline, which multiplies the full masked P, makes every row NaN).  That case is
+checked against exactly that rule, with the block size of the kernel that ran."""
 
 from __future__ import annotations
 
 import numpy as np
 import pytest
 
-from tests.parity_util import TOL, as_f32, inputs, oracle_f32, run_gpu, say
+from tests.parity_util import TOL, as_f32, inputs, kernel_for, oracle_f32, run_gpu, say
 
 pytestmark = pytest.mark.gpu
 
@@ -60,11 +62,14 @@ def test_nonfinite_propagation(gpu, tensor, row, value, causal):
     with np.errstate(invalid="ignore", over="ignore"):
         ref = oracle_f32(q, k, v, causal=causal)
     assert not np.isfinite(ref).all()
-    nan_from = (row // 128) * 128 if (tensor == "v" and causal) else None
-    if nan_from is not None:
+    poisoned_v = tensor == "v" and causal
+    if poisoned_v:
         assert np.isnan(ref[0, 1, row:, :]).all() and np.isfinite(ref[0, 1, :row, :]).all()
     for split in ("off", 1):
-        say(f"non-finite {tensor}[0,1,{row},:]={value} causal={causal} split={split}")
+        kernel = kernel_for(q, k, v, causal=causal, split=split, accum_mode="fp32")
+        block = 32 if kernel.startswith("ta_fwd_wide_") else 128
+        nan_from = (row // block) * block if poisoned_v else None
+        say(f"non-finite {tensor}[0,1,{row},:]={value} causal={causal} split={split} kernel={kernel}")
         out = run_gpu(q, k, v, causal=causal, split=split, accum_mode="fp32")
         _compare(as_f32(out), ref, "bfloat16", f"{tensor} row {row} = {value} causal={causal} split={split}",
                  nan_from_row=nan_from)

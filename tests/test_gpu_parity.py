@@ -367,23 +367,26 @@ def test_eight_wave_64_row_tiles(gpu, tn, s, causal, dtype):
     """Tiles (64, tn) with fp32 accumulation run the 64-row eight-wave kernel (four key
     slices per row block, merged at the end): lengths that are multiples of 64 but not of
     the 128-key step (320, 448: the tail-masked variant), ragged ones, D = 64 and 128, and
-    narrower head dims padded in place (D = 48 and 96); [B,S,H,D] views for one case."""
+    narrower head dims padded in place (D = 48 and 96); [B,S,H,D] views for one case.  The
+    heads are enough that 32-row blocks would need a second round of the CUs: smaller grids
+    run the wide kernel at D = 64 and 128 (tests/test_gpu_wide.py)."""
     import torch
 
     from tiledattention import sdpa
 
+    h = max(3, 256 // (2 * -(-s // 32)) + 1)
     for d in (64, 128, 48, 96):
-        q, k, v = inputs((2, 3, s, d), dtype, 6400 + s + d + tn)
+        q, k, v = inputs((2, h, s, d), dtype, 6400 + s + d + tn)
         assert kernel_for(q, k, v, causal=causal, tile_m=64, tile_n=tn).startswith("ta_fwd_pp64_")
-        say(f"64-row eight-wave {dtype} (2,3,{s},{d}) causal={causal} tiles=(64,{tn})")
+        say(f"64-row eight-wave {dtype} (2,{h},{s},{d}) causal={causal} tiles=(64,{tn})")
         out = run_gpu(q, k, v, causal=causal, tile_m=64, tile_n=tn)
-        assert out.shape == (2, 3, s, d)
+        assert out.shape == (2, h, s, d)
         ref = oracle_f32(q, k, v, causal=causal)
         check_close(as_f32(out), ref, dtype, what=f"64-row D={d}")
         if d == 96 and s == 1000:
             dev = torch.device("cuda:0")
             bshd = [t.transpose(1, 2).contiguous().to(dev).transpose(1, 2) for t in (q, k, v)]
-            say(f"64-row eight-wave {dtype} (2,3,{s},{d}) [B,S,H,D] views")
+            say(f"64-row eight-wave {dtype} (2,{h},{s},{d}) [B,S,H,D] views")
             from tests.parity_util import knobs
             with knobs(tile_m=64, tile_n=tn):
                 out = sdpa(*bshd, causal=causal)

@@ -17,7 +17,7 @@ from threading import Lock
 
 from ._errors import DependencyError
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 TA_OK = 0
 TA_EINVAL = 1
@@ -41,6 +41,7 @@ TA_LAYOUT_PAIRS = 1
 TA_LAYOUT_ROWS256 = 2
 TA_LAYOUT_SPLIT = 3
 TA_LAYOUT_PAIRED_SPLIT = 4
+TA_LAYOUT_WIDE = 5
 
 
 # Every symbol the header declares; tests check the built library exports all of them.
@@ -198,7 +199,8 @@ def library_path() -> Path:
 
 def code_object_paths() -> list[Path]:
     d = lib_dir()
-    return [d / f"attn_fwd_m{tm}_n{tn}.hsaco" for tm, tn in TILE_SHAPES] + [d / "attn_fwd_pp.hsaco"]
+    return [d / f"attn_fwd_m{tm}_n{tn}.hsaco" for tm, tn in TILE_SHAPES] + [d / "attn_fwd_pp.hsaco",
+                                                                            d / "attn_fwd_wide.hsaco"]
 
 
 def _declare(lib: ctypes.CDLL) -> None:

@@ -111,6 +111,21 @@ __device__ static inline float fast_log2(float x) { return __builtin_amdgcn_logf
 __device__ static inline float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 __device__ static inline float vmax3(float a, float b, float c) { return vmax(a, vmax(b, c)); }
 
+// 16-byte chunk swizzle of the unpadded LDS key tiles of the eight-wave and wide kernels
+// (row = 2D bytes, 64 banks x 4 bytes):
+// * K: a b128 read pass covers 16 consecutive rows at one logical chunk;
+//   physical chunk = logical ^ (row & 15) for D = 128, ^ ((row >> 1) & 7) for D = 64.
+// * V: a b64 transposed read pass covers 4 consecutive rows x 4 logical chunks;
+//   physical chunk = logical ^ 4 * (row & 3) for D = 128, ^ 4 * ((row >> 1) & 1) for D = 64.
+template <int D>
+__device__ static inline int pp_swz_k(int row) {
+  return D == 128 ? (row & 15) : ((row >> 1) & 7);
+}
+template <int D>
+__device__ static inline int pp_swz_v(int row) {
+  return D == 128 ? ((row & 3) << 2) : (((row >> 1) & 1) << 2);
+}
+
 // Buffer resource for rows [0, rows) of a row-major tensor with `row_bytes` between rows:
 // loads past the last row return zeros (the hardware range check), which zero-fills the
 // ragged last key tile without any per-lane select.

@@ -39,20 +39,6 @@
 
 namespace ta {
 
-// 16-byte chunk swizzle of the unpadded LDS tiles (row = 2D bytes, 64 banks x 4 bytes):
-// * K: a b128 read pass covers 16 consecutive rows at one logical chunk;
-//   physical chunk = logical ^ (row & 15) for D = 128, ^ ((row >> 1) & 7) for D = 64.
-// * V: a b64 transposed read pass covers 4 consecutive rows x 4 logical chunks;
-//   physical chunk = logical ^ 4 * (row & 3) for D = 128, ^ 4 * ((row >> 1) & 1) for D = 64.
-template <int D>
-__device__ static inline int pp_swz_k(int row) {
-  return D == 128 ? (row & 15) : ((row >> 1) & 7);
-}
-template <int D>
-__device__ static inline int pp_swz_v(int row) {
-  return D == 128 ? ((row & 3) << 2) : (((row >> 1) & 1) << 2);
-}
-
 // Stage size of the eight-wave kernel at head dim D: 128 key rows of 2 D bytes.
 constexpr int pp_stage_bytes(int d) { return kPPKeys * 2 * d; }
 

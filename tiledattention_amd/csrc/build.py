@@ -7,6 +7,8 @@ Outputs (into ``tiledattention_amd/lib/`` unless told otherwise):
   ``attn_fwd.hip`` with ``hipcc --genco --offload-arch=gfx950``;
 * ``attn_fwd_pp.hsaco``: the eight-wave kernels (dtype x head dim x causal x tail) that
   serve the (128, 64) tile shape with fp32 accumulation, from ``attn_fwd_pp.hip``;
+* ``attn_fwd_wide.hsaco``: the short-row kernels (32 query rows a workgroup, the keys split
+  across its eight waves) that serve 64-row tiles on small grids, from ``attn_fwd_wide.hip``;
 * ``libtiledattn.so``: the host library implementing ``include/tiledattn.h``, linked from
   ``tiledattn.cpp`` (g++) and ``tiledattn_static.hip`` (hipcc; the static device scratch of
   ``ta_sdpa_fwd_split_static``);
@@ -81,6 +83,17 @@ def pp_code_object_cmd(out_dir: Path) -> list[str]:
         "-o",
         str(out_dir / "attn_fwd_pp.hsaco"),
         str(HERE / "attn_fwd_pp.hip"),
+    ]
+
+
+def wide_code_object_cmd(out_dir: Path) -> list[str]:
+    return [
+        _hipcc(),
+        *HIP_FLAGS,
+        "--genco",
+        "-o",
+        str(out_dir / "attn_fwd_wide.hsaco"),
+        str(HERE / "attn_fwd_wide.hip"),
     ]
 
 
@@ -165,7 +178,7 @@ def build(out_dir: Path | None = None, jobs: int | None = None) -> Path:
     out = Path(out_dir) if out_dir is not None else LIB_DIR
     out.mkdir(parents=True, exist_ok=True)
     cmds = [code_object_cmd(tm, tn, out) for tm, tn in TILES]
-    cmds += [pp_code_object_cmd(out)]
+    cmds += [pp_code_object_cmd(out), wide_code_object_cmd(out)]
     workers = jobs or min(len(cmds) + 1, max(1, (os.cpu_count() or 2)))
     with cf.ThreadPoolExecutor(max_workers=workers) as pool:
         futs = [pool.submit(_run, c) for c in cmds] + [pool.submit(_build_library, out)]

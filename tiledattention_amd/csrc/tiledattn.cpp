@@ -60,6 +60,7 @@ std::map<int, unsigned*> g_counters;
 std::map<std::pair<int, void*>, int> g_regions;
 std::map<int, int> g_regions_used;
 const char kPPObject[] = "attn_fwd_pp.hsaco";
+const char kWideObject[] = "attn_fwd_wide.hsaco";
 
 std::string default_dir() {
   Dl_info info;
@@ -424,6 +425,26 @@ int32_t plan_split(int64_t S, int64_t n_bh, bool causal, int ncu) {
   return best_c;
 }
 
+// Whether a whole-row launch of a 64-row tile runs the wide kernel (attn_fwd_wide.hip,
+// ta_fwd_wide_*: 32 query rows a workgroup, its eight waves splitting the keys of every
+// pass of 512 keys at D = 128, 1024 at D = 64; fp32 accumulation): D = 64 or 128, a grid of
+// 32-row blocks that fits one round of one workgroup per CU, and either at most two passes
+// for the longest block or at most four on more than half the CUs.  There the eight-wave kernel's
+// chain of 128-key steps is the latency (back to back, B1 H8 bf16 D = 128 causal, 64-row
+// kernel -> wide: S = 512 8.1 -> 6.6 us, S = 1024 11.0 -> 9.0; fp16 D = 64 non-causal
+// S = 1024 7.9 -> 6.4; B1 H4 S2048 causal against the 64-row split 15.9 -> 13.4).  With
+// fewer blocks and more passes the split spreads the keys over more CUs (B1 H1 S2048 D = 128
+// causal: split 12.6, wide 13.2), and a second round of workgroups loses to the 64-row
+// kernel (B1 H8 S2048: 17.6 against 19.2; B1 H32 S512: 8.6 against 11.2).
+bool use_wide(int64_t S, int64_t n_bh, int64_t D, int ncu) {
+  if ((D != 64 && D != 128) || S <= 0 || n_bh <= 0 || ncu <= 0) return false;
+  const int64_t grid = n_bh * ((S + 31) / 32);
+  if (grid > ncu) return false;
+  const int64_t pass_keys = D == 128 ? 512 : 1024;
+  const int64_t passes = (S + pass_keys - 1) / pass_keys;
+  return passes <= 2 || (passes <= 4 && 2 * grid > ncu);
+}
+
 // Split plan for the 64-row kernel (ta_fwd_pp64_split_*): 0 (whole rows) or the chunk
 // length with the shortest modelled time, for grids whose 64-row blocks fill at most half
 // of the CUs (larger grids keep whole rows, or the 128-row kernel's plan).  Time model in
@@ -441,6 +462,7 @@ int32_t plan_split64(int64_t S, int64_t n_bh, bool causal, int64_t d, int ncu) {
   const int64_t nq64 = (S + 63) / 64;
   const int64_t len = (S + ta::kPPKeys - 1) / ta::kPPKeys;
   if (ncu < 8 || S <= 0 || n_bh <= 0 || 2 * n_bh * nq64 > ncu || len < 2) return 0;
+  if (use_wide(S, n_bh, d, ncu)) return 0;  // whole rows on the wide kernel
   auto step = [&](int64_t wgs) { return t * (1.0 + kLoad * (double)wgs / ncu); };
   const double whole = kF + (double)len * step(n_bh * nq64);
   double best = whole * 0.98;
@@ -713,6 +735,15 @@ ta_status plan_launch(const ta_fwd_args* a, int64_t n_bh, int64_t n_qblk, int32_
       pl->tail = t256;
       pl->layout = TA_LAYOUT_ROWS256;
     }
+  } else if (eight_wave64(a->tile_m, a->tile_n, a->accum, a->D) && use_wide(a->S, n_bh, a->D, ncu)) {
+    // The aligned variant's S (a multiple of 128) is whole 32-row blocks and whole passes of
+    // a wave's keys, as its t0 form needs.
+    char name[64];
+    snprintf(name, sizeof(name), "ta_fwd_wide_%s_d%d_c%d_t%d", dt, (int)a->D, a->causal ? 1 : 0, aligned ? 0 : 1);
+    pl->main = KernelId{kWideObject, name, 512u};
+    pl->grid = n_bh * ((a->S + 31) / 32);
+    pl->rows = 32;
+    pl->layout = TA_LAYOUT_WIDE;
   }
   return check_grid(pl->grid, pl->main.block, "kernel");
 }
@@ -768,6 +799,7 @@ ta_status launch_plan_locked(const ta_fwd_args* a, const LaunchPlan& pl, ta::Fwd
   if (s == TA_OK && pl.merge) s = get_function_locked(a->device, pl.merge_id, &mfn);
   if (s != TA_OK) return s;
   if (pl.layout == TA_LAYOUT_ROWS256) p->n_qblk = static_cast<int32_t>((a->S + 255) / 256);
+  if (pl.layout == TA_LAYOUT_WIDE) p->n_qblk = static_cast<int32_t>((a->S + 31) / 32);
   // the split numbering and the merge count 128-row blocks, whatever rows a workgroup takes
   if (pl.merge) p->n_qblk = static_cast<int32_t>((a->S + kSplitRows - 1) / kSplitRows);
   p->merge_cnt = nullptr;
@@ -996,8 +1028,9 @@ ta_status ta_sdpa_fwd(const ta_fwd_args* a, void* stream) {
   int64_t n_bh = 0, n_qblk = 0;
   ta_status vst = validate_args(a, &n_bh, &n_qblk);
   if (vst != TA_OK || n_qblk == 0) return vst;
-  // The whole-row grid bounds every layout's (pairs and 256-row blocks only shrink it), so
-  // an oversized request is rejected before any device call.
+  // The whole-row grid bounds every layout's (pairs and 256-row blocks only shrink it; the
+  // wide kernel's runs only within one round of the CUs), so an oversized request is
+  // rejected before any device call.
   const KernelId base = kernel_id(a->dtype, (int)a->D, a->tile_m, a->tile_n, a->causal,
                                   !unmasked_tail(a), a->accum);
   ta_status gst = check_grid(n_bh * n_qblk, base.block, "kernel");
