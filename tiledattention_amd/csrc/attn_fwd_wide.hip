@@ -23,9 +23,10 @@
 // * Softmax per pass with the exact running max (P = 2^(s c - m c) <= 1 packs to either
 //   input dtype; O and l are rescaled when a later pass raises m), l summed from the
 //   rounded P that the P.V MFMAs use.
-// * Merge: every wave writes its m, then 2^((m_w - m) c) l_w and its O scaled by the same
-//   weight (fp32, 16-byte chunks XOR-swizzled by row) into the freed stages; each wave then
-//   sums the eight partials of 4 rows and stores them, divided by the summed l.
+// * Merge: every wave writes its O (fp32, 16-byte chunks XOR-swizzled by row), m and l as
+//   soon as its own P.V is done, over its own rows of the stages; after one barrier each
+//   wave sums the eight states of 4 rows with the weights 2^((m_w - m) c) and stores them,
+//   divided by the weighted sum of l.
 //
 // One workgroup per CU (138 KiB of LDS); the host runs it when its grid of 32-row blocks
 // fits one round of the CUs.
@@ -54,8 +55,9 @@ __device__ __forceinline__ void attn_fwd_wide_body(const FwdParams& p) {
   constexpr int RPL = 1024 / RB;         // key rows per 1 KiB chunk: 4 / 8
   constexpr int OWN = KW / RPL;          // 1 KiB chunks of a wave's rows: 16
   constexpr int QCH = 32 * RB / 1024;    // 1 KiB chunks of the Q tile: 8 / 4
-  constexpr int PW = 32 * D * 4;         // bytes of one wave's fp32 partial O: 16 / 8 KiB
-  static_assert(8 * PW <= REGION && QCH <= 8, "merge partials fit the stages; Q chunks <= waves");
+  constexpr int SLOT = OWN * 1024;       // a wave's own rows of the stages: 16 KiB
+  static_assert(32 * D * 4 <= SLOT && 8 * SLOT == REGION && QCH <= 8,
+                "a wave's fp32 O fits its own rows; Q chunks <= waves");
   __shared__ __attribute__((aligned(1024))) char region[REGION];
   __shared__ __attribute__((aligned(1024))) char lds_q[32 * RB];
   __shared__ float ml[2][8][32];  // per wave and row: m, then 2^((m_w - m) c) l_w
@@ -266,52 +268,54 @@ __device__ __forceinline__ void attn_fwd_wide_body(const FwdParams& p) {
   }
 
   // ---- merge of the eight waves' states of each row -----------------------------------
-  // A wave that never had a key keeps m = kNegLarge, l = 0, O = 0: its weight is 0 (every
-  // row has at least one key, so the row max is a real score).
+  // Each wave writes its O (unweighted, fp32), m and l as soon as its last P.V is done: O
+  // into its own rows of the stages (bytes [16 w, 16 w + 16) KiB, which no other wave reads
+  // or loads), m and l beside; one barrier, then wave w sums rows 4 w .. 4 w + 3 of the
+  // eight states with the weights 2^((m_w - m) c), m = max_w m_w.  A wave that never had a
+  // key keeps m = kNegLarge, l = 0, O = 0: its weight is 0 (every row has at least one key,
+  // so the row max is a real score).
   float la, lb;
   swap32(l_part, la, lb);
-  const float l_tot = la + lb;
-  if (hl == 0) ml[0][wave][l32] = m_run;
-  barrier();  // every wave's m, and every wave is done with the stages
-  float mx = ml[0][0][l32];
-#pragma unroll
-  for (int w = 1; w < 8; ++w) mx = vmax(mx, ml[0][w][l32]);
-  const float aw = fast_exp2((m_run - mx) * c);
-  if (hl == 0) ml[1][wave][l32] = aw * l_tot;
+  if (hl == 0) {
+    ml[0][wave][l32] = m_run;
+    ml[1][wave][l32] = la + lb;
+  }
   // O^T lane layout: row l32, d = 32 db + 8 g + 4 hl + e (e < 4): 16-byte chunk
   // ch = 8 db + 2 g + hl of the row, stored at chunk ch ^ (row & 15) (conflict-free)
-  char* part = region + wave * PW;
+  char* part = region + wave * SLOT;
 #pragma unroll
   for (int db = 0; db < DB; ++db) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int ch = 8 * db + 2 * g + hl;
       *(f32x4*)(part + l32 * (D * 4) + 16 * (ch ^ (l32 & 15))) =
-          f32x4{o_acc[db][4 * g] * aw, o_acc[db][4 * g + 1] * aw, o_acc[db][4 * g + 2] * aw,
-                o_acc[db][4 * g + 3] * aw};
+          f32x4{o_acc[db][4 * g], o_acc[db][4 * g + 1], o_acc[db][4 * g + 2], o_acc[db][4 * g + 3]};
     }
   }
   barrier();
-  // wave w sums rows 4 w .. 4 w + 3: lane l takes row 4 w + l / 16 and the D / 16 columns
-  // from (l % 16) D / 16
+  // lane l takes row 4 w + l / 16 and the D / 16 columns from (l % 16) D / 16
   constexpr int VPL = D / 16;   // values per lane: 8 / 4
   constexpr int CPL = VPL / 4;  // 16-byte chunks per lane: 2 / 1
   const int row = 4 * wave + (lane >> 4);
   const int ch0 = (lane & 15) * CPL;
+  float mx = ml[0][0][row];
+#pragma unroll
+  for (int w = 1; w < 8; ++w) mx = vmax(mx, ml[0][w][row]);
   float acc[VPL];
 #pragma unroll
   for (int e = 0; e < VPL; ++e) acc[e] = 0.0f;
   float lsum = 0.0f;
 #pragma unroll
   for (int w = 0; w < 8; ++w) {
-    const char* pw = region + w * PW + row * (D * 4);
+    const float aw = fast_exp2((ml[0][w][row] - mx) * c);
+    lsum += aw * ml[1][w][row];
+    const char* pw = region + w * SLOT + row * (D * 4);
 #pragma unroll
     for (int cc = 0; cc < CPL; ++cc) {
       const f32x4 v = *(const f32x4*)(pw + 16 * ((ch0 + cc) ^ (row & 15)));
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc[4 * cc + e] += v[e];
+      for (int e = 0; e < 4; ++e) acc[4 * cc + e] += aw * v[e];
     }
-    lsum += ml[1][w][row];
   }
   const float inv = 1.0f / lsum;
   const int q = q0 + row;
