@@ -106,6 +106,7 @@ def test_rocprof_summary_from_profiler_csvs(tmp_path):
     text = (tmp_path / "r.md").read_text()
     assert "# rocprofv3 One-Pass Summary" in text and "`ta_fwd_pp_bf16_d128_c1_t0`" in text
     assert "| tiledattention | `ta_fwd_pp_bf16_d128_c1_t0` | 0.128 | 53.6" in text
+    assert "| tiledattention | GRBM_GUI_ACTIVE | 2016856.000 |" in text  # every counter's mean
     assert study.main(["--out", str(tmp_path / "o"), "--rocprof-dir", str(d)]) == 0
     assert (tmp_path / "o" / "rocprof_summary.md").exists()
 

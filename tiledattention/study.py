@@ -528,6 +528,11 @@ def write_rocprof_summary(path: Path, results: list[tuple[str, dict]], config: d
             f"{f(_ratio(m, 'SQ_VALU_MFMA_COEXEC_CYCLES', 'SQ_VALU_MFMA_BUSY_CYCLES'))} | "
             f"{f(_ratio(m, 'SQ_WAIT_ANY', 'SQ_WAVE_CYCLES'))} | {f(_ratio(m, 'SQ_WAIT_INST_LDS', 'SQ_WAVE_CYCLES'))} | "
             f"{f(m.get('SQ_LDS_BANK_CONFLICT'))} | {f(m.get('FETCH_SIZE'))} | {f(m.get('WRITE_SIZE'))} |")
+    lines += ["", "## Counters (mean per dispatch, summed over counter dimensions)", "",
+              "| Method | Counter | Mean |", "| --- | --- | --- |"]
+    for method, m in results:
+        for name in sorted(k for k in m if k not in ("kernel", "kernel_ms")):
+            lines.append(f"| {method} | {name} | {f(m[name])} |")
     lines += ["", "## Quick Diagnosis", ""]
     for method, m in results:
         lines += [f"### {method}", "", f"- Primary kernel: `{m.get('kernel')}`",
