@@ -21,6 +21,7 @@
 #include <map>
 #include <mutex>
 #include <queue>
+#include <unordered_map>
 #include <string>
 #include <tuple>
 #include <vector>
@@ -265,6 +266,8 @@ ta_status check_grid(int64_t blocks, unsigned block, const char* what) {
   return TA_OK;
 }
 
+void clear_resolved_plans();  // below: the resolved launch plans hold functions of the modules
+
 // Caller holds g_mu.  Unloads every module; the launch paths resolve and launch under the
 // same lock, so no launch can use a function of a module unloaded here.
 ta_status cache_reset_locked() {
@@ -277,6 +280,7 @@ ta_status cache_reset_locked() {
   }
   g_modules.clear();
   g_funcs.clear();
+  clear_resolved_plans();
   g_counters.clear();
   g_regions.clear();
   g_regions_used.clear();
@@ -790,14 +794,70 @@ ta_status describe_model(const ta_fwd_args* a, int32_t chunk_steps, int ncu, ta_
   return TA_OK;
 }
 
-// Resolves the plan's kernels and enqueues them.  Caller holds g_mu and has made the device
-// current; p carries the tensors (and, for a split, the workspace).
-ta_status launch_plan_locked(const ta_fwd_args* a, const LaunchPlan& pl, ta::FwdParams* p,
-                             void* stream) {
-  hipFunction_t fn = nullptr, mfn = nullptr;
-  ta_status s = get_function_locked(a->device, pl.main, &fn);
-  if (s == TA_OK && pl.merge) s = get_function_locked(a->device, pl.merge_id, &mfn);
-  if (s != TA_OK) return s;
+// A plan with its kernels resolved on the device.
+struct ResolvedPlan {
+  LaunchPlan pl;
+  hipFunction_t fn = nullptr;   // the attention kernel
+  hipFunction_t mfn = nullptr;  // the merge kernel (split layouts)
+};
+
+// Resolved plans of recent launches, keyed by every argument the plan depends on (the
+// tensors and strides are not among them) and the device's CU count: a call of a known
+// configuration skips the planning (kernel names, rules) and the function lookup.  Cleared
+// with the module cache (cache_reset_locked), so a plan never outlives its functions.
+struct PlanKey {
+  int64_t B, H, S, D;
+  int32_t causal, dtype, tile_m, tile_n, accum, device, sched, d_real, aligned, ncu, chunk, pad;
+  bool operator==(const PlanKey& o) const {
+    return B == o.B && H == o.H && S == o.S && D == o.D && causal == o.causal && dtype == o.dtype &&
+           tile_m == o.tile_m && tile_n == o.tile_n && accum == o.accum && device == o.device &&
+           sched == o.sched && d_real == o.d_real && aligned == o.aligned && ncu == o.ncu && chunk == o.chunk;
+  }
+};
+struct PlanKeyHash {
+  size_t operator()(const PlanKey& k) const {
+    uint64_t h = 1469598103934665603ull;
+    auto mix = [&](uint64_t v) { h = (h ^ v) * 1099511628211ull; };
+    mix((uint64_t)k.B); mix((uint64_t)k.H); mix((uint64_t)k.S); mix((uint64_t)k.D);
+    mix(((uint64_t)(uint32_t)k.causal << 32) | (uint32_t)k.dtype);
+    mix(((uint64_t)(uint32_t)k.tile_m << 32) | (uint32_t)k.tile_n);
+    mix(((uint64_t)(uint32_t)k.accum << 32) | (uint32_t)k.device);
+    mix(((uint64_t)(uint32_t)k.sched << 32) | (uint32_t)k.d_real);
+    mix(((uint64_t)(uint32_t)k.aligned << 32) | (uint32_t)k.ncu);
+    mix((uint64_t)(uint32_t)k.chunk);
+    return (size_t)h;
+  }
+};
+std::unordered_map<PlanKey, ResolvedPlan, PlanKeyHash> g_resolved;
+constexpr size_t kResolvedMax = 4096;
+void clear_resolved_plans() { g_resolved.clear(); }
+
+// Caller holds g_mu and has made the device current.  The resolved plan of a launch (from
+// the cache, or planned and resolved now); the pointer stays valid until the cache lock is
+// released.
+ta_status resolved_plan_locked(const ta_fwd_args* a, int64_t n_bh, int64_t n_qblk, int32_t chunk_steps,
+                               int ncu, const ResolvedPlan** out) {
+  const PlanKey key{a->B,      a->H,     a->S,      a->D,     a->causal, a->dtype,  a->tile_m, a->tile_n,
+                    a->accum,  a->device, a->sched, a->d_real, a->aligned, ncu,      chunk_steps, 0};
+  auto it = g_resolved.find(key);
+  if (it != g_resolved.end()) {
+    *out = &it->second;
+    return TA_OK;
+  }
+  ResolvedPlan r;
+  ta_status st = plan_launch(a, n_bh, n_qblk, chunk_steps, ncu, &r.pl);
+  if (st == TA_OK) st = get_function_locked(a->device, r.pl.main, &r.fn);
+  if (st == TA_OK && r.pl.merge) st = get_function_locked(a->device, r.pl.merge_id, &r.mfn);
+  if (st != TA_OK) return st;
+  if (g_resolved.size() >= kResolvedMax) g_resolved.clear();
+  *out = &g_resolved.emplace(key, std::move(r)).first->second;
+  return TA_OK;
+}
+
+// Enqueues a resolved plan.  Caller holds g_mu and has made the device current; p carries
+// the tensors (and, for a split, the workspace).
+ta_status launch_plan_locked(const ta_fwd_args* a, const ResolvedPlan& r, ta::FwdParams* p, void* stream) {
+  const LaunchPlan& pl = r.pl;
   if (pl.layout == TA_LAYOUT_ROWS256) p->n_qblk = static_cast<int32_t>((a->S + 255) / 256);
   if (pl.layout == TA_LAYOUT_WIDE) p->n_qblk = static_cast<int32_t>((a->S + 31) / 32);
   // the split numbering and the merge count 128-row blocks, whatever rows a workgroup takes
@@ -806,11 +866,11 @@ ta_status launch_plan_locked(const ta_fwd_args* a, const LaunchPlan& pl, ta::Fwd
   if (pl.merge && pl.merge_in_kernel) p->merge_cnt = merge_counters_locked(a->device, stream);
   void* params[] = {p};
   hipStream_t hs = static_cast<hipStream_t>(stream);
-  hipError_t e = hipModuleLaunchKernel(fn, static_cast<unsigned>(pl.grid), 1, 1, pl.main.block, 1, 1,
+  hipError_t e = hipModuleLaunchKernel(r.fn, static_cast<unsigned>(pl.grid), 1, 1, pl.main.block, 1, 1,
                                        0, hs, params, nullptr);
   if (e != hipSuccess) return fail(TA_EHIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
   if (pl.merge && p->merge_cnt == nullptr) {
-    e = hipModuleLaunchKernel(mfn, static_cast<unsigned>(pl.merge_grid), 1, 1, pl.merge_id.block, 1,
+    e = hipModuleLaunchKernel(r.mfn, static_cast<unsigned>(pl.merge_grid), 1, 1, pl.merge_id.block, 1,
                               1, 0, hs, params, nullptr);
     if (e != hipSuccess) return fail(TA_EHIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
   }
@@ -1031,9 +1091,10 @@ ta_status ta_sdpa_fwd(const ta_fwd_args* a, void* stream) {
   // The whole-row grid bounds every layout's (pairs and 256-row blocks only shrink it; the
   // wide kernel's runs only within one round of the CUs), so an oversized request is
   // rejected before any device call.
-  const KernelId base = kernel_id(a->dtype, (int)a->D, a->tile_m, a->tile_n, a->causal,
-                                  !unmasked_tail(a), a->accum);
-  ta_status gst = check_grid(n_bh * n_qblk, base.block, "kernel");
+  const unsigned base_block = eight_wave_family(a->tile_m, a->tile_n, a->accum, a->D)
+                                  ? 512u
+                                  : static_cast<unsigned>(a->tile_m * 2);  // kernel_id's block
+  ta_status gst = check_grid(n_bh * n_qblk, base_block, "kernel");
   if (gst != TA_OK) return gst;
   ta::FwdParams p;
   fill_params(a, n_bh, n_qblk, &p);
@@ -1047,10 +1108,10 @@ ta_status ta_sdpa_fwd(const ta_fwd_args* a, void* stream) {
   int ncu = 0;
   ta_status cst = cu_count_locked(a->device, &ncu);
   if (cst != TA_OK) return cst;
-  LaunchPlan pl;
-  ta_status st = plan_launch(a, n_bh, n_qblk, 0, ncu, &pl);
+  const ResolvedPlan* rp = nullptr;
+  ta_status st = resolved_plan_locked(a, n_bh, n_qblk, 0, ncu, &rp);
   if (st != TA_OK) return st;
-  return launch_plan_locked(a, pl, &p, stream);
+  return launch_plan_locked(a, *rp, &p, stream);
 }
 
 ta_status ta_plan_call(int64_t B, int64_t H, int64_t S, int64_t D, int32_t dtype, int32_t causal,
@@ -1180,9 +1241,10 @@ ta_status ta_sdpa_fwd_split(const ta_fwd_args* a, int32_t chunk_steps, void* wor
     return fail(TA_EHIP, "set device %d: %s", a->device, hipGetErrorString(guard.err));
   int ncu = 0;
   st = cu_count_locked(a->device, &ncu);
-  if (st == TA_OK) st = plan_launch(a, n_bh, n_qblk, chunk_steps, ncu, &pl);
+  const ResolvedPlan* rp = nullptr;
+  if (st == TA_OK) st = resolved_plan_locked(a, n_bh, n_qblk, chunk_steps, ncu, &rp);
   if (st != TA_OK) return st;
-  return launch_plan_locked(a, pl, &p, stream);
+  return launch_plan_locked(a, *rp, &p, stream);
 }
 
 }  // extern "C"
