@@ -12,6 +12,8 @@ GPU, and compares the whole output at the north-star bound.
 
 from __future__ import annotations
 
+import random
+
 import pytest
 
 from tests.parity_util import as_f32, check_close, inputs, kernel_for, oracle_f32, run_gpu, say
@@ -77,3 +79,58 @@ def test_wide_strided_views_custom_scale_and_repeat(gpu):
     torch.cuda.synchronize()
     assert torch.equal(out1, out2)
     check_close(as_f32(out1), oracle_f32(q, k, v, causal=True, scale=0.3), "bfloat16", what="wide strided")
+
+
+def _wide_draw(rng) -> dict:
+    """A configuration inside the wide kernel's rule at 256 CUs: S <= 1024, B * H * ceil(S/32)
+    <= 256; head dims that reach kernel D = 64 or 128 (in place, or padded on the host for
+    33 and 100), never (64, 96] (the native D = 96 kernel)."""
+    s = rng.choice([1, 31, 33, 64, 200, 255, 256, 257, 500, 511, 640, 777, 1000, 1024])
+    blocks = -(-s // 32)
+    bh_max = max(1, 256 // blocks)
+    bh = rng.randint(1, min(bh_max, 12))
+    b = rng.choice([d for d in (1, 2, 3) if bh % d == 0])
+    return dict(b=b, h=bh // b, s=s, d=rng.choice([8, 24, 33, 40, 56, 64, 100, 104, 120, 128]),
+                dtype=rng.choice(["float16", "bfloat16"]), causal=rng.random() < 0.5,
+                scale=rng.choice([None, None, 0.05, 0.3]), mag=rng.choice([0.5, 1.0, 2.0]),
+                bshd=rng.random() < 0.3, seed=rng.randrange(1 << 30))
+
+
+_WIDE_CASES = [_wide_draw(r) for r in [random.Random(20261202)] for _ in range(24)]
+
+
+@pytest.mark.parametrize("case", _WIDE_CASES, ids=[f"w{i}" for i in range(len(_WIDE_CASES))])
+def test_wide_randomized(gpu, case):
+    """Seeded random configurations inside the wide rule against the explicit fp32 oracle, at
+    the north-star tolerance scaled by the input magnitude; draws with a sharp softmax
+    (logit spread above 6) at the P-rounding bound 3 u max|v| instead (the reasoning of
+    tests/test_gpu_randomized.py)."""
+    import math
+
+    import numpy as np
+    import torch
+
+    from tiledattention import sdpa
+    from tests.parity_util import TOL
+
+    c = case
+    q, k, v = inputs((c["b"], c["h"], c["s"], c["d"]), c["dtype"], c["seed"], scale_inputs=c["mag"])
+    dev = torch.device("cuda:0")
+    if c["bshd"]:
+        qd, kd, vd = (t.transpose(1, 2).contiguous().to(dev).transpose(1, 2) for t in (q, k, v))
+    else:
+        qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    kernel = kernel_for(qd, kd, vd, causal=c["causal"])
+    assert kernel.startswith("ta_fwd_wide_"), (kernel, c)
+    say(f"wide random {kernel} {c}")
+    out = sdpa(qd, kd, vd, causal=c["causal"], scale=c["scale"])
+    torch.cuda.synchronize()
+    assert out.shape == q.shape and out.dtype == q.dtype
+    scale = c["scale"] if c["scale"] is not None else 1.0 / math.sqrt(c["d"])
+    spread = scale * c["mag"] ** 2 * math.sqrt(c["d"])
+    tol = TOL[c["dtype"]] * max(1.0, c["mag"])
+    if spread > 6.0:
+        u = 2.0 ** -8 if c["dtype"] == "bfloat16" else 2.0 ** -11
+        tol = max(tol, 3 * u * float(np.abs(v.float().numpy()).max()))
+    ref = oracle_f32(q, k, v, causal=c["causal"], scale=c["scale"])
+    check_close(as_f32(out), ref, c["dtype"], tol=tol, what=f"wide random (logit spread {spread:.1f})")
