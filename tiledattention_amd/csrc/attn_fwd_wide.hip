@@ -147,6 +147,21 @@ __device__ __forceinline__ void attn_fwd_wide_body(const FwdParams& p) {
   const int v_rd = (koff + 4 * hl + tr_r) * RB + 16 * ((tr_d >> 3) ^ pp_swz_v<D>(4 * hl + tr_r)) + 2 * (tr_d & 7);
   const char* st = region + sw * STAGE;
 
+  // Issue order of a run of N MFMAs whose operands come from LDS (RPM reads each): the
+  // reads of the first AHEAD MFMAs, then each MFMA followed by the reads of the MFMA AHEAD
+  // places later, so that no MFMA waits on a read issued just before it.
+  auto run_order = [&](auto n_tag, auto rpm_tag) {
+    constexpr int N = decltype(n_tag)::value;
+    constexpr int RPM = decltype(rpm_tag)::value;
+    constexpr int AHEAD = 4;
+    __builtin_amdgcn_sched_group_barrier(0x100, AHEAD * RPM, 0);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (i + AHEAD < N) __builtin_amdgcn_sched_group_barrier(0x100, RPM, 0);
+    }
+  };
+
   // ---- state (lane = query l32 of the block, half hl of each 32-key block's keys) -------
   u32x4 qf[DK];  // B operand of S^T = K Q^T
   float m_run = kNegLarge;
@@ -192,6 +207,7 @@ __device__ __forceinline__ void attn_fwd_wide_body(const FwdParams& p) {
           s[bk] = DTy::mfma(a, qf[kk], kk == 0 ? f32x16{} : s[bk]);
         }
       }
+      run_order(std::integral_constant<int, DK * KB>{}, std::integral_constant<int, 1>{});
       wait_lds();  // its K reads are done: its V over the same rows
       load_own(vp, p.v_ss, v_rb, false, kbase);
 
@@ -263,6 +279,7 @@ __device__ __forceinline__ void attn_fwd_wide_body(const FwdParams& p) {
           }
         }
       }
+      run_order(std::integral_constant<int, KB * 2 * DB>{}, std::integral_constant<int, 2>{});
       wait_lds();  // its V reads are done before the next pass's K over the same rows
     }
   }
