@@ -1432,11 +1432,14 @@ __device__ unsigned ta_merge_counters[ta::kMergeRegions * ta::kMergeRegionCounte
 // Input-dtype accumulation (D = 64 and 128, whole rows), one kernel per TILE_N (the keys of
 // a wave's slice between roundings of O): ta_fwd_ppl_n<TN>_<f16|bf16>_d<D>_c_t (128-row
 // blocks, tiles (128, TN)) and ta_fwd_ppl64_n<TN>_<...> (64-row blocks, tiles (64, TN)).
-// One workgroup per CU (two waves per SIMD): at 128 VGPRs the exact max and the rounding of
-// O beside P spilled registers to scratch.
+// The residency of the fp32 kernels (TA_PP_WAVES): two workgroups per CU for non-causal
+// D = 64, one otherwise.  At 128 VGPRs the 64-row D = 64 kernels fit (113) and the 128-row
+// ones spill 5-13 registers, and both still run 6-12 % faster with the second workgroup's
+// waves to issue from (C4 D = 64 tiles (64, 64) 613 -> 690, (128, 128) 785 -> 842 TFLOP/s
+// bf16, outputs bit-identical); the causal D = 64 kernels take 169 VGPRs.
 #define TA_PPL_DEFINE(NAME, TN, DTN, DT, D, C, T, TMR)                                      \
   extern "C" __global__ void __launch_bounds__(512)                                       \
-      __attribute__((amdgpu_waves_per_eu(2, 2)))                                          \
+      __attribute__((amdgpu_waves_per_eu(TA_PP_WAVES(D, C), TA_PP_WAVES(D, C))))           \
       ta_fwd_##NAME##_n##TN##_##DTN##_d##D##_c##C##_t##T(ta::FwdParams p) {                \
     ta::attn_fwd_pp_body<DT, D, (C != 0), (T != 0), false, false, TMR, TN>(p);            \
   }
