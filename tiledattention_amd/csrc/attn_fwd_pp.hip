@@ -1432,14 +1432,16 @@ __device__ unsigned ta_merge_counters[ta::kMergeRegions * ta::kMergeRegionCounte
 // Input-dtype accumulation (D = 64 and 128, whole rows), one kernel per TILE_N (the keys of
 // a wave's slice between roundings of O): ta_fwd_ppl_n<TN>_<f16|bf16>_d<D>_c_t (128-row
 // blocks, tiles (128, TN)) and ta_fwd_ppl64_n<TN>_<...> (64-row blocks, tiles (64, TN)).
-// The residency of the fp32 kernels (TA_PP_WAVES): two workgroups per CU for non-causal
-// D = 64, one otherwise.  At 128 VGPRs the 64-row D = 64 kernels fit (113) and the 128-row
-// ones spill 5-13 registers, and both still run 6-12 % faster with the second workgroup's
-// waves to issue from (C4 D = 64 tiles (64, 64) 613 -> 690, (128, 128) 785 -> 842 TFLOP/s
-// bf16, outputs bit-identical); the causal D = 64 kernels take 169 VGPRs.
+// Two workgroups per CU at D = 64 (one at D = 128, where the LDS takes the CU) for the
+// 64-row kernels and the non-causal 128-row ones.  At 128 VGPRs the 64-row kernels fit
+// (113-123) and the 128-row ones spill 5-13 registers; the second workgroup's waves to issue
+// from make them faster all the same (outputs bit-identical): C4 D = 64 bf16 tiles (64, 64)
+// 613 -> 690, (128, 128) 785 -> 842 TFLOP/s; causal B1 H8 S8192 bf16 (64, 64) 127.9 -> 108.8
+// us.  The causal 128-row kernels stay at one (B1 H8 S8192 (128, 64) 111 -> 146 us with two).
+#define TA_PPL_WAVES(D, C, TMR) ((D) == 64 && ((C) == 0 || (TMR) == 64) ? 4 : 2)
 #define TA_PPL_DEFINE(NAME, TN, DTN, DT, D, C, T, TMR)                                      \
   extern "C" __global__ void __launch_bounds__(512)                                       \
-      __attribute__((amdgpu_waves_per_eu(TA_PP_WAVES(D, C), TA_PP_WAVES(D, C))))           \
+      __attribute__((amdgpu_waves_per_eu(TA_PPL_WAVES(D, C, TMR), TA_PPL_WAVES(D, C, TMR)))) \
       ta_fwd_##NAME##_n##TN##_##DTN##_d##D##_c##C##_t##T(ta::FwdParams p) {                \
     ta::attn_fwd_pp_body<DT, D, (C != 0), (T != 0), false, false, TMR, TN>(p);            \
   }
