@@ -1404,10 +1404,12 @@ __device__ unsigned ta_merge_counters[ta::kMergeRegions * ta::kMergeRegionCounte
   }
 
 // 64-row blocks (tiles (64, 64) and (64, 128) with fp32 accumulation, D = 64, 96, 128 and 160):
-// ta_fwd_pp64_<f16|bf16>_d<D>_c<0|1>_t<0|1>, the same residency as the 128-row kernels.
+// ta_fwd_pp64_<f16|bf16>_d<D>_c<0|1>_t<0|1>.  Two workgroups per CU at D = 64, causal or not
+// (104 VGPRs; causal B1 H8 S8192 bf16 87.2 -> 81.1 us, B4 H16 S4096 194.3 -> 171.0 us, small
+// grids within 1 %, outputs bit-identical); one at D = 96-160, whose stages fill the LDS.
 #define TA_PP64_DEFINE(DTN, DT, D, C, T)                                                   \
   extern "C" __global__ void __launch_bounds__(512)                                       \
-      __attribute__((amdgpu_waves_per_eu(TA_PP_WAVES(D, C), TA_PP_WAVES(D, C))))           \
+      __attribute__((amdgpu_waves_per_eu((D) == 64 ? 4 : 2, (D) == 64 ? 4 : 2)))           \
       ta_fwd_pp64_##DTN##_d##D##_c##C##_t##T(ta::FwdParams p) {                            \
     ta::attn_fwd_pp_body<DT, D, (C != 0), (T != 0), false, false, 64>(p);                 \
   }
@@ -1432,13 +1434,12 @@ __device__ unsigned ta_merge_counters[ta::kMergeRegions * ta::kMergeRegionCounte
 // Input-dtype accumulation (D = 64 and 128, whole rows), one kernel per TILE_N (the keys of
 // a wave's slice between roundings of O): ta_fwd_ppl_n<TN>_<f16|bf16>_d<D>_c_t (128-row
 // blocks, tiles (128, TN)) and ta_fwd_ppl64_n<TN>_<...> (64-row blocks, tiles (64, TN)).
-// Two workgroups per CU at D = 64 (one at D = 128, where the LDS takes the CU) for the
-// 64-row kernels and the non-causal 128-row ones.  At 128 VGPRs the 64-row kernels fit
-// (113-123) and the 128-row ones spill 5-13 registers; the second workgroup's waves to issue
-// from make them faster all the same (outputs bit-identical): C4 D = 64 bf16 tiles (64, 64)
-// 613 -> 690, (128, 128) 785 -> 842 TFLOP/s; causal B1 H8 S8192 bf16 (64, 64) 127.9 -> 108.8
-// us.  The causal 128-row kernels stay at one (B1 H8 S8192 (128, 64) 111 -> 146 us with two).
-#define TA_PPL_WAVES(D, C, TMR) ((D) == 64 && ((C) == 0 || (TMR) == 64) ? 4 : 2)
+// Two workgroups per CU for the 64-row kernels at D = 64 (113-123 VGPRs at that bound; one
+// at D = 128, where the LDS takes the CU): the second workgroup's waves to issue from make
+// them faster, outputs bit-identical (C4 D = 64 bf16 tile (64, 64) 613 -> 690 TFLOP/s, causal
+// B1 H8 S8192 bf16 127.9 -> 108.8 us).  The 128-row kernels stay at one: at 128 VGPRs they
+// spill 6-15 registers to scratch.
+#define TA_PPL_WAVES(D, C, TMR) ((D) == 64 && (TMR) == 64 ? 4 : 2)
 #define TA_PPL_DEFINE(NAME, TN, DTN, DT, D, C, T, TMR)                                      \
   extern "C" __global__ void __launch_bounds__(512)                                       \
       __attribute__((amdgpu_waves_per_eu(TA_PPL_WAVES(D, C, TMR), TA_PPL_WAVES(D, C, TMR)))) \
